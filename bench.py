@@ -1,0 +1,213 @@
+"""Benchmark: one page-sparse attention call (route + fused attention) on one
+MI355X, at the full-window base workload: 12 heads x 4608 queries x d128 bf16
+against a 432-page (27648-token) window, 64 exact pages per query block
+(24 anchors + own + 39 by risk), every other page compensated from summaries.
+
+Prints ONE JSON line.  `value` is milliseconds per call (lower is better) with
+all inputs resident in HBM.  The roofline object covers the dominant kernel
+(the fused exact+compensation+merge kernel), timed with HIP events on the
+stream it is launched on.  cpu_baseline times the CPU oracle (a torch
+restatement of the reference's CPU path) on a bounded sample of the same call.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--frames", type=int, default=18, help="window frames (18 -> 432 pages)")
+    ap.add_argument("--precise-av", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--cpu-sample-blocks", type=int, default=4)
+    return ap.parse_args()
+
+
+def time_loop(fn, iters, stream):
+    import torch
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(iters):
+        fn()
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; heads shard across GPUs without "
+                                   "exchange, so run --gpus 1"}))
+        sys.exit(2)
+    import torch
+    from streaming_sparse_amd import _lib, workload
+    from streaming_sparse_amd.attention import Workspace
+    from streaming_sparse_amd.legacy_components import attention, rep_values, kv_strides
+    from streaming_sparse_amd.route import route
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    x = workload.make_call(cfg=1, frames=args.frames)
+    gen_s = time.time() - t0
+    g = x.to(dev)
+    P = x.pages
+    H, N, D = 12, 4608, 128
+    C = P * 15 // 100
+    ws = Workspace()
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, want_mask=False)
+        return attention(g.q, g.k, g.v, g.summary, g.basis, ids, ws, precise_av=args.precise_av)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` calls, synchronized on both sides
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        out = step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_call = start.elapsed_time(end) / args.steps
+
+    # per-kernel timings (same stream, same inputs)
+    ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, want_mask=False)
+    vrep = ws.tensor('ssa_rep_values', (H, P, 4, D), dev, torch.bfloat16)
+    rep_values(g.summary, g.basis, P, vrep)
+    tok, head = kv_strides(g.k, g.v)
+    L = _lib.lib()
+    flags = 1 if args.precise_av else 0
+
+    def attn_only():
+        _lib.check(L.ssa_attention(_lib.ptr(g.q), _lib.ptr(g.k), _lib.ptr(g.v), _lib.ptr(g.summary.keys),
+                                   _lib.ptr(vrep), _lib.ptr(ids), _lib.ptr(out), N, H, P,
+                                   g.summary.head_pages, P, C, tok, head, flags, _lib.stream_handle(dev)),
+                   "ssa_attention")
+
+    def route_only():
+        route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, want_mask=False)
+
+    def rep_only():
+        rep_values(g.summary, g.basis, P, vrep)
+
+    iters = max(10, args.steps)
+    attn_ms = time_loop(attn_only, iters, stream)
+    route_ms = time_loop(route_only, iters, stream)
+    rep_ms = time_loop(rep_only, iters, stream)
+
+    dense_ms = None
+    if not args.no_dense:
+        qd = g.q[0].transpose(0, 1)[None]
+        kd = g.k[0].transpose(0, 1)[None]
+        vd = g.v[0].transpose(0, 1)[None]
+        dense = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)
+        for _ in range(3):
+            dense()
+        dense_ms = time_loop(dense, max(5, iters // 5), stream)
+
+    # algorithmic work of the fused kernel (exact + compensation), per call
+    exact_flop = 4.0 * N * H * D * 64 * C
+    comp_flop = 2.0 * N * H * D * 4 * P + 2.0 * N * H * P * D + 6.0 * N * H * P * 8 + 2.0 * N * H * 8 * D
+    gather_bytes = H * (N // 64) * C * 64 * D * 2 * 2
+    achieved_tflops = (exact_flop + comp_flop) / (attn_ms * 1e-3) / 1e12
+    gather_gbs = gather_bytes / (attn_ms * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(x, C, args.cpu_sample_blocks)
+
+    line = {
+        "metric": METRIC,
+        "value": round(ms_call, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_call, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V with RoPE, k-means page summaries)",
+        "config": {"workload": f"full-window base tier: P={P} pages ({64 * P} KV tokens), {C} exact pages "
+                               f"per 64-query block, 12 heads x 4608 queries x d128, route + attention",
+                   "pages": P, "exact_pages": C, "heads": H, "queries": N, "head_dim": D,
+                   "precise_av": bool(args.precise_av)},
+        "breakdown_ms": {"route": round(route_ms, 4), "rep_values": round(rep_ms, 4),
+                         "attention_kernel": round(attn_ms, 4)},
+        "dense_sdpa_ms": None if dense_ms is None else round(dense_ms, 4),
+        "ratio_vs_dense": None if dense_ms is None else round(ms_call / dense_ms, 4),
+        "roofline": {"bound": "mfma", "achieved": round(achieved_tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "attn_kernel (exact + compensation + merge)",
+                     "algorithmic_gflop": round((exact_flop + comp_flop) / 1e9, 2),
+                     "page_gather_gb": round(gather_bytes / 1e9, 3),
+                     "page_gather_GBps": round(gather_gbs, 1),
+                     "page_gather_frac_of_hbm_peak": round(gather_gbs / PEAK_HBM_GBS, 4)},
+        "cpu_baseline": cpu,
+        "input_gen_s": round(gen_s, 2),
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(x, count, blocks):
+    """CPU oracle on a bounded sample: the router over the whole call (all
+    72 blocks x 12 heads, it is cheap) and the attention over `blocks` query
+    blocks, scaled to a full call (72 blocks)."""
+    import torch
+    from oracle import reference as ref
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    tiles = list(range(0, 72, max(1, 72 // blocks)))[:blocks]
+
+    def run():
+        t0 = time.perf_counter()
+        pr = ref.probes(x.q)
+        r = ref.risk(pr, ref.route_logits(pr, x.summary.keys), x.summary.stats, x.theta)
+        ids = ref.select_base(r, x.own, count)
+        t1 = time.perf_counter()
+        ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, ids, tiles=tiles)
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    run()
+    times = sorted((run() for _ in range(3)), key=lambda a: a[0] + a[1])
+    route_s, attn_s = times[1]
+    total_ms = (route_s + attn_s * 72 / len(tiles)) * 1e3
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(total_ms, 1), "unit": "ms", "cores": cores, "kind": "port",
+            "sample": f"oracle route over the full call + attention over {len(tiles)} of 72 query blocks "
+                      f"(x12 heads), scaled to 72 blocks; median of 3 after 1 warm-up; cpu: {model}"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,255 @@
+"""CPU restatement of the reference's page-sparse attention path.
+
+TEST INFRASTRUCTURE ONLY.  This module is the parity oracle: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it, and only to check or time against the HIP path.  The product path
+(``streaming_sparse_amd``) never imports it and has no CPU fallback.
+
+Every function restates one routine of jurky123/streaming_sparse in plain torch
+on the CPU (float32 by default, float64 on request), citing the reference
+file:line it follows.  Path aliases: VR = local_experiments/video_runtime_v1,
+RV = local_experiments/review_v1, VB = reproduction/vbench_current.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+HAAR = ((1, 1, -1, -1), (1, -1, 1, -1), (1, -1, -1, 1))            # RV/ops.py:10
+PROBE_OFFSETS = (0, 4, 8, 13, 17, 21, 25, 29, 34, 38, 42, 46, 50, 55, 59, 63)
+ANCHORS = 24
+CURRENT = 72
+
+
+def haar(dtype=torch.float32):
+    return torch.tensor(HAAR, dtype=dtype)
+
+
+def deployed(x):
+    """bf16 rounding of a stored operand (RV/ops.py:41)."""
+    return x.to(torch.bfloat16).float()
+
+
+# ---------------------------------------------------------------- router ----
+
+def probes(q, offsets=PROBE_OFFSETS):
+    """q [1,N,H,D] -> probe rows [H,T,16,D] of each 64-query block
+    (VR/runtime.py:84 offsets; VR/route_probes.py:6-21 gather)."""
+    _, n, h, d = q.shape
+    x = q[0].transpose(0, 1).reshape(h, n // 64, 64, d)
+    return x[:, :, list(offsets)].contiguous()
+
+
+def route_logits(pr, keys, dtype=torch.float32):
+    """z = bf16(probe) . bf16(repK)^T * D^-1/2 with fp32 accumulation
+    (VR/tensor_bmm.py:56-66, kernel :7-30) -> [H,T,16,P,4]."""
+    h, t, m, d = pr.shape
+    p = keys.shape[1]
+    a = deployed(pr).to(dtype).reshape(h, t * m, d)
+    b = deployed(keys).to(dtype).reshape(h, p * 4, d)
+    z = torch.bmm(a, b.transpose(1, 2)) * (d ** -0.5)
+    return z.reshape(h, t, m, p, 4)
+
+
+def risk(pr, z, stats, theta, dtype=torch.float32):
+    """Per-page risk [H,T,P]: the four features of RV/ops.py:80-111 in the
+    deployed form VR/risk_online.py:140-149 (row normaliser :151-159, fused
+    reduction :86-122): prob = exp(z-max)/sum exp(z-max) over the P*4 reps of
+    each probe row, u = max(0, sum_g q2_g*st_g), beta = |q|/sqrt(D)*st_8,
+    c = st[p,1,11] + max_p st[p,1,11], value = ((t0 x0 + t1 x1) + t2 x2) + t3 x3,
+    mean over the 16 probes."""
+    h, t, m, d = pr.shape
+    q = deployed(pr).to(dtype)
+    st = stats.to(dtype)
+    z = z.to(dtype)
+    flat = z.flatten(-2)
+    mx = flat.amax(-1, keepdim=True)
+    den = (flat - mx).exp().sum(-1, keepdim=True)
+    prob = ((flat - mx).exp() / den).reshape_as(z)                     # [H,T,M,P,4]
+    alpha = prob.sum(-1)
+    q2 = q.square().reshape(h, t, m, 8, 16).sum(-1) / d
+    qn = q.norm(dim=-1) / math.sqrt(d)
+    u = torch.einsum('htmg,hprg->htmpr', q2, st[..., :8]).clamp_min(0)
+    beta = qn[..., None, None] * st[:, None, None, :, :, 8]
+    bp = st[:, :, 1, 11]
+    c = (bp + bp.amax(-1, keepdim=True))[:, None, None]
+    x0 = alpha * st[:, None, None, :, 0, 11] + ((prob - alpha[..., None] / 4).abs() * st[:, None, None, :, :, 9]).sum(-1)
+    x1 = (prob * u.sqrt() * st[:, None, None, :, :, 10]).sum(-1)
+    x2 = c * (prob * beta).sum(-1)
+    x3 = c * (prob * (u + beta.square())).sum(-1)
+    th = theta.to(dtype)[:, None, None, None, :]
+    value = ((x0 * th[..., 0] + x1 * th[..., 1]) + x2 * th[..., 2]) + x3 * th[..., 3]
+    return value.sum(2) / m
+
+
+def route_features(q, keys, stats, dtype=torch.float32):
+    """RouteOps.features (RV/ops.py:80-111) for all pages valid: q [H,Q,D] ->
+    features [H,Q,P,4] and logZ [H,Q]."""
+    h, n, d = q.shape
+    q = deployed(q).to(dtype)
+    k = deployed(keys).to(dtype)
+    st = stats.to(dtype)
+    z = torch.einsum('hqd,hprd->hqpr', q, k) / math.sqrt(d)
+    logz = z.flatten(2).logsumexp(-1)
+    prob = (z - logz[:, :, None, None]).exp()
+    alpha = prob.sum(-1)
+    q2 = q.square().reshape(h, n, 8, 16).sum(-1) / d
+    qn = q.norm(dim=-1) / math.sqrt(d)
+    u = torch.einsum('hqg,hprg->hqpr', q2, st[..., :8]).clamp_min(0)
+    beta = qn[:, :, None, None] * st[:, None, :, :, 8]
+    bp = st[:, :, 1, 11]
+    c = bp[:, None, :] + bp.amax(-1)[:, None, None]
+    x0 = alpha * st[:, None, :, 0, 11] + ((prob - alpha[..., None] / 4).abs() * st[:, None, :, :, 9]).sum(-1)
+    x1 = (prob * u.sqrt() * st[:, None, :, :, 10]).sum(-1)
+    x2 = c * (prob * beta).sum(-1)
+    x3 = c * (prob * (u + beta.square())).sum(-1)
+    return torch.stack((x0, x1, x2, x3), -1), logz
+
+
+def _rank_desc(score, valid):
+    """Stable descending order: larger score first, ties -> lower page index.
+    Invalid entries last."""
+    s = score.masked_fill(~valid, -torch.inf)
+    return s.sort(dim=-1, descending=True, stable=True).indices
+
+
+def select_base(risk_, own, count):
+    """Base tier LUT (VR/runtime.py:279-288): [own, 0..23, the count-25
+    highest-risk pages excluding own and anchors, by descending risk]."""
+    h, t, p = risk_.shape
+    page = torch.arange(p)
+    valid = (page[None, None] >= ANCHORS) & (page[None, None] != own[..., None])
+    order = _rank_desc(risk_, valid)[..., :count - 1 - ANCHORS]
+    frame = page[:ANCHORS].expand(h, t, -1)
+    return torch.cat((own[..., None], frame, order), -1).int()
+
+
+def quota_mask(risk_, own, current, total):
+    """Anchor/history/current partition selection (VB/quota_mask.py:7-39):
+    pages < 24 always; history [24, P-72) keeps its top (total - A); current
+    [P-72, P) keeps its top A with own forced (+inf); ties -> lower index."""
+    h, t, p = risk_.shape
+    mask = torch.zeros(h, t, p, dtype=torch.bool)
+    mask[..., :ANCHORS] = True
+    for hh in range(h):
+        a = int(current[hh])
+        slots_hist = total - a
+        hist = risk_[hh, :, ANCHORS:p - CURRENT]
+        if slots_hist > 0:
+            order = hist.sort(dim=-1, descending=True, stable=True).indices[:, :slots_hist] + ANCHORS
+            mask[hh].scatter_(-1, order, True)
+        cur = risk_[hh, :, p - CURRENT:].clone()
+        cur.scatter_(-1, (own[hh] - (p - CURRENT))[:, None], torch.inf)
+        if a > 0:
+            order = cur.sort(dim=-1, descending=True, stable=True).indices[:, :a] + (p - CURRENT)
+            mask[hh].scatter_(-1, order, True)
+    return mask
+
+
+def lut(risk_, mask, own, count):
+    """Final page LUT (VB/graph.py:210): topk(count) of risk masked to the
+    selection with own = +inf -> own first, then descending risk (ties -> lower
+    index; torch.topk leaves tie order unspecified)."""
+    ranked = risk_.masked_fill(~mask, -torch.inf).scatter(-1, own[..., None], torch.inf)
+    return ranked.sort(dim=-1, descending=True, stable=True).indices[..., :count].int()
+
+
+def select_topk(risk_, own, count):
+    """Fixed-count selection with own forced, no anchors (RouteOps.select with
+    threshold None, RV/ops.py:113-138; VR/fixed_page_select.py:8-47)."""
+    ranked = risk_.scatter(-1, own[..., None], torch.inf)
+    ids = ranked.sort(dim=-1, descending=True, stable=True).indices[..., :count]
+    mask = torch.zeros_like(risk_, dtype=torch.bool).scatter(-1, ids, True)
+    return ids.int(), mask
+
+
+def mask_from_ids(ids, pages):
+    """Selected-page set of each (head, block) from its LUT
+    (RV/tuned_attention.py:37-40; LE high_sparse_runtime.py:12-17)."""
+    h, t, _ = ids.shape
+    return torch.zeros(h, t, pages, dtype=torch.bool).scatter(-1, ids.long(), True)
+
+
+# ------------------------------------------------------------- attention ----
+
+def selected_attention(q, k, v, s, basis, ids, dtype=torch.float32, tiles=None):
+    """SelectedAttention.fixed (RV/runtime.py:107-133): exact softmax attention
+    over the LUT pages, summary compensation over the unselected pages (rep
+    logits, V mean plus Haar/rank-8 detail through the basis), and the log-mass
+    merge.  q [1,N,H,D]; k,v [1,64P,H,D]; s a Summary over the P pages; basis
+    [H,D,8]; ids [H,T,C].  Returns [1,N,H,D] in `dtype` (callers round to bf16).
+    `tiles` optionally restricts the query blocks evaluated."""
+    _, n, h, d = q.shape
+    p = k.shape[1] // 64
+    count = ids.shape[-1]
+    query_all = q[0].transpose(0, 1)
+    keys = k[0].transpose(0, 1).reshape(h, p * 64, d)
+    values = v[0].transpose(0, 1).reshape(h, p * 64, d)
+    reps = s.keys[:, :p].reshape(h, p * 4, d).to(dtype)
+    means = s.mean[:, :p].to(dtype)
+    detail = s.detail[:, :p].to(dtype).flatten(1, 2)
+    bas = deployed(basis).to(dtype)
+    ha = haar(dtype)
+    mask = mask_from_ids(ids, p)
+    offsets = torch.arange(64)
+    tiles = range(n // 64) if tiles is None else tiles
+    out = torch.zeros(h, n, d, dtype=dtype)
+    for tile in tiles:
+        query = query_all[:, tile * 64:(tile + 1) * 64].to(dtype)
+        sel = ids[:, tile, :count].long()
+        tokens = (sel[:, :, None] * 64 + offsets).flatten(1)
+        index = tokens[:, :, None].expand(-1, -1, d)
+        kk = keys.gather(1, index).to(dtype)
+        vv = values.gather(1, index).to(dtype)
+        z = torch.bmm(query, kk.transpose(1, 2)) / math.sqrt(d)
+        ze = z.logsumexp(-1)
+        exact = torch.bmm(z.softmax(-1), vv)
+        zs = torch.bmm(query, reps.transpose(1, 2)).reshape(h, 64, p, 4) / math.sqrt(d)
+        zs = zs.masked_fill(mask[:, tile, None, :, None], -torch.inf)
+        zt = zs.flatten(2).logsumexp(-1) + math.log(16)
+        normalizer = torch.where(torch.isfinite(zt), zt - math.log(16), torch.zeros_like(zt))
+        weights = (zs - normalizer[:, :, None, None]).exp()
+        mean = torch.bmm(weights.sum(-1), means)
+        contrasts = torch.einsum('hqpr,ar->hqpa', weights, ha)
+        code = torch.bmm(contrasts.flatten(2), detail)
+        tail = mean + torch.bmm(code, bas.transpose(1, 2))
+        total = torch.logaddexp(ze, zt)
+        out[:, tile * 64:(tile + 1) * 64] = exact * (ze - total).exp()[..., None] + tail * (zt - total).exp()[..., None]
+    return out.transpose(0, 1)[None]
+
+
+def dense_attention(q, k, v, dtype=torch.float32, chunk=512):
+    """Full softmax attention over all window tokens: the all-pages-exact case
+    (RV/test_ops.py:19-23 compares against scaled_dot_product_attention)."""
+    _, n, h, d = q.shape
+    qq = q[0].transpose(0, 1).to(dtype)
+    kk = k[0].transpose(0, 1).to(dtype)
+    vv = v[0].transpose(0, 1).to(dtype)
+    out = torch.empty(h, n, d, dtype=dtype)
+    for a in range(0, n, chunk):
+        z = torch.bmm(qq[:, a:a + chunk], kk.transpose(1, 2)) / math.sqrt(d)
+        out[:, a:a + chunk] = torch.bmm(z.softmax(-1), vv)
+    return out.transpose(0, 1)[None]
+
+
+# ---------------------------------------------------------------- checks ----
+
+def near_tie_rows(risk_, boundary, rel=1e-3):
+    """Rows whose selection boundary is a near tie: the last kept and first
+    dropped scores (in stable descending order) differ by at most `rel`
+    relative.  boundary [H,T] = number kept from `risk_` (already restricted to
+    the candidates, -inf elsewhere).  Returns bool [H,T]."""
+    s = risk_.sort(dim=-1, descending=True).values
+    idx = boundary.clamp(1, s.shape[-1] - 1).long()
+    last = s.gather(-1, (idx - 1)[..., None])[..., 0]
+    nxt = s.gather(-1, idx[..., None])[..., 0]
+    scale = torch.maximum(last.abs(), nxt.abs())
+    tie = (last - nxt).abs() <= rel * scale
+    return tie & torch.isfinite(nxt)
+
+
+def rel_l2(a, b):
+    a = a.double()
+    b = b.double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))

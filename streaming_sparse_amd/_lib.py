@@ -1,0 +1,48 @@
+"""ctypes binding of libssattn.so (declared in include/ssattn.h).
+
+The library is built in-tree by ``streaming_sparse_amd.build``.  There is no
+fallback: if the library is missing or a call fails, an error is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssattn.so")
+_lib = None
+
+_vp, _i, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
+SIGNATURES = {
+    "ssa_rep_values": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp],
+    "ssa_route": [_vp, _ll, _ll, _ll, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp],
+}
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m streaming_sparse_amd.build`")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        _lib = handle
+    return _lib
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def check(status: int, name: str):
+    if status != 0:
+        raise RuntimeError(f"{name} failed with hipError {status}")

@@ -1,0 +1,360 @@
+// Page router for gfx950: probe logits, row normaliser, risk and the page
+// table, fused in one kernel per (head, pair of query blocks).
+//
+// Reference path (intersection tier, VB/graph.py:102-211):
+//   z    = bf16(probe) . bf16(repK)^T * D^-1/2           (VR/tensor_bmm.py:56-66)
+//   norm = max / sum exp over the P*4 reps of each probe  (VR/risk_online.py:151-159)
+//   risk = mean over 16 probes of ((t0 x0 + t1 x1) + t2 x2) + t3 x3
+//                                                         (VR/risk_online.py:86-122)
+//   mask = quota selection (VB/quota_mask.py:7-39) or the base LUT
+//          (VR/runtime.py:279-288) or fixed top-k (VR/fixed_page_select.py:8-47)
+//   ids  = own first, then descending risk                (VB/graph.py:210)
+//
+// Workgroup: 256 threads (4 waves) = 32 probes (2 query blocks) of one head.
+// Each wave takes every 4th tile of 32 reps (8 pages).  S^T = R . Probe^T runs
+// on v_mfma_f32_32x32x16_bf16, so a lane holds one probe and the 4 reps of
+// each of its pages: the page's features are lane-local.  Two passes over the
+// reps: the first finds each probe's max and sum of exp, the second turns the
+// recomputed logits into probabilities and features; per-page values are
+// summed over the 16 probe lanes of a block with cross-lane shuffles.  The
+// risk rows then stay in LDS for selection, which ranks 64-bit keys
+// (orderable risk, ~page) by counting: no sort network, ties -> lower page.
+#include "common.h"
+
+using namespace ssa;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxPages = 512;
+constexpr int kAnchors = 24;
+constexpr int kCurrent = 72;
+
+__constant__ int kProbeOffsets[16] = {0, 4, 8, 13, 17, 21, 25, 29, 34, 38, 42, 46, 50, 55, 59, 63};
+
+struct RouteParams {
+  const uint16_t* q;           // probe source
+  long long q_head, q_block, q_row;   // element strides: head, query block, probe row
+  int gathered;                // 1: q is [H,T,16,D] probes; 0: q is [1,N,H,D] queries
+  const uint16_t* rk;          // rep keys [H, HP, 4, D]
+  const uint16_t* stats;       // [H, HP, 4, 12]
+  const float* theta;          // [H, 4]
+  const int32_t* current;      // [H] current-page quota A (quota mode)
+  const int32_t* own;          // [H, T] or null (own = P - T + t)
+  float* risk;                 // [H, T, P]
+  int32_t* ids;                // [H, T, C] or null
+  uint8_t* mask;               // [H, T, P] or null
+  int H, T, P, HP, C, mode, total;
+};
+
+struct Smem {
+  float part[4][32][2];        // per-wave (max, sum) of each probe
+  float risk[2][kMaxPages];
+  unsigned long long key[2][kMaxPages];
+  uint8_t sel[2][kMaxPages];
+  float bmax_w[4];
+};
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ void rep_logits(const uint16_t* rkh, int tile, int P, int lane, const u32x4 (&qop)[8],
+                                           f32x16& S) {
+  // A operand: rep row tile*32 + lane%32, dims 64*hh + 8*st + [0,8)
+  const int hh = lane >> 5;
+  const int row = min(tile * 32 + (lane & 31), P * 4 - 1);
+  const uint16_t* a = rkh + (long long)row * kHeadDim + 64 * hh;
+  u32x4 av[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) av[st] = ldg16(a + 8 * st);
+  S = f32x16{};
+#pragma unroll
+  for (int st = 0; st < 8; ++st) S = mfma32(av[st], qop[st], S);
+}
+
+__global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
+  __shared__ Smem s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int NP = (p.T + 1) >> 1;
+  const int work = xcd_remap(blockIdx.x, p.H * NP);
+  const int h = work / NP, t0 = 2 * (work % NP);
+  const int P = p.P;
+  const int pi = lane & 31, hh = lane >> 5;
+  const int blk = pi >> 4, m = pi & 15;
+  const int tq = min(t0 + blk, p.T - 1);
+
+  // probe operand (B): dims 64*hh + 8*st + [0,8); and its moments
+  const long long row = p.gathered ? m : kProbeOffsets[m];
+  const uint16_t* qp = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row + 64 * hh;
+  u32x4 qop[8];
+  float q2[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 8 * st);
+  {
+    float g4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float a = bf16_lo(qop[st][w]), b = bf16_hi(qop[st][w]);
+        g4[st >> 1] += a * a + b * b;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float other = __shfl_xor(g4[g], 32);
+      q2[4 * hh + g] = g4[g] / kHeadDim;
+      q2[4 * (1 - hh) + g] = other / kHeadDim;
+    }
+  }
+  float qsum = 0.f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) qsum += q2[g];
+  const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
+
+  // per-head bound of the page value norm: max_p stats[p,1,11]
+  const uint16_t* sth = p.stats + (long long)h * p.HP * 48;
+  {
+    float b = -INFINITY;
+    for (int i = tid; i < P; i += kThreads) b = fmaxf(b, bf16_to_f32(sth[i * 48 + 12 + 11]));
+    b = wave_max(b);
+    if (lane == 0) s.bmax_w[wave] = b;
+  }
+
+  const uint16_t* rkh = p.rk + (long long)h * p.HP * 4 * kHeadDim;
+  const int ntiles = (P + 7) >> 3;
+  const float inv_sqrt_d = 1.0f / sqrtf((float)kHeadDim);
+
+  // pass 1: max and sum of exp over all reps, per probe
+  float mx = -INFINITY, den = 0.f;
+  for (int tile = wave; tile < ntiles; tile += 4) {
+    f32x16 S;
+    rep_logits(rkh, tile, P, lane, qop, S);
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int page = tile * 8 + 2 * (i >> 2) + hh;
+      S[i] = page < P ? S[i] * inv_sqrt_d : -INFINITY;
+      tmax = fmaxf(tmax, S[i]);
+    }
+    const float mnew = fmaxf(mx, tmax);
+    const float muse = mnew == -INFINITY ? 0.f : mnew;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc += expf(S[i] - muse);
+    den = (mx == -INFINITY ? 0.f : den * expf(mx - mnew)) + acc;
+    mx = mnew;
+  }
+  {
+    const float omx = __shfl_xor(mx, 32), oden = __shfl_xor(den, 32);
+    const float mm = fmaxf(mx, omx);
+    den = (mx == -INFINITY ? 0.f : den * expf(mx - mm)) + (omx == -INFINITY ? 0.f : oden * expf(omx - mm));
+    mx = mm;
+    if (hh == 0) {
+      s.part[wave][pi][0] = mx;
+      s.part[wave][pi][1] = den;
+    }
+  }
+  __syncthreads();
+  float MX = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) MX = fmaxf(MX, s.part[w][pi][0]);
+  float DEN = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float wm = s.part[w][pi][0];
+    if (wm != -INFINITY) DEN += s.part[w][pi][1] * expf(wm - MX);
+  }
+  const float bmax = fmaxf(fmaxf(s.bmax_w[0], s.bmax_w[1]), fmaxf(s.bmax_w[2], s.bmax_w[3]));
+  const float th0 = p.theta[h * 4 + 0], th1 = p.theta[h * 4 + 1], th2 = p.theta[h * 4 + 2], th3 = p.theta[h * 4 + 3];
+
+  // pass 2: probabilities -> four features -> theta-weighted value -> probe mean
+  for (int tile = wave; tile < ntiles; tile += 4) {
+    f32x16 S;
+    rep_logits(rkh, tile, P, lane, qop, S);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int page = tile * 8 + 2 * j + hh;
+      const int pc = min(page, P - 1);
+      const uint16_t* sp = sth + pc * 48;
+      uint32_t sw[24];
+#pragma unroll
+      for (int c = 0; c < 6; ++c) {
+        const u32x4 v4 = ldg16(sp + 8 * c);
+        sw[4 * c + 0] = v4[0];
+        sw[4 * c + 1] = v4[1];
+        sw[4 * c + 2] = v4[2];
+        sw[4 * c + 3] = v4[3];
+      }
+      // stats[p, r, f] = element r*12 + f of the 48 bf16 values
+      auto st = [&](int r, int f) -> float {
+        const int e = r * 12 + f;
+        return (e & 1) ? bf16_hi(sw[e >> 1]) : bf16_lo(sw[e >> 1]);
+      };
+      float prob[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) prob[i] = expf(S[4 * j + i] * inv_sqrt_d - MX) / DEN;
+      const float alpha = ((prob[0] + prob[1]) + prob[2]) + prob[3];
+      const float c = st(1, 11) + bmax;
+      float x0 = alpha * st(0, 11), x1 = 0.f, x2 = 0.f, x3 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float u = 0.f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) u = fmaf(q2[g], st(i, g), u);
+        u = fmaxf(u, 0.f);
+        const float beta = qn * st(i, 8);
+        x0 += fabsf(prob[i] - alpha * 0.25f) * st(i, 9);
+        x1 += prob[i] * sqrtf(u) * st(i, 10);
+        x2 += prob[i] * beta;
+        x3 += prob[i] * (u + beta * beta);
+      }
+      x2 *= c;
+      x3 *= c;
+      float val = ((x0 * th0 + x1 * th1) + x2 * th2) + x3 * th3;
+      // sum over the 16 probes of this lane's block (lanes 32*hh + 16*blk + [0,16))
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) val += __shfl_xor(val, o);
+      if (m == 0 && page < P) s.risk[blk][page] = val / 16.0f;
+    }
+  }
+  __syncthreads();
+
+  const int nrow = min(2, p.T - t0);
+  for (int i = tid; i < 2 * P; i += kThreads) {
+    const int b = i / P, pg = i % P;
+    if (b < nrow) p.risk[((long long)h * p.T + t0 + b) * P + pg] = s.risk[b][pg];
+  }
+  if (p.mode < 0) return;
+
+  // ---------------------------------------------------------------- select
+  // keys: (orderable risk << 32) | ~page, descending order = risk desc, page asc
+  int own[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int tb = min(t0 + b, p.T - 1);
+    own[b] = p.own ? p.own[(long long)h * p.T + tb] : P - p.T + tb;
+  }
+  const int A = p.mode == 1 ? p.current[h] : 0;
+  for (int i = tid; i < 2 * P; i += kThreads) {
+    const int b = i / P, pg = i % P;
+    unsigned long long key = ((unsigned long long)orderable(s.risk[b][pg]) << 32) | (0xffffffffu - (uint32_t)pg);
+    bool cand;
+    if (p.mode == 0) {
+      cand = pg >= kAnchors && pg != own[b];
+    } else if (p.mode == 1) {
+      cand = pg >= kAnchors;
+      if (pg == own[b]) key = ~0ull;                       // own forced first (+inf)
+    } else {
+      cand = true;
+      if (pg == own[b]) key = ~0ull;
+    }
+    s.key[b][pg] = cand ? key : 0ull;
+  }
+  __syncthreads();
+  for (int i = tid; i < 2 * P; i += kThreads) {
+    const int b = i / P, pg = i % P;
+    const unsigned long long k = s.key[b][pg];
+    bool keep = false;
+    int rank = 0;
+    if (k != 0ull) {
+      if (p.mode == 1) {
+        const bool cur = pg >= P - kCurrent;
+        const int lo = cur ? P - kCurrent : kAnchors, hi = cur ? P : P - kCurrent;
+        for (int j = lo; j < hi; ++j) rank += s.key[b][j] > k;
+        keep = rank < (cur ? A : p.total - A);
+      } else {
+        for (int j = 0; j < P; ++j) rank += s.key[b][j] > k;
+        keep = rank < (p.mode == 0 ? p.C - 1 - kAnchors : p.C);
+      }
+    }
+    if (p.mode != 2 && pg < kAnchors) keep = true;
+    if (p.mode == 0 && pg == own[b]) keep = true;
+    s.sel[b][pg] = keep;
+    if (p.mode == 0 && keep && pg >= kAnchors && pg != own[b] && b < nrow && p.ids)
+      p.ids[((long long)h * p.T + t0 + b) * p.C + 1 + kAnchors + rank] = pg;
+    if (p.mode == 2 && keep && b < nrow && p.ids)
+      p.ids[((long long)h * p.T + t0 + b) * p.C + rank] = pg;
+  }
+  __syncthreads();
+  if (p.mode == 0 && p.ids) {
+    for (int i = tid; i < 2 * (1 + kAnchors); i += kThreads) {
+      const int b = i / (1 + kAnchors), j = i % (1 + kAnchors);
+      if (b < nrow) p.ids[((long long)h * p.T + t0 + b) * p.C + j] = j == 0 ? own[b] : j - 1;
+    }
+  }
+  if (p.mode == 1 && p.ids) {
+    // LUT: own first, then every selected page by descending risk
+    for (int i = tid; i < 2 * P; i += kThreads) {
+      const int b = i / P, pg = i % P;
+      if (!s.sel[b][pg] || b >= nrow) continue;
+      int slot = 0;
+      if (pg != own[b]) {
+        const unsigned long long k = ((unsigned long long)orderable(s.risk[b][pg]) << 32) | (0xffffffffu - (uint32_t)pg);
+        int rank = 0;
+        for (int j = 0; j < P; ++j) {
+          if (!s.sel[b][j] || j == own[b]) continue;
+          const unsigned long long kj = ((unsigned long long)orderable(s.risk[b][j]) << 32) | (0xffffffffu - (uint32_t)j);
+          rank += kj > k;
+        }
+        slot = 1 + rank;
+      }
+      if (slot < p.C) p.ids[((long long)h * p.T + t0 + b) * p.C + slot] = pg;
+    }
+  }
+  if (p.mask) {
+    for (int i = tid; i < 2 * P; i += kThreads) {
+      const int b = i / P, pg = i % P;
+      if (b < nrow) p.mask[((long long)h * p.T + t0 + b) * P + pg] = s.sel[b][pg];
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// mode: -1 risk only; 0 base (own + 24 anchors + top C-25); 1 anchor/current/
+// history quota with `total` = A+B non-anchor pages and current[h] = A;
+// 2 fixed top-C with own forced.
+int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
+              int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
+              const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, int heads, int blocks, int pages,
+              int head_pages, int count, int mode, int total, hipStream_t stream) {
+  if (heads <= 0 || blocks <= 0 || pages <= 0 || pages > kMaxPages || head_pages < pages || mode < -1 ||
+      mode > 2)
+    return (int)hipErrorInvalidValue;
+  if (mode == 0 && (count < 1 + kAnchors || pages < kAnchors + kCurrent)) return (int)hipErrorInvalidValue;
+  if (mode == 1 && (count != kAnchors + total || pages <= kAnchors + kCurrent || current == nullptr))
+    return (int)hipErrorInvalidValue;
+  if (mode == 2 && (count < 1 || count > pages)) return (int)hipErrorInvalidValue;
+  RouteParams p;
+  p.q = (const uint16_t*)q;
+  p.q_head = q_head_stride;
+  p.q_block = q_block_stride;
+  p.q_row = q_row_stride;
+  p.gathered = gathered;
+  p.rk = (const uint16_t*)keys;
+  p.stats = (const uint16_t*)stats;
+  p.theta = theta;
+  p.current = current;
+  p.own = own;
+  p.risk = risk;
+  p.ids = ids;
+  p.mask = mask;
+  p.H = heads;
+  p.T = blocks;
+  p.P = pages;
+  p.HP = head_pages;
+  p.C = count;
+  p.mode = mode;
+  p.total = total;
+  const int np = (blocks + 1) / 2;
+  hipLaunchKernelGGL(route_kernel, dim3(heads * np), dim3(kThreads), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

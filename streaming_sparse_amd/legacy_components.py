@@ -1,0 +1,111 @@
+"""Attention dispatcher with the reference's signatures, on the HIP library.
+
+Mirrors local_experiments/video_runtime_v1/legacy_components.py:
+``attention(q,k,v,s,basis,ids,workspace,*,bf16_av=True)`` (:24-46) and
+``risk(probes,z,summary,theta)`` (:14-22).  Every call goes to libssattn.so;
+there is no CPU or eager-torch fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .ops import Summary
+
+HEAD_DIM = 128
+
+
+def _check_summary(s: Summary, h: int, p: int):
+    hp = s.head_pages
+    d = HEAD_DIM
+    for name, t, inner in (('keys', s.keys, 4 * d), ('mean', s.mean, d), ('detail', s.detail, 24),
+                           ('stats', s.stats, 48)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"summary.{name} must be bf16")
+        if t.shape[0] != h or t.shape[1] < p:
+            raise ValueError(f"summary.{name} shape {tuple(t.shape)} does not cover {h} heads x {p} pages")
+        if t.stride(0) != hp * inner or t[0, 0].numel() != inner or not t[0].is_contiguous():
+            raise ValueError(f"summary.{name} must be a page slice of a contiguous [H,{hp},...] slab")
+    return hp
+
+
+def kv_strides(k: torch.Tensor, v: torch.Tensor):
+    """(token stride, head stride) in elements of the resident K/V cache.
+    Token-major contiguous [1,L,H,D] or the head-major strided variant
+    (legacy_components.py:28-30)."""
+    d = k.shape[-1]
+    major = k.stride(1) == d and k.stride(2) >= k.shape[1] * d
+    if k.is_contiguous() and v.is_contiguous():
+        return k.stride(1), k.stride(2)
+    if major and k.stride() == v.stride():
+        return k.stride(1), k.stride(2)
+    raise ValueError("k/v must be contiguous [1,L,H,D] or head-major with equal strides")
+
+
+@torch.no_grad()
+def rep_values(s: Summary, basis: torch.Tensor, pages: int, out: torch.Tensor):
+    """Per-rep compensation values [H,P,4,D] (bf16) for the fused kernel."""
+    h = s.mean.shape[0]
+    hp = _check_summary(s, h, pages)
+    b = basis.to(torch.bfloat16).contiguous()
+    if b.shape != (h, HEAD_DIM, 8):
+        raise ValueError("basis must be [H,128,8]")
+    _lib.check(_lib.lib().ssa_rep_values(_lib.ptr(s.mean), _lib.ptr(s.detail), _lib.ptr(b), _lib.ptr(out), h, pages,
+                                         hp, out.shape[1], _lib.stream_handle(out.device)), "ssa_rep_values")
+    return out
+
+
+@torch.no_grad()
+def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=False):
+    """Exact attention over the LUT pages + summary compensation + merge.
+
+    q [1,N,H,128] bf16 contiguous; k, v [1,64P,H,128] bf16 (resident cache);
+    s a Summary covering the P pages; basis [H,128,8]; ids [H,N/64,C] int32 with
+    own page first.  Returns ``out`` [1,N,H,128] bf16, owned by `workspace`
+    and overwritten by the next call.  ``bf16_av`` is accepted for signature
+    compatibility; ``precise_av`` selects two-term (hi+lo) bf16 P.V in every
+    unit, the reference's exact-stage arithmetic."""
+    _, n, h, d = q.shape
+    p = k.shape[1] // 64
+    count = ids.shape[-1]
+    if d != HEAD_DIM or q.dtype != torch.bfloat16 or not q.is_contiguous():
+        raise ValueError("q must be contiguous [1,N,H,128] bf16")
+    if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or k.shape != v.shape:
+        raise ValueError("k, v must be bf16 with equal shapes")
+    tok, head = kv_strides(k, v)
+    hp = _check_summary(s, h, p)
+    if ids.dtype != torch.int32 or ids.shape[:2] != (h, n // 64):
+        raise ValueError("ids must be int32 [H,N/64,C]")
+    ids = ids.contiguous()
+
+    def buf(name, shape, dtype):
+        return workspace.tensor('ssa_' + name, shape, q.device, dtype)
+
+    vrep = rep_values(s, basis, p, buf('rep_values', (h, p, 4, d), torch.bfloat16))
+    out = buf('out', q.shape, q.dtype)
+    flags = 1 if precise_av else 0
+    _lib.check(_lib.lib().ssa_attention(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(s.keys), _lib.ptr(vrep),
+                                        _lib.ptr(ids), _lib.ptr(out), n, h, p, hp, p, count, tok, head, flags,
+                                        _lib.stream_handle(q.device)), "ssa_attention")
+    return out
+
+
+@torch.no_grad()
+def risk(probes, z, summary, theta):
+    """Per-page risk [H,T,P] fp32 from probe rows [H,T,16,128].  The probe
+    logits are recomputed on chip from `probes` and the rep keys (z is the
+    reference's precomputed q.repK/sqrt(D) and is only shape-checked)."""
+    h, t, m, d = probes.shape
+    p = summary.mean.shape[1]
+    if m != 16 or d != HEAD_DIM:
+        raise ValueError("probes must be [H,T,16,128]")
+    if z is not None and tuple(z.shape[:3]) != (h, t, m):
+        raise ValueError("z does not match probes")
+    hp = _check_summary(summary, h, p)
+    pr = probes.to(torch.bfloat16).contiguous()
+    th = theta.float().contiguous()
+    out = torch.empty(h, t, p, device=probes.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ssa_route(_lib.ptr(pr), t * m * d, m * d, d, 1, _lib.ptr(summary.keys),
+                                    _lib.ptr(summary.stats), _lib.ptr(th), None, None, _lib.ptr(out), None, None,
+                                    h, t, p, hp, 0, -1, 0, _lib.stream_handle(probes.device)), "ssa_route")
+    return out

@@ -1,0 +1,83 @@
+"""Page router with the tiers of the reference runtime, on the HIP library.
+
+``route`` returns ``(ids, mask, risk, stats)`` like the reference's
+``BatchGraphs.replay`` (reproduction/vbench_current/graph.py:212-221):
+
+* ``tier='base'``: ids = [own, anchors 0..23, the floor(0.15 P) - 25 highest-
+  risk other pages] (local_experiments/video_runtime_v1/runtime.py:279-288).
+* ``tier='intersection'``: anchors + top A current pages (own forced) + top
+  (n - A) history pages; ids = own first then descending risk
+  (reproduction/vbench_current/quota_mask.py:7-39, graph.py:150-151,210).
+* ``tier='topk'``: fixed top-floor(0.1 P) with own forced
+  (local_experiments/review_v1/ops.py:113-138).
+
+Probe rows are read straight from q (16 per 64-query block at the reference's
+offsets, local_experiments/video_runtime_v1/runtime.py:84).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .legacy_components import HEAD_DIM, _check_summary
+
+ANCHORS = 24
+CURRENT = 72
+MODES = {'base': 0, 'intersection': 1, 'topk': 2}
+
+
+def tier_count(tier: str, pages: int, n: int | None = None) -> int:
+    if tier == 'base':
+        return pages * 15 // 100
+    if tier == 'intersection':
+        return ANCHORS + int(n)
+    if tier == 'topk':
+        return max(1, int(pages * 0.1))
+    raise ValueError(tier)
+
+
+@torch.no_grad()
+def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=None, workspace=None,
+          want_mask=True):
+    """q [1,N,H,128] bf16 queries of the current chunk; summary over the P
+    window pages; theta [H,4]; own [H,T] (default: page P-T+t).  For the
+    intersection tier pass current_slots [H] (A per head, >= 1) and n = A+B."""
+    _, nq, h, d = q.shape
+    if d != HEAD_DIM or q.dtype != torch.bfloat16 or not q.is_contiguous():
+        raise ValueError("q must be contiguous [1,N,H,128] bf16")
+    t = nq // 64
+    p = summary.mean.shape[1]
+    hp = _check_summary(summary, h, p)
+    mode = MODES[tier]
+    count = tier_count(tier, p, n)
+    dev = q.device
+    cur = None
+    total = 0
+    if tier == 'intersection':
+        if current_slots is None or n is None:
+            raise ValueError("intersection tier needs current_slots and n")
+        cur = torch.as_tensor(current_slots, device=dev).to(torch.int32).contiguous()
+        if cur.shape != (h,):
+            raise ValueError("current_slots must be [H]")
+        total = int(n)
+    if tier == 'base' and p < ANCHORS + CURRENT:
+        raise ValueError("base tier needs a history window")
+
+    def buf(name, shape, dtype):
+        if workspace is None:
+            return torch.empty(shape, device=dev, dtype=dtype)
+        return workspace.tensor('route_' + name, shape, dev, dtype)
+
+    ow = None if own is None else own.to(device=dev, dtype=torch.int32).contiguous()
+    risk = buf('risk', (h, t, p), torch.float32)
+    ids = buf('ids', (h, t, count), torch.int32)
+    mask = buf('mask', (h, t, p), torch.uint8) if want_mask else None
+    th = theta.float().contiguous()
+    _lib.check(_lib.lib().ssa_route(_lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys),
+                                    _lib.ptr(summary.stats), _lib.ptr(th), _lib.ptr(cur), _lib.ptr(ow),
+                                    _lib.ptr(risk), _lib.ptr(ids), _lib.ptr(mask), h, t, p, hp, count, mode, total,
+                                    _lib.stream_handle(dev)), "ssa_route")
+    stats = torch.zeros(3, device=dev, dtype=torch.int64)
+    return ids, (mask.bool() if mask is not None else None), risk, stats
