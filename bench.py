@@ -34,7 +34,21 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--cpu-sample-blocks", type=int, default=4)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB (scales rocprof FETCH/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def calibrate_copy(mib):
+    import torch
+    src = torch.empty(mib * (1 << 20), dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes": src.numel(), "copies": 3}), flush=True)
 
 
 def time_loop(fn, iters, stream):
@@ -55,6 +69,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only; heads shard across GPUs without "
                                    "exchange, so run --gpus 1"}))
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
     import torch
     from streaming_sparse_amd import _lib, workload
     from streaming_sparse_amd.attention import Workspace
@@ -73,9 +90,12 @@ def main():
     ws = Workspace()
     stream = torch.cuda.current_stream(dev)
 
+    basis = g.basis.to(torch.bfloat16).contiguous()   # the caller keeps the basis bf16-rounded
+
     def step():
-        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, want_mask=False)
-        return attention(g.q, g.k, g.v, g.summary, g.basis, ids, ws, precise_av=args.precise_av)
+        # own page of block t is P-72+t (the kernel's default when own is None)
+        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, precise_av=args.precise_av)
 
     for _ in range(args.warmup):
         step()
@@ -92,9 +112,9 @@ def main():
     ms_call = start.elapsed_time(end) / args.steps
 
     # per-kernel timings (same stream, same inputs)
-    ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, want_mask=False)
+    ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
     vrep = ws.tensor('ssa_rep_values', (H, P, 4, D), dev, torch.bfloat16)
-    rep_values(g.summary, g.basis, P, vrep)
+    rep_values(g.summary, basis, P, vrep)
     tok, head = kv_strides(g.k, g.v)
     L = _lib.lib()
     flags = 1 if args.precise_av else 0
@@ -106,10 +126,10 @@ def main():
                    "ssa_attention")
 
     def route_only():
-        route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, want_mask=False)
+        route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
 
     def rep_only():
-        rep_values(g.summary, g.basis, P, vrep)
+        rep_values(g.summary, basis, P, vrep)
 
     iters = max(10, args.steps)
     attn_ms = time_loop(attn_only, iters, stream)

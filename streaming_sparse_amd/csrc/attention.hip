@@ -47,8 +47,8 @@ struct AttnParams {
 };
 
 struct Smem {
-  uint8_t kbuf[64 * 256];
-  uint8_t vt[128 * 128];
+  alignas(16) uint8_t kbuf[64 * 256];
+  alignas(16) uint8_t vt[128 * 128];
   int units[kMaxCount + kMaxRepTiles];
   uint32_t maskw[16];
   int nunits;

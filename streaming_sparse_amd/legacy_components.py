@@ -47,7 +47,7 @@ def rep_values(s: Summary, basis: torch.Tensor, pages: int, out: torch.Tensor):
     """Per-rep compensation values [H,P,4,D] (bf16) for the fused kernel."""
     h = s.mean.shape[0]
     hp = _check_summary(s, h, pages)
-    b = basis.to(torch.bfloat16).contiguous()
+    b = basis if (basis.dtype == torch.bfloat16 and basis.is_contiguous()) else basis.to(torch.bfloat16).contiguous()
     if b.shape != (h, HEAD_DIM, 8):
         raise ValueError("basis must be [H,128,8]")
     _lib.check(_lib.lib().ssa_rep_values(_lib.ptr(s.mean), _lib.ptr(s.detail), _lib.ptr(b), _lib.ptr(out), h, pages,

@@ -70,7 +70,9 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
             return torch.empty(shape, device=dev, dtype=dtype)
         return workspace.tensor('route_' + name, shape, dev, dtype)
 
-    ow = None if own is None else own.to(device=dev, dtype=torch.int32).contiguous()
+    ow = None
+    if own is not None:
+        ow = own if (own.dtype == torch.int32 and own.is_contiguous()) else own.to(device=dev, dtype=torch.int32).contiguous()
     risk = buf('risk', (h, t, p), torch.float32)
     ids = buf('ids', (h, t, count), torch.int32)
     mask = buf('mask', (h, t, p), torch.uint8) if want_mask else None
@@ -79,5 +81,12 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
                                     _lib.ptr(summary.stats), _lib.ptr(th), _lib.ptr(cur), _lib.ptr(ow),
                                     _lib.ptr(risk), _lib.ptr(ids), _lib.ptr(mask), h, t, p, hp, count, mode, total,
                                     _lib.stream_handle(dev)), "ssa_route")
-    stats = torch.zeros(3, device=dev, dtype=torch.int64)
-    return ids, (mask.bool() if mask is not None else None), risk, stats
+    if workspace is None:
+        stats = torch.zeros(3, device=dev, dtype=torch.int64)
+    else:
+        key = ('route_stats', (3,), torch.device(dev), torch.int64)
+        if key not in workspace.entries:
+            workspace.entries[key] = torch.zeros(3, device=dev, dtype=torch.int64)
+        stats = workspace.entries[key]
+    # uint8 0/1 storage viewed as bool without a conversion kernel
+    return ids, (mask.view(torch.bool) if mask is not None else None), risk, stats
