@@ -19,6 +19,13 @@
  *   ssa_route       <- VB/graph.py:102-211 BatchGraphs.compute (probe QK, risk,
  *                      quota_mask / base selection, final LUT) and
  *                      VR/legacy_components.py:14-22 risk(probes,z,summary,theta)
+ *   ssa_encode      <- VR/page.py:6-14 encode(summary,reader,phi,B) and
+ *                      VideoRuntime.encode (VR/runtime.py:160-164)
+ *   ssa_pset        <- the Full_Pset branch of BatchGraphs.compute
+ *                      (VB/graph.py:169-208): quota_pool.pool, read /
+ *                      compact_scores (VR/page.py:17-21, VR/reader_reduce.py:150-190,
+ *                      VR/scores.py:54-91), apply_best (VR/scores.py:102-107) and
+ *                      the final LUT (VB/graph.py:210)
  */
 #ifndef SSATTN_H
 #define SSATTN_H
@@ -66,6 +73,40 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, int heads, int blocks, int pages,
               int head_pages, int count, int mode, int total, hipStream_t stream);
+
+/* Full_Pset page encodings of pages [first_page, first_page + pages) of the
+ * summary slab (keys/mean/detail/stats as in ssa_route, capacity head_pages):
+ * coef [H,enc_pages,128] bf16 = co[85] (reader, [5,17]) | 11 zeros | A[32]
+ * (phi, [8,4]); mean_b [H,enc_pages,16] and detail_b [H,enc_pages,3,16] fp64.
+ * Weights fp32: w1t [712, 2*hidden] = both first layers transposed (columns
+ * [0,hidden) reader, [hidden,2*hidden) phi), b1 [2*hidden]; w2_reader
+ * [85,hidden], b2_reader [85]; w2_phi [32,hidden], b2_phi [32] (torch Linear
+ * layout); B [128,16] fp64; basis [H,128,8] bf16.  hidden <= 256. */
+int ssa_encode(const void* keys, const void* mean, const void* detail, const void* stats, int head_pages,
+               const void* basis, const float* w1t, const float* b1, const float* w2_reader, const float* b2_reader,
+               const float* w2_phi, const float* b2_phi, const double* B, void* coef, double* mean_b,
+               double* detail_b, int enc_pages, int heads, int first_page, int pages, int hidden,
+               hipStream_t stream);
+
+/* Full_Pset swap correction of the heads listed in heads[n_heads] (indices
+ * into total_heads), after ssa_route in mode 1 produced risk, mask and ids.
+ * Probe rows as in ssa_route; keys [H,head_pages,4,128] bf16; encodings from
+ * ssa_encode; wq [8,128] fp32 (phi query map).  For each scoped (head, block)
+ * the best legal same-partition swap is applied to mask [H,blocks,pages]
+ * (0/1 bytes) iff its gain > 0 and every legal score is finite, and the row
+ * of ids [H,blocks,count] is rebuilt (own first, then descending risk).
+ * Caller-owned scratch: cand n_heads*blocks*16*48*34 fp64, rows
+ * n_heads*blocks*16*52 fp64, pool n_heads*blocks*64 int32.  Per-row outputs:
+ * gain [n_heads,blocks] fp64, info [n_heads,blocks,3] int32 = (executed, best
+ * pair index remove*32+add, non-finite legal scores); scores
+ * [n_heads,blocks,16,32] fp64 (illegal pairs -1e30) or NULL.
+ * Requires 96 < pages <= 512 and pages - count >= 64. */
+int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
+             int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
+             const double* detail_b, int enc_pages, const float* wq, const float* risk, uint8_t* mask,
+             int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand, double* rows,
+             int32_t* pool, double* gain, int32_t* info, double* scores, int total_heads, int blocks, int pages,
+             int count, hipStream_t stream);
 
 #ifdef __cplusplus
 }

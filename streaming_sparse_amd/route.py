@@ -11,6 +11,11 @@
 * ``tier='topk'``: fixed top-floor(0.1 P) with own forced
   (local_experiments/review_v1/ops.py:113-138).
 
+With ``full_pset`` heads (intersection tier), the Full_Pset swap correction
+runs on those heads after selection and rewrites their mask and ids
+(reproduction/vbench_current/graph.py:169-210); ``stats`` is then
+(executed swaps, corrected rows, non-finite scores).
+
 Probe rows are read straight from q (16 per 64-query block at the reference's
 offsets, local_experiments/video_runtime_v1/runtime.py:84).
 """
@@ -40,10 +45,12 @@ def tier_count(tier: str, pages: int, n: int | None = None) -> int:
 
 @torch.no_grad()
 def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=None, workspace=None,
-          want_mask=True):
+          want_mask=True, full_pset=None, encoding=None, reader=None):
     """q [1,N,H,128] bf16 queries of the current chunk; summary over the P
     window pages; theta [H,4]; own [H,T] (default: page P-T+t).  For the
-    intersection tier pass current_slots [H] (A per head, >= 1) and n = A+B."""
+    intersection tier pass current_slots [H] (A per head, >= 1) and n = A+B.
+    full_pset: head ids to correct with `encoding` (pset.Encoding over the
+    window) and `reader` (pset.Reader)."""
     _, nq, h, d = q.shape
     if d != HEAD_DIM or q.dtype != torch.bfloat16 or not q.is_contiguous():
         raise ValueError("q must be contiguous [1,N,H,128] bf16")
@@ -64,6 +71,11 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
         total = int(n)
     if tier == 'base' and p < ANCHORS + CURRENT:
         raise ValueError("base tier needs a history window")
+    correcting = full_pset is not None and len(full_pset) > 0
+    if correcting:
+        if tier != 'intersection' or encoding is None or reader is None:
+            raise ValueError("full_pset needs the intersection tier, an encoding and a reader")
+        want_mask = True
 
     def buf(name, shape, dtype):
         if workspace is None:
@@ -81,7 +93,10 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
                                     _lib.ptr(summary.stats), _lib.ptr(th), _lib.ptr(cur), _lib.ptr(ow),
                                     _lib.ptr(risk), _lib.ptr(ids), _lib.ptr(mask), h, t, p, hp, count, mode, total,
                                     _lib.stream_handle(dev)), "ssa_route")
-    if workspace is None:
+    if correcting:
+        from . import pset
+        stats, _ = pset.correct(q, summary, encoding, reader, risk, mask, ids, ow, full_pset, workspace)
+    elif workspace is None:
         stats = torch.zeros(3, device=dev, dtype=torch.int64)
     else:
         key = ('route_stats', (3,), torch.device(dev), torch.int64)

@@ -225,3 +225,27 @@ def quota_table(cfg: int, layers: int = 29, steps: int = 4, heads: int = HEADS,
             out[s, l, :, 0] = a
             out[s, l, :, 1] = n - a
     return out
+
+
+def reader_weights(cfg: int = 3, hidden: int = 256) -> dict:
+    """Seeded Full_Pset model weights, fp32 N(0, 0.02), in torch's [out, in]
+    Linear layout.  Structure of the reference models:
+    LocalReader.page = Linear(712,hidden) -> GELU -> Linear(hidden,85)
+    (local_experiments/e27_adaptive_query/coefficients.py:4-8,
+    local_experiments/e29_local_reader/core.py:6-10); AdaptivePhi.page =
+    Linear(712,hidden) -> GELU -> Linear(hidden,32) and AdaptivePhi.query =
+    Linear(128,8,bias=False) (local_experiments/e27_adaptive_query/core.py:8-11);
+    the reader projection B [128,16] (fp64 at use) is N(0,1)/sqrt(128)."""
+    g = torch.Generator().manual_seed(seed_for(cfg, 0, 0, 5))
+
+    def normal(*shape, std=0.02):
+        return (torch.randn(*shape, generator=g) * std).contiguous()
+
+    return dict(
+        reader_w1=normal(hidden, 712), reader_b1=normal(hidden),
+        reader_w2=normal(85, hidden), reader_b2=normal(85),
+        phi_w1=normal(hidden, 712), phi_b1=normal(hidden),
+        phi_w2=normal(32, hidden), phi_b2=normal(32),
+        wq=normal(8, HEAD_DIM),
+        B=(torch.randn(HEAD_DIM, 16, generator=g, dtype=torch.float64) / math.sqrt(HEAD_DIM)).contiguous(),
+    )

@@ -1,0 +1,154 @@
+"""Full_Pset on the HIP path vs. the CPU oracle (oracle/pset.py) on identical
+seeded inputs: config-3 shapes (432-page window, intersection quotas,
+heads {3,4,9}).
+
+Bar: encodings bit-exact except isolated 1-ulp bf16 roundings of the MLP
+outputs; swap scores within 1e-4 of the row's score scale; executed swaps and
+the final masks identical except rows whose decision is a near tie (best and
+second-best legal gain, or the best gain and 0, within 1e-3 relative)."""
+import functools
+import math
+
+import pytest
+import torch
+
+from oracle import pset as opset
+from oracle import reference as ref
+from streaming_sparse_amd import pset, workload
+from streaming_sparse_amd.attention import Workspace
+from streaming_sparse_amd.route import route
+
+pytestmark = pytest.mark.gpu
+HEADS = [3, 4, 9]
+
+
+@functools.lru_cache(maxsize=None)
+def inputs(frames=18):
+    x = workload.make_call(cfg=3, frames=frames)
+    w = workload.reader_weights()
+    tab = workload.quota_table(3)
+    a = tab[0, 3, :, 0]
+    n = int(tab[0, 3, 0].sum())
+    return x, w, a, n
+
+
+def gpu_encoding(x, w, device):
+    g = x.to(device)
+    reader = pset.Reader(w, device)
+    enc = pset.encode(g.summary, g.basis, reader)
+    torch.cuda.synchronize()
+    return g, reader, enc
+
+
+def test_encode_matches_oracle(device):
+    x, w, _, _ = inputs(9)
+    _, _, enc = gpu_encoding(x, w, device)
+    want = opset.encode(x.summary.keys, x.summary.mean, x.summary.detail, x.summary.stats, x.basis, w)
+    for name, got in (('co', enc.co.cpu()), ('A', enc.A.cpu())):
+        ref_v = want[name]
+        diff = got != ref_v
+        frac = float(diff.float().mean())
+        # an fp32 accumulation-order difference moves a value across a bf16
+        # rounding boundary: one bf16 ulp (at most 2^-7 relative), or a few
+        # ulps of a value that cancelled to near zero
+        err = (got.float() - ref_v.float()).abs()
+        bound = ref_v.float().abs() * 2.0 ** -7 + 1e-6
+        print(f"{name}: {int(diff.sum())} of {diff.numel()} bf16 values differ, max abs {float(err.max()):.2e}",
+              flush=True)
+        assert bool((err <= bound).all()) and frac < 1e-3
+    torch.testing.assert_close(enc.mean.cpu(), want['mean'], atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(enc.detail.cpu(), want['detail'], atol=1e-12, rtol=1e-12)
+    assert (enc.coef[..., 85:96] == 0).all()
+
+
+def _near_tie(scores, legal, rel=1e-3):
+    """Rows whose decision is fragile: best two legal scores, or the best
+    score and 0, within `rel` of the row's score scale."""
+    s = scores.masked_fill(~legal, -math.inf).flatten(-2)
+    top = s.topk(2, dim=-1).values
+    scale = s.masked_fill(~legal.flatten(-2), 0).abs().amax(-1).clamp_min(1e-300)
+    return ((top[..., 0] - top[..., 1]).abs() <= rel * scale) | (top[..., 0].abs() <= rel * scale)
+
+
+def test_pset_matches_oracle(device):
+    x, w, a, n = inputs()
+    g, reader, enc = gpu_encoding(x, w, device)
+    ws = Workspace()
+    ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='intersection', own=g.own, current_slots=a, n=n,
+                               workspace=ws)
+    mask0 = mask.clone()
+    ids0 = ids.clone()
+    stats, rows = pset.correct(g.q, g.summary, enc, reader, risk, mask, ids, g.own, HEADS, want_scores=True)
+    torch.cuda.synchronize()
+    # oracle on the same selection, risk and encodings
+    pr = ref.probes(x.q)
+    z = ref.route_logits(pr, x.summary.keys)
+    enc_o = dict(co=enc.co.cpu(), A=enc.A.cpu(), mean=enc.mean.cpu(), detail=enc.detail.cpu())
+    m0 = mask0.cpu()
+    want_mask, orow, ostats = opset.correct(pr.bfloat16().float(), z, risk.cpu(), m0, x.own, enc_o, w['wq'], HEADS)
+    legal = orow['legal'].reshape(len(HEADS), 72, 16, 32)
+    got_s = rows['scores'].cpu()
+    want_s = orow['scores']
+    scale = want_s.masked_fill(~legal, 0).abs().flatten(-2).amax(-1).clamp_min(1e-300)
+    err = ((got_s - want_s).abs().masked_fill(~legal, 0).flatten(-2).amax(-1) / scale)
+    print(f"scores: max err / row scale {float(err.max()):.2e}; gpu executed {int(stats[0])}, "
+          f"oracle executed {int(ostats[0])} of {int(ostats[1])}", flush=True)
+    assert float(err.max()) < 1e-4
+    assert (got_s.masked_fill(legal, 0) == -1e30).masked_fill(legal, True).all()
+    pool = rows['pool'].cpu()
+    assert torch.equal(pool[..., :16].long(), orow['remove'])
+    assert torch.equal(pool[..., 16:48].long(), orow['add'])
+    ties = _near_tie(want_s, legal)
+    ex_g = rows['executed'].cpu().bool()
+    same = (ex_g == orow['executed']) & (~ex_g | (rows['argmax'].cpu().long() == orow['argmax']))
+    print(f"decisions: {int(same.sum())}/{same.numel()} identical, {int(ties.sum())} near-tie rows", flush=True)
+    assert bool((same | ties).all())
+    got_mask = mask.cpu()
+    hs = torch.tensor(HEADS)
+    rows_equal = (got_mask[hs] == want_mask[hs]).all(-1)
+    assert bool((rows_equal | ties).all())
+    others = [i for i in range(12) if i not in HEADS]
+    assert torch.equal(got_mask[others], m0[others]) and torch.equal(ids.cpu()[others], ids0.cpu()[others])
+    # LUT of every corrected row: own first, exactly the new mask, descending risk
+    got_ids = ids.cpu()
+    assert torch.equal(ref.mask_from_ids(got_ids, x.pages), got_mask)
+    assert (got_ids[..., 0] == x.own).all()
+    rk = risk.cpu().gather(-1, got_ids[..., 1:].long())
+    assert (rk[..., :-1] >= rk[..., 1:]).all()
+    # quotas survive the swaps
+    assert (got_mask[..., x.pages - 72:].sum(-1) == a[:, None]).all()
+    assert (got_mask[..., :24]).all()
+
+
+def test_route_full_pset_end_to_end(device):
+    """route(..., full_pset=heads) against the oracle chain risk (fp64) ->
+    quota mask -> Full_Pset, on rows that are not near ties at either step."""
+    x, w, a, n = inputs()
+    g, reader, enc = gpu_encoding(x, w, device)
+    ids, mask, risk, stats = route(g.q, g.summary, g.theta, tier='intersection', own=g.own, current_slots=a, n=n,
+                                   full_pset=HEADS, encoding=enc, reader=reader)
+    torch.cuda.synchronize()
+    pr = ref.probes(x.q)
+    z = ref.route_logits(pr, x.summary.keys)
+    r64 = ref.risk(pr, ref.route_logits(pr, x.summary.keys, torch.float64), x.summary.stats, x.theta,
+                   dtype=torch.float64)
+    m0 = ref.quota_mask(r64, x.own, a, n)
+    enc_o = dict(co=enc.co.cpu(), A=enc.A.cpu(), mean=enc.mean.cpu(), detail=enc.detail.cpu())
+    want, orow, _ = opset.correct(pr.bfloat16().float(), z, r64.float(), m0, x.own, enc_o, w['wq'], HEADS)
+    P = x.pages
+    hist = r64.clone()
+    hist[..., :24] = -math.inf
+    hist[..., P - 72:] = -math.inf
+    cur = r64.clone()
+    cur[..., :P - 72] = -math.inf
+    cur.scatter_(-1, x.own[..., None], math.inf)
+    route_ties = ref.near_tie_rows(hist, (n - a)[:, None].expand_as(x.own)) | \
+        ref.near_tie_rows(cur, a[:, None].expand_as(x.own))
+    hs = torch.tensor(HEADS)
+    ties = route_ties.clone()
+    ties[hs] |= _near_tie(orow['scores'], orow['legal'].reshape(len(HEADS), 72, 16, 32))
+    same = (mask.cpu() == want).all(-1)
+    print(f"end to end: {int(same.sum())}/{same.numel()} masks identical, {int(ties.sum())} near-tie rows, "
+          f"executed {int(stats[0])}/{int(stats[1])}", flush=True)
+    assert bool((same | ties).all())
+    assert int(stats[1]) == len(HEADS) * 72 and int(stats[2]) == 0
