@@ -1,17 +1,25 @@
-"""Benchmark: one page-sparse attention call (route + fused attention) on one
-MI355X, at the full-window base workload: 12 heads x 4608 queries x d128 bf16
-against a 432-page (27648-token) window, 64 exact pages per query block
-(24 anchors + own + 39 by risk), every other page compensated from summaries.
+"""Benchmark: one page-sparse attention call on one MI355X.
 
-Prints ONE JSON line.  `value` is milliseconds per call (lower is better) with
-all inputs resident in HBM.  The roofline object covers the dominant kernel
-(the fused exact+compensation+merge kernel), timed with HIP events on the
-stream it is launched on.  cpu_baseline times the CPU oracle (a torch
-restatement of the reference's CPU path) on a bounded sample of the same call.
+Headline workload: the full-window base tier, 12 heads x 4608 queries x d128
+bf16 against a 432-page (27648-token) window with 64 exact pages per 64-query
+block (24 anchors + own + 39 by risk) and every other page compensated from
+its summary.  One step = route + rep values + fused attention over one call's
+inputs, all resident in HBM.
+
+Also measured in the same run:
+* the intersection tier: 24 anchors + A current + B history pages per head,
+  (A, B) from a seeded per-(step, layer, head) quota table;
+* the same with the Full_Pset swap correction on heads {3, 4, 9}, plus the
+  encodings of the 72 current pages x 12 heads that a denoise step refreshes;
+* torch's dense scaled_dot_product_attention over the whole window.
+
+Prints ONE JSON line; `value` is ms per call (lower is better).  The
+roofline object covers the dominant kernel (fused exact + compensation +
+merge), timed with HIP events on the stream it runs on.  cpu_baseline times
+the CPU oracle on a bounded sample of the headline call.
 """
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -22,6 +30,7 @@ sys.path.insert(0, ROOT)
 METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+PSET_HEADS = (3, 4, 9)
 
 
 def parse():
@@ -33,6 +42,7 @@ def parse():
     ap.add_argument("--precise-av", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the intersection / Full_Pset lines")
     ap.add_argument("--cpu-sample-blocks", type=int, default=4)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (scales rocprof FETCH/WRITE_SIZE)")
@@ -52,6 +62,8 @@ def calibrate_copy(mib):
 
 
 def time_loop(fn, iters, stream):
+    """Average ms of `fn` over `iters` back-to-back launches, HIP events on
+    the stream the work is enqueued on."""
     import torch
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
@@ -73,7 +85,7 @@ def main():
         calibrate_copy(args.calibrate_copy)
         return
     import torch
-    from streaming_sparse_amd import _lib, workload
+    from streaming_sparse_amd import _lib, pset, workload
     from streaming_sparse_amd.attention import Workspace
     from streaming_sparse_amd.legacy_components import attention, rep_values, kv_strides
     from streaming_sparse_amd.route import route
@@ -89,7 +101,6 @@ def main():
     C = P * 15 // 100
     ws = Workspace()
     stream = torch.cuda.current_stream(dev)
-
     basis = g.basis.to(torch.bfloat16).contiguous()   # the caller keeps the basis bf16-rounded
 
     def step():
@@ -99,7 +110,6 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
     # timed region: exactly `steps` calls, synchronized on both sides
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -125,16 +135,11 @@ def main():
                                    g.summary.head_pages, P, C, tok, head, flags, _lib.stream_handle(dev)),
                    "ssa_attention")
 
-    def route_only():
-        route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
-
-    def rep_only():
-        rep_values(g.summary, basis, P, vrep)
-
     iters = max(10, args.steps)
     attn_ms = time_loop(attn_only, iters, stream)
-    route_ms = time_loop(route_only, iters, stream)
-    rep_ms = time_loop(rep_only, iters, stream)
+    route_ms = time_loop(lambda: route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False),
+                         iters, stream)
+    rep_ms = time_loop(lambda: rep_values(g.summary, basis, P, vrep), iters, stream)
 
     dense_ms = None
     if not args.no_dense:
@@ -145,6 +150,8 @@ def main():
         for _ in range(3):
             dense()
         dense_ms = time_loop(dense, max(5, iters // 5), stream)
+
+    extra = None if args.no_extra else intersection_lines(args, dense_ms, iters)
 
     # algorithmic work of the fused kernel (exact + compensation), per call
     exact_flop = 4.0 * N * H * D * 64 * C
@@ -185,10 +192,69 @@ def main():
                      "page_gather_gb": round(gather_bytes / 1e9, 3),
                      "page_gather_GBps": round(gather_gbs, 1),
                      "page_gather_frac_of_hbm_peak": round(gather_gbs / PEAK_HBM_GBS, 4)},
+        "extra": extra,
         "cpu_baseline": cpu,
         "input_gen_s": round(gen_s, 2),
     }
     print(json.dumps(line), flush=True)
+
+
+def intersection_lines(args, dense_ms, iters):
+    """The intersection tier (per-head A/B quotas, layer 3 step 0 of a seeded
+    table) and the same call with Full_Pset on heads {3,4,9} plus the
+    current-page encodings."""
+    import torch
+    from streaming_sparse_amd import pset, workload
+    from streaming_sparse_amd.attention import Workspace
+    from streaming_sparse_amd.legacy_components import attention
+    from streaming_sparse_amd.route import route
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    x = workload.make_call(cfg=2, frames=args.frames)
+    g = x.to(dev)
+    P = x.pages
+    tab = workload.quota_table(2)
+    a = tab[0, 3, :, 0]
+    n = int(tab[0, 3, 0].sum())
+    ac = a.to(dev)
+    basis = g.basis.to(torch.bfloat16).contiguous()
+    ws = Workspace()
+    reader = pset.Reader(workload.reader_weights(), dev)
+    enc = pset.encode(g.summary, basis, reader)
+
+    def plain():
+        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
+                             want_mask=False)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws)
+
+    def corrected():
+        pset.encode(g.summary, basis, reader, out=enc, first=P - 72, pages=72)
+        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
+                             full_pset=PSET_HEADS, encoding=enc, reader=reader)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws)
+
+    out = {}
+    for name, fn in (("intersection", plain), ("intersection_full_pset", corrected)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        out[name + "_ms"] = round(time_loop(fn, iters, stream), 4)
+    out["intersection_exact_pages"] = 24 + n
+    out["intersection_current_quota_A"] = a.tolist()
+    out["ratio_intersection_vs_dense"] = None if dense_ms is None else round(out["intersection_ms"] / dense_ms, 4)
+    out["ratio_full_pset_vs_dense"] = None if dense_ms is None else \
+        round(out["intersection_full_pset_ms"] / dense_ms, 4)
+    route_i = lambda: route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
+                            want_mask=True)
+    out["route_intersection_ms"] = round(time_loop(route_i, iters, stream), 4)
+    ids, mask, risk, _ = route_i()
+    out["pset_correction_ms"] = round(time_loop(
+        lambda: pset.correct(g.q, g.summary, enc, reader, risk, mask, ids, None, PSET_HEADS, ws), iters, stream), 4)
+    out["encode_current_72x12_ms"] = round(time_loop(
+        lambda: pset.encode(g.summary, basis, reader, out=enc, first=P - 72, pages=72), iters, stream), 4)
+    out["full_pset_heads"] = list(PSET_HEADS)
+    return out
 
 
 def cpu_baseline(x, count, blocks):

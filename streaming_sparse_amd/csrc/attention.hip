@@ -9,28 +9,39 @@
 //          detail_pa) . basis^T; log-mass lt = mx + log2(den) + 4      -> (O_t, lt)
 //   merge: rho = 1/(1+2^(le-lt)); out = (1-rho) O_e + rho O_t
 // which equals ONE softmax over the union of the exact tokens (logit s,
-// value v) and the unselected reps (logit z + 4, value mean_p + code_r .
-// basis^T).  This kernel runs that union softmax: it walks "units" of 64 keys
-// -- first the C exact pages (rows of the resident [L,H,D] cache), then the
-// rep tiles of 16 pages x 4 reps whose pages are not all selected -- with a
-// single running max/sum and one [64 x 128] accumulator.  Rep values are
+// value v) and the unselected reps (logit z + 4 in log2 units, value
+// mean_p + code_r . basis^T).  This kernel runs that union softmax: it walks
+// "units" of 64 keys -- first the C exact pages (rows of the resident
+// [L,H,D] cache), then the rep tiles of 16 pages x 4 reps whose pages are not
+// all selected -- with one running max/sum per query.  Rep values are
 // pre-projected by rep_values_kernel (bf16 rows, like the V rows of a page).
 //
-// Layout per workgroup (2 waves, 64 queries of one head):
-//   wave w owns queries 32w..32w+31.  S^T = K . Q^T and O^T = V^T . P^T use
-//   v_mfma_f32_32x32x16_bf16 so each lane holds a single query (lane % 32):
-//   the softmax state is lane-local.  K is staged in LDS row-major, V is
-//   transposed to [dim][key] in LDS with keys permuted (bits 2<->3 swapped) so
-//   each lane's 8 P^T values in MFMA k-order are 16 contiguous bytes.
+// Workgroup: 4 waves, 64 queries of one head.  Wave w: pair w/2 takes keys
+// 32*pair..32*pair+31 of every unit, queries 32*(w%2)..+31.  Per unit:
+//   * K and V rows go straight from memory into a double-buffered LDS ring
+//     (16-byte global->LDS loads, no register staging); the next unit's
+//     loads are in flight while the current one computes;
+//   * S^T = K . Q^T on v_mfma_f32_32x32x16_bf16: a lane holds one query, so
+//     the softmax state is lane-local;
+//   * O^T += V^T . P^T with V^T read by the LDS transpose read
+//     (ds_read_b64_tr_b16) from row-major V;
+//   * the O/l rescale runs only when some lane's running max grows.
+// The two key halves are merged through LDS at the end.
 #include "common.h"
 
 using namespace ssa;
 
 namespace {
 
-constexpr int kThreads = 128;
+constexpr int kThreads = 256;
 constexpr int kMaxCount = 512;
 constexpr int kMaxRepTiles = 32;   // pages <= 512 -> ceil(P/16) <= 32
+constexpr int kBuf = 64 * 256;     // one 64-row x 128-dim bf16 tile (K or V)
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
 
 struct AttnParams {
   const uint16_t* q;
@@ -46,29 +57,31 @@ struct AttnParams {
   float scale_log2;            // log2(e) / sqrt(D)
 };
 
-struct Smem {
-  alignas(16) uint8_t kbuf[64 * 256];
-  alignas(16) uint8_t vt[128 * 128];
-  int units[kMaxCount + kMaxRepTiles];
-  uint32_t maskw[16];
-  int nunits;
-};
-
-struct Stage {
-  u32x4 k[8];
-  u32x4 v[8];
-};
-
+// K tile: 16-byte chunk c of row r at chunk c ^ (r & 15).
 __device__ __forceinline__ int k_off(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
-__device__ __forceinline__ int vt_off(int d, int chunk) {
-  return d * 128 + ((chunk ^ ((d & 7) ^ ((d >> 3) & 7))) << 4);
-}
-// Physical position of key kappa inside a unit's transposed V row.
-__device__ __forceinline__ int key_pos(int kappa) {
-  return (kappa & ~12) | ((kappa & 4) << 1) | ((kappa & 8) >> 1);
+// V tile: chunk c of row r at chunk c ^ vswz(r & 3); keeps the transpose reads
+// of 4 rows x 16 or 32 dims on distinct banks.
+__device__ __forceinline__ int vswz(int row) { return (0xEA40 >> (4 * (row & 3))) & 15; }   // 0, 4, 10, 14
+__device__ __forceinline__ int v_off(int row, int chunk) { return row * 256 + ((chunk ^ vswz(row)) << 4); }
+
+// s_waitcnt vmcnt(0) (expcnt/lgkmcnt left at their maxima) as the intrinsic,
+// so the compiler's own wait-count tracking sees it.
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// 16-byte global->LDS load of one wave: lane l's 16 bytes at gptr land at
+// lds + 16*l.  Issued from inline asm so the compiler does not fence later
+// LDS reads of the other ring slot on it; wait_loads() before the barrier
+// orders it.
+__device__ __forceinline__ void dma16(const void* gptr, lds_u8* lds) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(base)
+               : "memory", "m0");
 }
 
-__device__ __forceinline__ void load_unit(const AttnParams& p, int e, int h, int tid, Stage& st) {
+// Enqueue the global->LDS loads of unit e (page e >= 0, rep tile -1-e < 0):
+// wave w loads rows 16w..16w+15 of K and of V, 1 KB per instruction.
+__device__ __forceinline__ void issue_unit(const AttnParams& p, int e, int h, int wave, int lane, lds_u8* kbuf,
+                                           lds_u8* vbuf) {
   const uint16_t* kb;
   const uint16_t* vb;
   long long rs;
@@ -82,117 +95,93 @@ __device__ __forceinline__ void load_unit(const AttnParams& p, int e, int h, int
     kb = p.rk + ((long long)h * p.HP * 4 + rt * 64) * kHeadDim;
     vb = p.rv + ((long long)h * p.HPV * 4 + rt * 64) * kHeadDim;
     rs = kHeadDim;
-    // rows of pages >= P are re-read from the last valid rep (masked later)
+    // rows of pages >= P re-read the last valid rep (masked in compute)
     last = min(63, p.P * 4 - rt * 64 - 1);
   }
-  const int c = tid & 15, r0 = tid >> 4;
+  const int pc = lane & 15;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = min(8 * i + r0, last);
-    st.k[i] = ldg16(kb + row * rs + c * 8);
-  }
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-#pragma unroll
-    for (int e4 = 0; e4 < 4; ++e4) {
-      const int row = min(4 * (8 * j + r0) + e4, last);
-      st.v[4 * j + e4] = ldg16(vb + row * rs + c * 8);
-    }
+  for (int jj = 0; jj < 4; ++jj) {
+    const int j = 4 * wave + jj;
+    const int row = 4 * j + (lane >> 4);
+    const long long src = (long long)min(row, last) * rs;
+    dma16(kb + src + 8 * (pc ^ (row & 15)), kbuf + j * 1024);
+    dma16(vb + src + 8 * (pc ^ vswz(row)), vbuf + j * 1024);
   }
 }
 
-__device__ __forceinline__ void store_unit(Smem& s, int tid, const Stage& st) {
-  const int c = tid & 15, r0 = tid >> 4;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 8 * i + r0;
-    *reinterpret_cast<u32x4*>(s.kbuf + k_off(row, c)) = st.k[i];
-  }
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int g = 8 * j + r0;
-    const int pos = key_pos(4 * g);
-    const int cc = pos >> 3, half = (pos >> 2) & 1;
-    const u32x4 a = st.v[4 * j + 0], b = st.v[4 * j + 1], c2 = st.v[4 * j + 2], d = st.v[4 * j + 3];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int w = i >> 1;
-      const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
-      const uint32_t lo = __builtin_amdgcn_perm(b[w], a[w], sel);
-      const uint32_t hi = __builtin_amdgcn_perm(d[w], c2[w], sel);
-      const int dim = 8 * c + i;
-      *reinterpret_cast<u32x2*>(s.vt + vt_off(dim, cc) + half * 8) = u32x2{lo, hi};
-    }
-  }
+// V^T operand for O^T += V^T P^T: dims 32*dt + lane%32, keys (MFMA k order)
+// 16*ks + 8*(e/4) + 4*hh + e%4 of this pair's half, from two transpose reads.
+__device__ __forceinline__ u32x4 v_operand(const lds_u8* vbuf, int pair, int ks, int dt, int lane) {
+  const int g = lane >> 4, i = lane & 15, hh = g >> 1;
+  const int chunk = 4 * dt + 2 * (g & 1) + ((i & 3) >> 1);
+  const int half = (i & 1) * 8;
+  const int row0 = 32 * pair + 16 * ks + 4 * hh + (i >> 2);
+  const bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vbuf + v_off(row0, chunk) + half));
+  const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vbuf + v_off(row0 + 8, chunk) + half));
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return u32x4{ua[0], ua[1], ub[0], ub[1]};
 }
 
 template <bool PRECISE>
-__device__ __forceinline__ void compute_unit(const Smem& s, const AttnParams& p, int e, int lane,
-                                             const u32x4 (&qop)[8], float& m, float& l, f32x16 (&O)[4]) {
+__device__ __forceinline__ void compute_unit(const lds_u8* kbuf, const lds_u8* vbuf, const AttnParams& p, int e,
+                                             const uint32_t* maskw, int pair, int lane, const u32x4 (&qop)[8],
+                                             float& m, float& l, f32x16 (&O)[4]) {
   const int r = lane & 31, hh = lane >> 5;
-  f32x16 S0 = {}, S1 = {};
+  f32x16 S = {};
 #pragma unroll
   for (int st = 0; st < 8; ++st) {
-    const int c = 2 * st + hh;
-    const u32x4 a0 = *reinterpret_cast<const u32x4*>(s.kbuf + k_off(r, c));
-    const u32x4 a1 = *reinterpret_cast<const u32x4*>(s.kbuf + k_off(32 + r, c));
-    S0 = mfma32(a0, qop[st], S0);
-    S1 = mfma32(a1, qop[st], S1);
+    const u32x4 a = *(lds_u32x4*)(kbuf + k_off(32 * pair + r, 2 * st + hh));
+    S = mfma32(a, qop[st], S);
   }
-  const float bias = e < 0 ? 4.0f : 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    S0[i] = S0[i] * p.scale_log2 + bias;
-    S1[i] = S1[i] * p.scale_log2 + bias;
-  }
+  // S[i]: key 32*pair + 8*(i/4) + 4*hh + i%4 of the unit, query lane%32
+  float bias = 0.0f;
   if (e < 0) {
+    bias = 4.0f;
     const int rt = -1 - e;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int page0 = 16 * rt + 2 * j + hh, page1 = page0 + 8;
-      const bool m0 = page0 >= p.P || ((s.maskw[page0 >> 5] >> (page0 & 31)) & 1u);
-      const bool m1 = page1 >= p.P || ((s.maskw[page1 >> 5] >> (page1 & 31)) & 1u);
+      const int page = 16 * rt + 8 * pair + 2 * j + hh;
+      const bool drop = page >= p.P || ((maskw[page >> 5] >> (page & 31)) & 1u);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (m0) S0[4 * j + i] = -INFINITY;
-        if (m1) S1[4 * j + i] = -INFINITY;
-      }
+      for (int i = 0; i < 4; ++i)
+        if (drop) S[4 * j + i] = -INFINITY;
     }
   }
-  float mloc = fmaxf(S0[0], S1[0]);
+  float mx = fmaxf(S[0], S[1]);
 #pragma unroll
-  for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, fmaxf(S0[i], S1[i]));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-  const float mnew = fmaxf(m, mloc);
-  const float muse = mnew == -INFINITY ? 0.0f : mnew;
-  const float alpha = __builtin_amdgcn_exp2f(m - muse);
+  for (int i = 2; i < 16; ++i) mx = fmaxf(mx, S[i]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mloc = mx * p.scale_log2 + bias;     // -inf stays -inf
+  if (__any(mloc > m)) {
+    const float mnew = fmaxf(m, mloc);
+    const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) O[dt] *= alpha;
+    m = mnew;
+  }
+  const float nb = bias - (m == -INFINITY ? 0.0f : m);
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    S0[i] = __builtin_amdgcn_exp2f(S0[i] - muse);
-    S1[i] = __builtin_amdgcn_exp2f(S1[i] - muse);
-    sum += S0[i] + S1[i];
+    S[i] = __builtin_amdgcn_exp2f(fmaf(S[i], p.scale_log2, nb));
+    sum += S[i];
   }
-  l = l * alpha + sum;
-  m = mnew;
+  l += sum;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) O[dt] *= alpha;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const f32x16& x = (ks >> 1) ? S1 : S0;
-    const int o = 8 * (ks & 1);
-    const u32x4 pb = {pack_bf16(x[o + 0], x[o + 1]), pack_bf16(x[o + 2], x[o + 3]), pack_bf16(x[o + 4], x[o + 5]),
-                      pack_bf16(x[o + 6], x[o + 7])};
+  for (int ks = 0; ks < 2; ++ks) {
+    const int o = 8 * ks;
+    const u32x4 pb = {pack_bf16(S[o + 0], S[o + 1]), pack_bf16(S[o + 2], S[o + 3]), pack_bf16(S[o + 4], S[o + 5]),
+                      pack_bf16(S[o + 6], S[o + 7])};
     u32x4 pl = {};
     if (PRECISE) {
 #pragma unroll
       for (int w = 0; w < 4; ++w)
-        pl[w] = pack_bf16(x[o + 2 * w] - bf16_lo(pb[w]), x[o + 2 * w + 1] - bf16_hi(pb[w]));
+        pl[w] = pack_bf16(S[o + 2 * w] - bf16_lo(pb[w]), S[o + 2 * w + 1] - bf16_hi(pb[w]));
     }
-    const int cc = 2 * ks + hh;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const u32x4 va = *reinterpret_cast<const u32x4*>(s.vt + vt_off(32 * dt + r, cc));
+      const u32x4 va = v_operand(vbuf, pair, ks, dt, lane);
       O[dt] = mfma32(va, pb, O[dt]);
       if (PRECISE) O[dt] = mfma32(va, pl, O[dt]);
     }
@@ -201,17 +190,23 @@ __device__ __forceinline__ void compute_unit(const Smem& s, const AttnParams& p,
 
 template <bool PRECISE>
 __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
-  __shared__ Smem s;
+  __shared__ alignas(16) uint8_t kv0[2 * kBuf];   // ring slot 0: K | V
+  __shared__ alignas(16) uint8_t kv1[2 * kBuf];   // ring slot 1: K | V
+  __shared__ int units[kMaxCount + kMaxRepTiles];
+  __shared__ uint32_t maskw[16];
+  __shared__ float xm[2][64], xl[2][64];
+  __shared__ int nunits_s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pair = wave >> 1, qw = wave & 1;
   const int work = xcd_remap(blockIdx.x, p.H * p.T);
   const int h = work / p.T, t = work % p.T;
-  if (tid < 16) s.maskw[tid] = 0u;
+  if (tid < 16) maskw[tid] = 0u;
   __syncthreads();
   const int32_t* ids = p.ids + ((long long)h * p.T + t) * p.C;
   for (int i = tid; i < p.C; i += kThreads) {
     const int pg = min(max(ids[i], 0), p.P - 1);
-    s.units[i] = pg;
-    atomicOr(&s.maskw[pg >> 5], 1u << (pg & 31));
+    units[i] = pg;
+    atomicOr(&maskw[pg >> 5], 1u << (pg & 31));
   }
   __syncthreads();
   if (wave == 0) {
@@ -219,48 +214,76 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
     bool live = false;
     if (lane < R) {
       const int p0 = lane * 16;
-      const uint32_t word = (s.maskw[p0 >> 5] >> (p0 & 31)) & 0xffffu;
+      const uint32_t word = (maskw[p0 >> 5] >> (p0 & 31)) & 0xffffu;
       const int valid = min(16, p.P - p0);
       const uint32_t vmask = valid >= 16 ? 0xffffu : ((1u << valid) - 1u);
       live = (~word & vmask) != 0u;
     }
     const unsigned long long bal = __ballot(live);
-    if (live) s.units[p.C + __popcll(bal & ((1ull << lane) - 1ull))] = -1 - lane;
-    if (lane == 0) s.nunits = p.C + __popcll(bal);
+    if (live) units[p.C + __popcll(bal & ((1ull << lane) - 1ull))] = -1 - lane;
+    if (lane == 0) nunits_s = p.C + __popcll(bal);
   }
   // query operand: lane's query row, dims 16*st + 8*hh + [0,8)
   const int r = lane & 31, hh = lane >> 5;
-  const long long qrow = (long long)(t * 64 + wave * 32 + r);
+  const long long qrow = (long long)(t * 64 + qw * 32 + r);
   u32x4 qop[8];
   const uint16_t* qp = p.q + qrow * p.q_tok + (long long)h * p.q_head + 8 * hh;
 #pragma unroll
   for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st);
   __syncthreads();
-  const int nunits = s.nunits;
+  const int nunits = nunits_s;
+  lds_u8* k0 = (lds_u8*)kv0;
+  lds_u8* v0 = (lds_u8*)kv0 + kBuf;
+  lds_u8* k1 = (lds_u8*)kv1;
+  lds_u8* v1 = (lds_u8*)kv1 + kBuf;
 
   float m = -INFINITY, l = 0.0f;
   f32x16 O[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
-  Stage st;
-  load_unit(p, s.units[0], h, tid, st);
-  for (int u = 0; u < nunits; ++u) {
-    const int e = s.units[u];
+  issue_unit(p, units[0], h, wave, lane, k0, v0);
+  wait_loads();
+  __syncthreads();
+  for (int u = 0; u < nunits; u += 2) {
+    if (u + 1 < nunits) issue_unit(p, units[u + 1], h, wave, lane, k1, v1);
+    compute_unit<PRECISE>(k0, v0, p, units[u], maskw, pair, lane, qop, m, l, O);
+    wait_loads();
     __syncthreads();
-    store_unit(s, tid, st);
+    if (u + 1 >= nunits) break;
+    if (u + 2 < nunits) issue_unit(p, units[u + 2], h, wave, lane, k0, v0);
+    compute_unit<PRECISE>(k1, v1, p, units[u + 1], maskw, pair, lane, qop, m, l, O);
+    wait_loads();
     __syncthreads();
-    if (u + 1 < nunits) load_unit(p, s.units[u + 1], h, tid, st);
-    compute_unit<PRECISE>(s, p, e, lane, qop, m, l, O);
   }
-  const float lt = l + __shfl_xor(l, 32);
-  const float inv = 1.0f / lt;
+  // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS
+  l += __shfl_xor(l, 32);
+  float* xo = reinterpret_cast<float*>(kv0);     // [qw][64 lanes][64] fp32 = 32 KB
+  if (pair == 1) {
+    float* d = xo + (qw * 64 + lane) * 64;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) d[16 * dt + i] = O[dt][i];
+    xm[qw][lane] = m;
+    xl[qw][lane] = l;
+  }
+  __syncthreads();
+  if (pair == 1) return;
+  const float m1 = xm[qw][lane], l1 = xl[qw][lane];
+  const float mt = fmaxf(m, m1);
+  const float mu = mt == -INFINITY ? 0.0f : mt;
+  const float a0 = __builtin_amdgcn_exp2f(m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+  const float inv = 1.0f / (l * a0 + l1 * a1);
+  const float* d = xo + (qw * 64 + lane) * 64;
   uint16_t* op = p.out + qrow * p.q_tok + (long long)h * p.q_head + 4 * hh;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const u32x2 w = {pack_bf16(O[dt][4 * j] * inv, O[dt][4 * j + 1] * inv),
-                       pack_bf16(O[dt][4 * j + 2] * inv, O[dt][4 * j + 3] * inv)};
+      float o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = (O[dt][4 * j + c] * a0 + d[16 * dt + 4 * j + c] * a1) * inv;
+      const u32x2 w = {pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
       *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * j) = w;
     }
   }

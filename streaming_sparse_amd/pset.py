@@ -116,7 +116,13 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, mask,
     head_list = [int(i) for i in heads]
     if not head_list or len(set(head_list)) != len(head_list) or min(head_list) < 0 or max(head_list) >= h:
         raise ValueError(f"full_pset heads must be distinct ids in [0,{h})")
-    hs = torch.tensor(head_list, dtype=torch.int32).to(dev)
+    key = ('pset_heads', tuple(head_list), torch.device(dev), torch.int32)
+    if workspace is not None and key in workspace.entries:
+        hs = workspace.entries[key]
+    else:
+        hs = torch.tensor(head_list, dtype=torch.int32).to(dev)
+        if workspace is not None:
+            workspace.entries[key] = hs
     n = hs.numel()
     hp = _summary_ok(summary)
     if encoding.coef.shape[1] < p:
@@ -141,7 +147,7 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, mask,
         _lib.ptr(risk), _lib.ptr(mask_u8), _lib.ptr(ids), _lib.ptr(ow), _lib.ptr(hs), n, _lib.ptr(cand),
         _lib.ptr(rows), _lib.ptr(pool), _lib.ptr(gain), _lib.ptr(info), _lib.ptr(scores), h, t, p,
         ids.shape[-1], _lib.stream_handle(dev)), "ssa_pset")
-    stats = torch.stack((info[..., 0].sum(dtype=torch.int64), torch.tensor(n * t, device=dev),
-                         info[..., 2].sum(dtype=torch.int64)))
+    stats = info.sum((0, 1), dtype=torch.int64)
+    stats[1] = n * t
     return stats, dict(gain=gain, executed=info[..., 0], argmax=info[..., 1], nonfinite=info[..., 2],
                        scores=scores, pool=pool)
