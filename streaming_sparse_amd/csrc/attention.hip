@@ -68,44 +68,61 @@ __device__ __forceinline__ int v_off(int row, int chunk) { return row * 256 + ((
 // so the compiler's own wait-count tracking sees it.
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// 16-byte global->LDS load of one wave: lane l's 16 bytes at gptr land at
-// lds + 16*l.  Issued from inline asm so the compiler does not fence later
-// LDS reads of the other ring slot on it; wait_loads() before the barrier
-// orders it.
-__device__ __forceinline__ void dma16(const void* gptr, lds_u8* lds) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(base)
+// 16-byte global->LDS load of one wave: lane l's 16 bytes at base + off
+// (bytes; base wave-uniform in SGPRs, off per lane) land at lds + 16*l.
+// Issued from inline asm so the compiler does not fence later LDS reads of
+// the other ring slot on it; wait_loads() before the barrier orders it.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 
-// Enqueue the global->LDS loads of unit e (page e >= 0, rep tile -1-e < 0):
-// wave w loads rows 16w..16w+15 of K and of V, 1 KB per instruction.
-__device__ __forceinline__ void issue_unit(const AttnParams& p, int e, int h, int wave, int lane, lds_u8* kbuf,
-                                           lds_u8* vbuf) {
+// Per-lane byte offsets of this wave's 4 K and 4 V rows of a unit (wave w
+// loads rows 16w..16w+15, 1 KB per instruction) for a row stride `rs`
+// (elements) and rows clamped to `last`.
+struct UnitOffsets {
+  uint32_t k[4], v[4];
+};
+
+__device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long long rs, int last) {
+  UnitOffsets o;
+  const int pc = lane & 15;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int row = 16 * wave + 4 * jj + (lane >> 4);
+    const uint32_t r = (uint32_t)(min(row, last) * rs);
+    o.k[jj] = 2u * (r + 8u * (uint32_t)(pc ^ (row & 15)));
+    o.v[jj] = 2u * (r + 8u * (uint32_t)(pc ^ vswz(row)));
+  }
+  return o;
+}
+
+// Enqueue the global->LDS loads of unit e (page e >= 0, rep tile -1-e < 0).
+__device__ __forceinline__ void issue_unit(const AttnParams& p, int e, int h, int wave, int lane,
+                                           const UnitOffsets& page_off, const UnitOffsets& rep_off,
+                                           lds_u8* kbuf, lds_u8* vbuf) {
   const uint16_t* kb;
   const uint16_t* vb;
-  long long rs;
-  int last = 63;
+  UnitOffsets o;
   if (e >= 0) {
-    kb = p.k + (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head;
-    vb = p.v + (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head;
-    rs = p.kv_tok;
+    const long long b = (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head;
+    kb = p.k + b;
+    vb = p.v + b;
+    o = page_off;
   } else {
     const int rt = -1 - e;
     kb = p.rk + ((long long)h * p.HP * 4 + rt * 64) * kHeadDim;
     vb = p.rv + ((long long)h * p.HPV * 4 + rt * 64) * kHeadDim;
-    rs = kHeadDim;
     // rows of pages >= P re-read the last valid rep (masked in compute)
-    last = min(63, p.P * 4 - rt * 64 - 1);
+    const int last = p.P * 4 - rt * 64 - 1;
+    o = last >= 63 ? rep_off : unit_offsets(wave, lane, kHeadDim, last);
   }
-  const int pc = lane & 15;
+  const uint32_t kl = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)kbuf + wave * 4096);
+  const uint32_t vl = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)vbuf + wave * 4096);
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
-    const int j = 4 * wave + jj;
-    const int row = 4 * j + (lane >> 4);
-    const long long src = (long long)min(row, last) * rs;
-    dma16(kb + src + 8 * (pc ^ (row & 15)), kbuf + j * 1024);
-    dma16(vb + src + 8 * (pc ^ vswz(row)), vbuf + j * 1024);
+    dma16(kb, o.k[jj], kl + jj * 1024);
+    dma16(vb, o.v[jj], vl + jj * 1024);
   }
 }
 
@@ -147,9 +164,10 @@ __device__ __forceinline__ void compute_unit(const lds_u8* kbuf, const lds_u8* v
         if (drop) S[4 * j + i] = -INFINITY;
     }
   }
-  float mx = fmaxf(S[0], S[1]);
+  float mx = S[0];
 #pragma unroll
-  for (int i = 2; i < 16; ++i) mx = fmaxf(mx, S[i]);
+  for (int i = 1; i < 15; i += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, S[i]), S[i + 1]);
+  mx = fmaxf(mx, S[15]);
   mx = fmaxf(mx, __shfl_xor(mx, 32));
   const float mloc = mx * p.scale_log2 + bias;     // -inf stays -inf
   if (__any(mloc > m)) {
@@ -241,16 +259,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   f32x16 O[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
-  issue_unit(p, units[0], h, wave, lane, k0, v0);
+  const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63);
+  const UnitOffsets rep_off = unit_offsets(wave, lane, kHeadDim, 63);
+  issue_unit(p, __builtin_amdgcn_readfirstlane(units[0]), h, wave, lane, page_off, rep_off, k0, v0);
   wait_loads();
   __syncthreads();
   for (int u = 0; u < nunits; u += 2) {
-    if (u + 1 < nunits) issue_unit(p, units[u + 1], h, wave, lane, k1, v1);
+    if (u + 1 < nunits)
+      issue_unit(p, __builtin_amdgcn_readfirstlane(units[u + 1]), h, wave, lane, page_off, rep_off, k1, v1);
     compute_unit<PRECISE>(k0, v0, p, units[u], maskw, pair, lane, qop, m, l, O);
     wait_loads();
     __syncthreads();
     if (u + 1 >= nunits) break;
-    if (u + 2 < nunits) issue_unit(p, units[u + 2], h, wave, lane, k0, v0);
+    if (u + 2 < nunits)
+      issue_unit(p, __builtin_amdgcn_readfirstlane(units[u + 2]), h, wave, lane, page_off, rep_off, k0, v0);
     compute_unit<PRECISE>(k1, v1, p, units[u + 1], maskw, pair, lane, qop, m, l, O);
     wait_loads();
     __syncthreads();

@@ -52,6 +52,7 @@ struct Smem {
   float risk[2][kMaxPages];
   unsigned long long key[2][kMaxPages];
   uint8_t sel[2][kMaxPages];
+  int list[2][kMaxPages];
   float bmax_w[4];
 };
 
@@ -73,6 +74,28 @@ __device__ __forceinline__ void rep_logits(const uint16_t* rkh, int tile, int P,
   S = f32x16{};
 #pragma unroll
   for (int st = 0; st < 8; ++st) S = mfma32(av[st], qop[st], S);
+}
+
+// Descending bitonic sort of 512 keys by the 128 threads of one row group;
+// every thread of the workgroup calls it (both rows sort in lockstep).
+__device__ __forceinline__ void bitonic_desc(unsigned long long* key, int bt) {
+  for (int k = 2; k <= kMaxPages; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int i = bt + 128 * r;                        // pair index 0..255
+        const int lo = 2 * i - (i & (j - 1));              // i with a zero bit inserted at j
+        const int hi = lo + j;
+        const bool desc = (lo & k) == 0;
+        const unsigned long long a = key[lo], c = key[hi];
+        if ((a < c) == desc) {
+          key[lo] = c;
+          key[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
@@ -126,7 +149,8 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
 
   const uint16_t* rkh = p.rk + (long long)h * p.HP * 4 * kHeadDim;
   const int ntiles = (P + 7) >> 3;
-  const float inv_sqrt_d = 1.0f / sqrtf((float)kHeadDim);
+  // logits in log2 units: z2 = q.k * log2(e) / sqrt(D); prob = 2^(z2 - max2) / den
+  const float c2 = kLog2e / sqrtf((float)kHeadDim);
 
   // pass 1: max and sum of exp over all reps, per probe
   float mx = -INFINITY, den = 0.f;
@@ -137,21 +161,22 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int page = tile * 8 + 2 * (i >> 2) + hh;
-      S[i] = page < P ? S[i] * inv_sqrt_d : -INFINITY;
+      S[i] = page < P ? S[i] * c2 : -INFINITY;
       tmax = fmaxf(tmax, S[i]);
     }
     const float mnew = fmaxf(mx, tmax);
     const float muse = mnew == -INFINITY ? 0.f : mnew;
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc += expf(S[i] - muse);
-    den = (mx == -INFINITY ? 0.f : den * expf(mx - mnew)) + acc;
+    for (int i = 0; i < 16; ++i) acc += __builtin_amdgcn_exp2f(S[i] - muse);
+    den = den * __builtin_amdgcn_exp2f(mx - muse) + acc;
     mx = mnew;
   }
   {
     const float omx = __shfl_xor(mx, 32), oden = __shfl_xor(den, 32);
     const float mm = fmaxf(mx, omx);
-    den = (mx == -INFINITY ? 0.f : den * expf(mx - mm)) + (omx == -INFINITY ? 0.f : oden * expf(omx - mm));
+    const float mu = mm == -INFINITY ? 0.f : mm;
+    den = den * __builtin_amdgcn_exp2f(mx - mu) + oden * __builtin_amdgcn_exp2f(omx - mu);
     mx = mm;
     if (hh == 0) {
       s.part[wave][pi][0] = mx;
@@ -164,10 +189,8 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   for (int w = 0; w < 4; ++w) MX = fmaxf(MX, s.part[w][pi][0]);
   float DEN = 0.f;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float wm = s.part[w][pi][0];
-    if (wm != -INFINITY) DEN += s.part[w][pi][1] * expf(wm - MX);
-  }
+  for (int w = 0; w < 4; ++w) DEN += s.part[w][pi][1] * __builtin_amdgcn_exp2f(s.part[w][pi][0] - MX);
+  const float inv_den = 1.0f / DEN;
   const float bmax = fmaxf(fmaxf(s.bmax_w[0], s.bmax_w[1]), fmaxf(s.bmax_w[2], s.bmax_w[3]));
   const float th0 = p.theta[h * 4 + 0], th1 = p.theta[h * 4 + 1], th2 = p.theta[h * 4 + 2], th3 = p.theta[h * 4 + 3];
 
@@ -196,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
       };
       float prob[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) prob[i] = expf(S[4 * j + i] * inv_sqrt_d - MX) / DEN;
+      for (int i = 0; i < 4; ++i) prob[i] = __builtin_amdgcn_exp2f(fmaf(S[4 * j + i], c2, -MX)) * inv_den;
       const float alpha = ((prob[0] + prob[1]) + prob[2]) + prob[3];
       const float c = st(1, 11) + bmax;
       float x0 = alpha * st(0, 11), x1 = 0.f, x2 = 0.f, x3 = 0.f;
@@ -208,7 +231,7 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
         u = fmaxf(u, 0.f);
         const float beta = qn * st(i, 8);
         x0 += fabsf(prob[i] - alpha * 0.25f) * st(i, 9);
-        x1 += prob[i] * sqrtf(u) * st(i, 10);
+        x1 += prob[i] * __builtin_amdgcn_sqrtf(u) * st(i, 10);
         x2 += prob[i] * beta;
         x3 += prob[i] * (u + beta * beta);
       }
@@ -231,85 +254,89 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   if (p.mode < 0) return;
 
   // ---------------------------------------------------------------- select
-  // keys: (orderable risk << 32) | ~page, descending order = risk desc, page asc
+  // Row b is sorted by 128 threads (tid / 128 = b) with a bitonic network
+  // over 512 64-bit keys, descending.  Key = (group << 62) | (orderable
+  // risk << 30) | (1023 - page): risk descending, ties -> lower page, and
+  // the group field orders the partitions (base / top-k: one group).
+  const int b = tid >> 7, bt = tid & 127;
   int own[2];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const int tb = min(t0 + b, p.T - 1);
-    own[b] = p.own ? p.own[(long long)h * p.T + tb] : P - p.T + tb;
+  for (int q = 0; q < 2; ++q) {
+    const int tb = min(t0 + q, p.T - 1);
+    own[q] = p.own ? p.own[(long long)h * p.T + tb] : P - p.T + tb;
   }
   const int A = p.mode == 1 ? p.current[h] : 0;
-  for (int i = tid; i < 2 * P; i += kThreads) {
-    const int b = i / P, pg = i % P;
-    unsigned long long key = ((unsigned long long)orderable(s.risk[b][pg]) << 32) | (0xffffffffu - (uint32_t)pg);
-    bool cand;
-    if (p.mode == 0) {
-      cand = pg >= kAnchors && pg != own[b];
-    } else if (p.mode == 1) {
-      cand = pg >= kAnchors;
-      if (pg == own[b]) key = ~0ull;                       // own forced first (+inf)
-    } else {
-      cand = true;
-      if (pg == own[b]) key = ~0ull;
-    }
-    s.key[b][pg] = cand ? key : 0ull;
-  }
-  __syncthreads();
-  for (int i = tid; i < 2 * P; i += kThreads) {
-    const int b = i / P, pg = i % P;
-    const unsigned long long k = s.key[b][pg];
-    bool keep = false;
-    int rank = 0;
-    if (k != 0ull) {
-      if (p.mode == 1) {
-        const bool cur = pg >= P - kCurrent;
-        const int lo = cur ? P - kCurrent : kAnchors, hi = cur ? P : P - kCurrent;
-        for (int j = lo; j < hi; ++j) rank += s.key[b][j] > k;
-        keep = rank < (cur ? A : p.total - A);
+  for (int pg = bt; pg < kMaxPages; pg += 128) {
+    unsigned long long key = 0ull;
+    if (pg < P) {
+      const unsigned long long ord = (unsigned long long)orderable(s.risk[b][pg]) << 30;
+      const unsigned long long low = (unsigned long long)(1023 - pg);
+      if (p.mode == 0) {
+        if (pg >= kAnchors && pg != own[b]) key = (1ull << 62) | ord | low;
+      } else if (p.mode == 1) {
+        if (pg == own[b]) key = (3ull << 62) - 1ull - (unsigned long long)pg;     // own first in current
+        else if (pg >= P - kCurrent) key = (2ull << 62) | ord | low;
+        else if (pg >= kAnchors) key = (1ull << 62) | ord | low;
       } else {
-        for (int j = 0; j < P; ++j) rank += s.key[b][j] > k;
-        keep = rank < (p.mode == 0 ? p.C - 1 - kAnchors : p.C);
+        key = pg == own[b] ? ~0ull : ((1ull << 62) | ord | low);
       }
     }
-    if (p.mode != 2 && pg < kAnchors) keep = true;
-    if (p.mode == 0 && pg == own[b]) keep = true;
-    s.sel[b][pg] = keep;
-    if (p.mode == 0 && keep && pg >= kAnchors && pg != own[b] && b < nrow && p.ids)
-      p.ids[((long long)h * p.T + t0 + b) * p.C + 1 + kAnchors + rank] = pg;
-    if (p.mode == 2 && keep && b < nrow && p.ids)
-      p.ids[((long long)h * p.T + t0 + b) * p.C + rank] = pg;
+    s.key[b][pg] = key;
   }
   __syncthreads();
-  if (p.mode == 0 && p.ids) {
-    for (int i = tid; i < 2 * (1 + kAnchors); i += kThreads) {
-      const int b = i / (1 + kAnchors), j = i % (1 + kAnchors);
-      if (b < nrow) p.ids[((long long)h * p.T + t0 + b) * p.C + j] = j == 0 ? own[b] : j - 1;
+  bitonic_desc(s.key[b], bt);
+  // s.key[b] sorted descending; the page of entry i is 1023 - (key & 1023)
+  auto page_at = [&](int i) -> int { return 1023 - (int)(s.key[b][i] & 1023ull); };
+  const bool row_ok = b < nrow;
+  int32_t* idsrow = p.ids ? p.ids + ((long long)h * p.T + t0 + b) * p.C : nullptr;
+  for (int pg = bt; pg < P; pg += 128) s.sel[b][pg] = 0;
+  __syncthreads();
+  if (p.mode == 0) {
+    // LUT = [own, 0..23, top C-25 candidates], already in order
+    for (int i = bt; i < p.C; i += 128) {
+      const int pg = i == 0 ? own[b] : (i <= kAnchors ? i - 1 : page_at(i - 1 - kAnchors));
+      s.sel[b][pg] = 1;
+      if (row_ok && idsrow) idsrow[i] = pg;
     }
-  }
-  if (p.mode == 1 && p.ids) {
-    // LUT: own first, then every selected page by descending risk
-    for (int i = tid; i < 2 * P; i += kThreads) {
-      const int b = i / P, pg = i % P;
-      if (!s.sel[b][pg] || b >= nrow) continue;
-      int slot = 0;
-      if (pg != own[b]) {
-        const unsigned long long k = ((unsigned long long)orderable(s.risk[b][pg]) << 32) | (0xffffffffu - (uint32_t)pg);
-        int rank = 0;
-        for (int j = 0; j < P; ++j) {
-          if (!s.sel[b][j] || j == own[b]) continue;
-          const unsigned long long kj = ((unsigned long long)orderable(s.risk[b][j]) << 32) | (0xffffffffu - (uint32_t)j);
-          rank += kj > k;
+  } else if (p.mode == 2) {
+    for (int i = bt; i < p.C; i += 128) {
+      const int pg = page_at(i);
+      s.sel[b][pg] = 1;
+      if (row_ok && idsrow) idsrow[i] = pg;
+    }
+  } else {
+    // quota: current top A at sorted [0, A) (own first), history top n-A at
+    // sorted [72, 72+n-A), anchors; list them, then order the LUT by risk
+    const int nh = p.total - A;
+    for (int i = bt; i < p.C; i += 128) {
+      const int pg = i < A ? page_at(i) : (i < A + nh ? page_at(kCurrent + i - A) : i - A - nh);
+      s.list[b][i] = pg;
+      s.sel[b][pg] = 1;
+    }
+    __syncthreads();
+    if (idsrow) {
+      for (int i = bt; i < p.C; i += 128) {
+        const int pg = s.list[b][i];
+        int slot = 0;
+        if (pg != own[b]) {
+          const uint32_t kx = orderable(s.risk[b][pg]);
+          int rank = 0;
+          for (int j = 0; j < p.C; ++j) {
+            const int y = s.list[b][j];
+            if (y == own[b]) continue;
+            const uint32_t ky = orderable(s.risk[b][y]);
+            rank += (ky > kx) || (ky == kx && y < pg);
+          }
+          slot = 1 + rank;
         }
-        slot = 1 + rank;
+        if (row_ok && slot < p.C) idsrow[slot] = pg;
       }
-      if (slot < p.C) p.ids[((long long)h * p.T + t0 + b) * p.C + slot] = pg;
     }
   }
+  __syncthreads();
   if (p.mask) {
-    for (int i = tid; i < 2 * P; i += kThreads) {
-      const int b = i / P, pg = i % P;
-      if (b < nrow) p.mask[((long long)h * p.T + t0 + b) * P + pg] = s.sel[b][pg];
-    }
+    for (int pg = bt; pg < P; pg += 128)
+      if (row_ok) p.mask[((long long)h * p.T + t0 + b) * P + pg] = s.sel[b][pg];
   }
 }
 
