@@ -245,12 +245,13 @@ def intersection_lines(args, dense_ms, iters):
     out["ratio_intersection_vs_dense"] = None if dense_ms is None else round(out["intersection_ms"] / dense_ms, 4)
     out["ratio_full_pset_vs_dense"] = None if dense_ms is None else \
         round(out["intersection_full_pset_ms"] / dense_ms, 4)
+    lse = torch.empty(12, 72, 16, device=dev)
     route_i = lambda: route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
-                            want_mask=True)
+                            want_mask=True, lse_out=lse)
     out["route_intersection_ms"] = round(time_loop(route_i, iters, stream), 4)
     ids, mask, risk, _ = route_i()
     out["pset_correction_ms"] = round(time_loop(
-        lambda: pset.correct(g.q, g.summary, enc, reader, risk, mask, ids, None, PSET_HEADS, ws), iters, stream), 4)
+        lambda: pset.correct(g.q, g.summary, enc, reader, risk, lse, mask, ids, None, PSET_HEADS, ws), iters, stream), 4)
     out["encode_current_72x12_ms"] = round(time_loop(
         lambda: pset.encode(g.summary, basis, reader, out=enc, first=P - 72, pages=72), iters, stream), 4)
     out["full_pset_heads"] = list(PSET_HEADS)

@@ -68,11 +68,13 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
  * mode 1: anchor/current/history quota, current[h] = A >= 1, total = A+B,
  *         count = 24 + total, ids = own then selected by descending risk;
  * mode 2: fixed top-count with own forced first.  Ties -> lower page.
- * ids [H,blocks,count] int32 and mask [H,blocks,pages] uint8 may be NULL. */
+ * ids [H,blocks,count] int32 and mask [H,blocks,pages] uint8 may be NULL; lse
+ * [H,blocks,16] fp32 (NULL to skip) receives each probe's log-sum-exp over
+ * all reps of the window (natural log), the input ssa_pset needs. */
 int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
-              const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, int heads, int blocks, int pages,
-              int head_pages, int count, int mode, int total, hipStream_t stream);
+              const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
+              int pages, int head_pages, int count, int mode, int total, hipStream_t stream);
 
 /* Full_Pset page encodings of pages [first_page, first_page + pages) of the
  * summary slab (keys/mean/detail/stats as in ssa_route, capacity head_pages):
@@ -91,22 +93,23 @@ int ssa_encode(const void* keys, const void* mean, const void* detail, const voi
 /* Full_Pset swap correction of the heads listed in heads[n_heads] (indices
  * into total_heads), after ssa_route in mode 1 produced risk, mask and ids.
  * Probe rows as in ssa_route; keys [H,head_pages,4,128] bf16; encodings from
- * ssa_encode; wq [8,128] fp32 (phi query map).  For each scoped (head, block)
+ * ssa_encode; wq [8,128] fp32 (phi query map); probe_lse [H,blocks,16] from
+ * ssa_route.  For each scoped (head, block)
  * the best legal same-partition swap is applied to mask [H,blocks,pages]
  * (0/1 bytes) iff its gain > 0 and every legal score is finite, and the row
  * of ids [H,blocks,count] is rebuilt (own first, then descending risk).
  * Caller-owned scratch: cand n_heads*blocks*16*48*34 fp64, rows
- * n_heads*blocks*16*52 fp64, pool n_heads*blocks*64 int32.  Per-row outputs:
+ * n_heads*blocks*16*4*52 fp64, pool n_heads*blocks*64 int32.  Per-row outputs:
  * gain [n_heads,blocks] fp64, info [n_heads,blocks,3] int32 = (executed, best
  * pair index remove*32+add, non-finite legal scores); scores
  * [n_heads,blocks,16,32] fp64 (illegal pairs -1e30) or NULL.
  * Requires 96 < pages <= 512 and pages - count >= 64. */
 int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
              int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
-             const double* detail_b, int enc_pages, const float* wq, const float* risk, uint8_t* mask,
-             int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand, double* rows,
-             int32_t* pool, double* gain, int32_t* info, double* scores, int total_heads, int blocks, int pages,
-             int count, hipStream_t stream);
+             const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,
+             uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand,
+             double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, int total_heads, int blocks,
+             int pages, int count, hipStream_t stream);
 
 #ifdef __cplusplus
 }

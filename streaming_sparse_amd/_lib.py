@@ -17,11 +17,12 @@ _vp, _i, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
 SIGNATURES = {
     "ssa_rep_values": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp],
-    "ssa_route": [_vp, _ll, _ll, _ll, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp],
+    "ssa_route": [_vp, _ll, _ll, _ll, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
+                  _vp],
     "ssa_encode": [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                    _i, _vp],
-    "ssa_pset": [_vp, _ll, _ll, _ll, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp,
-                 _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "ssa_pset": [_vp, _ll, _ll, _ll, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
+                 _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
 }
 
 

@@ -37,7 +37,6 @@ constexpr int kCoefStride = 128;    // bf16 per page: co[85] | 0 x 11 | A[32]
 constexpr int kCoefA = 96;
 constexpr int kCand = 48;           // 16 removes + 32 adds
 constexpr int kCandVals = 34;       // lm, beta, approx[16], rp[16]
-constexpr int kRowVals = 52;        // H[16], E[16], ob[16], lb, logmax, -, -
 constexpr int kPoolInts = 64;       // 48 candidate pages + 16 legal bit rows
 
 // ------------------------------------------------------------- encoding ----
@@ -174,7 +173,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
   }
 }
 
-// ----------------------------------------------------------------- rows ----
+// ----------------------------------------------------------------- pool ----
 
 struct PsetParams {
   const uint16_t* q;
@@ -187,6 +186,7 @@ struct PsetParams {
   int EP;
   const float* wq;
   const float* risk;
+  const float* lse;            // [H, T, 16] per-probe LSE over all reps (from the router)
   uint8_t* mask;
   int32_t* ids;
   const int32_t* own;
@@ -202,23 +202,133 @@ struct PsetParams {
 
 __constant__ int kProbeOffsets[16] = {0, 4, 8, 13, 17, 21, 25, 29, 34, 38, 42, 46, 50, 55, 59, 63};
 
-struct RowsSmem {
-  float risk[2][kMaxPages];
-  uint8_t sel[2][kMaxPages];
-  uint8_t isadd[2][kMaxPages];
-  int8_t slot[2][kMaxPages];
-  int rslot[2][16];
-  int aslot[2][32];
-  int spare[2][32];
-  int cnt[2][4];                       // movable hist/cur, unselected hist/cur
-  float u[32][8];
-  double lse[4][32][2];
-  double part[4][32][kRowVals];
-};
-
 __device__ __forceinline__ int own_page(const PsetParams& p, int h, int t) {
   return p.own ? p.own[(long long)h * p.T + t] : p.P - p.T + t;
 }
+
+struct PoolSmem {
+  float risk[kMaxPages];
+  uint8_t sel[kMaxPages];
+  uint8_t isadd[kMaxPages];
+  unsigned long long key[kMaxPages];
+  int cnt[4];                  // movable history, movable current, unselected history, unselected current
+  int spare[32];
+};
+
+// One workgroup per scoped (head, block): the stratified pools of
+// VB/quota_pool.py:3-46 from one descending bitonic sort of 512 keys whose
+// group field orders history removes > current removes > history adds >
+// current adds; removes rank by ascending risk, adds by descending risk,
+// ties -> lower page.
+__global__ __launch_bounds__(256) void pset_pool_kernel(PsetParams p) {
+  __shared__ PoolSmem s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hs = blockIdx.x / p.T, t = blockIdx.x % p.T;
+  const int h = p.heads[hs];
+  const int P = p.P;
+  const long long rowoff = ((long long)h * p.T + t) * P;
+  const int own = own_page(p, h, t);
+  for (int i = tid; i < kMaxPages; i += 256) {
+    s.risk[i] = i < P ? p.risk[rowoff + i] : 0.f;
+    s.sel[i] = i < P ? (p.mask[rowoff + i] ? 1 : 0) : 1;
+    s.isadd[i] = 0;
+  }
+  if (tid < 4) s.cnt[tid] = 0;
+  __syncthreads();
+  for (int pg = tid; pg < kMaxPages; pg += 256) {
+    unsigned long long key = 0ull;
+    if (pg >= kAnchors && pg < P) {
+      const int cur = pg >= P - kCurrent;
+      const uint32_t ord = orderable(s.risk[pg]);
+      int group = 0;
+      uint32_t kv = 0;
+      if (s.sel[pg] && pg != own) {
+        group = cur ? 3 : 4;
+        kv = ~ord;
+      } else if (!s.sel[pg]) {
+        group = cur ? 1 : 2;
+        kv = ord;
+      }
+      if (group) {
+        key = ((unsigned long long)group << 60) | ((unsigned long long)kv << 20) | (unsigned long long)(1023 - pg);
+        atomicAdd(&s.cnt[4 - group], 1);
+      }
+    }
+    s.key[pg] = key;
+  }
+  __syncthreads();
+  for (int k = 2; k <= kMaxPages; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const int lo = 2 * tid - (tid & (j - 1)), hi = lo + j;
+      const bool desc = (lo & k) == 0;
+      const unsigned long long a = s.key[lo], c = s.key[hi];
+      if ((a < c) == desc) {
+        s.key[lo] = c;
+        s.key[hi] = a;
+      }
+      __syncthreads();
+    }
+  }
+  const int nmh = s.cnt[0], nmc = s.cnt[1], nuh = s.cnt[2], nuc = s.cnt[3];
+  auto page_at = [&](int i) -> int { return 1023 - (int)(s.key[i] & 1023ull); };
+  // valid adds, then spare pages (neither selected nor a valid add), ascending
+  if (tid < 32) {
+    const int q = tid >> 4, k = tid & 15;
+    const int n = q ? nuc : nuh;
+    if (k < n) s.isadd[page_at(nmh + nmc + (q ? nuh : 0) + k)] = 1;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int cnt = 0;
+    for (int base = 0; base < P; base += 64) {
+      const int pg = base + lane;
+      const bool fr = pg < P && !s.sel[pg] && !s.isadd[pg];
+      const unsigned long long bal = __ballot(fr);
+      const int r = cnt + __popcll(bal & ((1ull << lane) - 1ull));
+      if (fr && r < 32) s.spare[r] = pg;
+      cnt += __popcll(bal);
+    }
+    if (lane < 32 && lane >= cnt) s.spare[lane] = -1;
+  }
+  __syncthreads();
+  if (tid < kCand) {
+    const int sl = tid;
+    int page;
+    bool valid;
+    if (sl < 16) {
+      const int q = sl >> 3, k = sl & 7;
+      valid = k < (q ? nmc : nmh);
+      page = valid ? page_at((q ? nmh : 0) + k) : sl;          // anchor stands in (never legal)
+    } else {
+      const int q = (sl - 16) >> 4, k = (sl - 16) & 15;
+      valid = k < (q ? nuc : nuh);
+      page = valid ? page_at(nmh + nmc + (q ? nuh : 0) + k) : s.spare[sl - 16];   // spare (never legal)
+    }
+    int32_t* po = p.pool + ((long long)hs * p.T + t) * kPoolInts;
+    po[sl] = page;
+    if (sl < 16) {
+      const int q = sl >> 3;
+      const int na = q ? nuc : nuh;
+      const uint32_t addbits = na >= 16 ? 0xffffu : ((1u << na) - 1u);
+      po[kCand + sl] = valid ? (int32_t)(addbits << (16 * q)) : 0;
+    }
+  }
+}
+
+// ----------------------------------------------------------------- rows ----
+
+constexpr int kSplit = 4;          // page ranges per (head, pair of blocks)
+constexpr int kRowPart = 52;       // accH[16], accT[16], accB[16], sH, sT, sB, max logs
+
+struct RowsSmem {
+  uint8_t sel[2][kMaxPages];
+  int8_t slot[2][kMaxPages];
+  float u[32][8];
+  float L[32];
+  alignas(16) float coef[4][8][128];     // per-wave staging of a tile's 8 pages (fp32)
+  alignas(16) double md[4][8][64];       // meanB[16] | detailB[48]
+  double part[4][32][kRowPart];
+};
 
 __device__ __forceinline__ void rep_tile(const uint16_t* rkh, int tile, int P, int lane, const u32x4 (&qop)[8],
                                          f32x16& S) {
@@ -233,128 +343,38 @@ __device__ __forceinline__ void rep_tile(const uint16_t* rkh, int tile, int P, i
   for (int st = 0; st < 8; ++st) S = mfma32(av[st], qop[st], S);
 }
 
-// log-sum-exp of the 4 rep logits of a page (fp64) and the softmax weights
-__device__ __forceinline__ double page_lse(const float (&z)[4], double (&w)[4]) {
-  const double zm = (double)fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
-  double s = 0.0;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    w[r] = exp((double)z[r] - zm);
-    s += w[r];
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) w[r] /= s;
-  return zm + log(s);
-}
-
+// One workgroup per (scoped head, pair of blocks, page range): per probe
+// and page, the log mass lm = LSE_r z - LSE z, the readout (rp, beta), the
+// summary approximation, then partial mixture sums; candidate pages write
+// their endpoint data.
 __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
   __shared__ RowsSmem s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NP = (p.T + 1) >> 1;
-  const int hs = blockIdx.x / NP, t0 = 2 * (blockIdx.x % NP);
+  const int sp = blockIdx.x % kSplit;
+  const int pair_id = (blockIdx.x / kSplit) % NP;
+  const int hs = blockIdx.x / (kSplit * NP);
+  const int t0 = 2 * pair_id;
   const int h = p.heads[hs];
   const int P = p.P;
   const int nrow = min(2, p.T - t0);
+  const int ntiles = (P + 7) >> 3;
+  const int tile0 = sp * ntiles / kSplit, tile1 = (sp + 1) * ntiles / kSplit;
 
-  // ---- rows of risk / selection, pools (VB/quota_pool.py:3-46)
   for (int i = tid; i < 2 * P; i += 256) {
     const int b = i / P, pg = i % P;
     const int tb = min(t0 + b, p.T - 1);
-    const long long r = ((long long)h * p.T + tb) * P + pg;
-    s.risk[b][pg] = p.risk[r];
-    s.sel[b][pg] = p.mask[r] ? 1 : 0;
-    s.isadd[b][pg] = 0;
+    s.sel[b][pg] = p.mask[((long long)h * p.T + tb) * P + pg] ? 1 : 0;
     s.slot[b][pg] = -1;
-  }
-  if (tid < 2 * 16) s.rslot[tid >> 4][tid & 15] = -1;
-  if (tid < 2 * 32) s.aslot[tid >> 5][tid & 31] = -1;
-  if (tid < 8) s.cnt[tid >> 2][tid & 3] = 0;
-  __syncthreads();
-  int own[2];
-#pragma unroll
-  for (int b = 0; b < 2; ++b) own[b] = own_page(p, h, min(t0 + b, p.T - 1));
-  for (int i = tid; i < 2 * P; i += 256) {
-    const int b = i / P, pg = i % P;
-    if (pg < kAnchors) continue;
-    const int part = pg >= P - kCurrent ? 1 : 0;
-    const int lo = part ? P - kCurrent : kAnchors, hi = part ? P : P - kCurrent;
-    const bool sel = s.sel[b][pg];
-    const uint32_t key = orderable(s.risk[b][pg]);
-    if (sel && pg != own[b]) {
-      // removes: ascending risk, ties -> lower page
-      int rank = 0;
-      for (int y = lo; y < hi; ++y) {
-        if (!s.sel[b][y] || y == own[b]) continue;
-        const uint32_t ky = orderable(s.risk[b][y]);
-        rank += (ky < key) || (ky == key && y < pg);
-      }
-      if (rank < 8) s.rslot[b][part * 8 + rank] = pg;
-      atomicAdd(&s.cnt[b][part], 1);
-    } else if (!sel) {
-      // adds: descending risk, ties -> lower page
-      int rank = 0;
-      for (int y = lo; y < hi; ++y) {
-        if (s.sel[b][y]) continue;
-        const uint32_t ky = orderable(s.risk[b][y]);
-        rank += (ky > key) || (ky == key && y < pg);
-      }
-      if (rank < 16) {
-        s.aslot[b][part * 16 + rank] = pg;
-        s.isadd[b][pg] = 1;
-      }
-      atomicAdd(&s.cnt[b][2 + part], 1);
-    }
-  }
-  __syncthreads();
-  if (wave < 2) {
-    // spare pages: neither selected nor a valid add, ascending index
-    const int b = wave;
-    int cnt = 0;
-    for (int base = 0; base < P; base += 64) {
-      const int pg = base + lane;
-      const bool fr = pg < P && !s.sel[b][pg] && !s.isadd[b][pg];
-      const unsigned long long bal = __ballot(fr);
-      const int r = cnt + __popcll(bal & ((1ull << lane) - 1ull));
-      if (fr && r < 32) s.spare[b][r] = pg;
-      cnt += __popcll(bal);
-    }
-    if (lane < 32 && lane >= cnt) s.spare[b][lane] = -1;
   }
   __syncthreads();
   if (tid < 2 * kCand) {
     const int b = tid / kCand, sl = tid % kCand;
-    int page;
-    if (sl < 16) {
-      page = s.rslot[b][sl];
-      if (page < 0) page = sl;                      // anchor page stands in (never legal)
-    } else {
-      page = s.aslot[b][sl - 16];
-      if (page < 0) page = s.spare[b][sl - 16];     // spare unselected page (never legal)
-    }
-    if (page >= 0) s.slot[b][page] = (int8_t)sl;
-    if (b < nrow) {
-      int32_t* po = p.pool + ((long long)hs * p.T + t0 + b) * kPoolInts;
-      po[sl] = page;
-      if (sl < 16) {
-        uint32_t bits = 0u;
-        if (s.rslot[b][sl] >= 0) {
-          const int part = sl >= 8;
-          for (int j = part * 16; j < part * 16 + 16; ++j) bits |= (s.aslot[b][j] >= 0 ? 1u : 0u) << j;
-        }
-        po[kCand + sl] = (int32_t)bits;
-      }
-    }
+    const int tb = min(t0 + b, p.T - 1);
+    const int page = p.pool[((long long)hs * p.T + tb) * kPoolInts + sl];
+    if (page >= 0 && page < P) s.slot[b][page] = (int8_t)sl;
   }
-
-  // ---- probe operand, reader query u = Wq . probe (fp32)
-  const int pi = lane & 31, hh = lane >> 5;
-  const int blk = pi >> 4, m = pi & 15;
-  const int tq = min(t0 + blk, p.T - 1);
-  const long long row = p.gathered ? m : kProbeOffsets[m];
-  const uint16_t* qbase = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
-  u32x4 qop[8];
-#pragma unroll
-  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qbase + 64 * hh + 8 * st);
+  // reader query u = Wq . probe (fp32) and the probe LSE from the router
   {
     const int pr = tid >> 3, i = tid & 7;
     const int tb = min(t0 + (pr >> 4), p.T - 1);
@@ -363,107 +383,87 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
     float acc = 0.f;
     for (int d = 0; d < 128; ++d) acc = fmaf(bf16_to_f32(qq[d]), p.wq[i * 128 + d], acc);
     s.u[pr][i] = acc;
+    if (i == 0) s.L[pr] = p.lse[((long long)h * p.T + tb) * 16 + (pr & 15)];
   }
-
-  const uint16_t* rkh = p.rk + (long long)h * p.HP * 4 * kHeadDim;
-  const int ntiles = (P + 7) >> 3;
-  const float inv_sqrt_d = 1.0f / sqrtf((float)kHeadDim);
-
-  // ---- pass 1: LSE over all reps of each probe
-  double mx = -INFINITY, sm = 0.0;
-  for (int tile = wave; tile < ntiles; tile += 4) {
-    f32x16 S;
-    rep_tile(rkh, tile, P, lane, qop, S);
+  const int pi = lane & 31, hh = lane >> 5;
+  const int blk = pi >> 4, m = pi & 15;
+  const int tq = min(t0 + blk, p.T - 1);
+  const long long row = p.gathered ? m : kProbeOffsets[m];
+  const uint16_t* qbase = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
+  u32x4 qop[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int page = tile * 8 + 2 * j + hh;
-      if (page >= P) continue;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const double z = (double)(S[4 * j + r] * inv_sqrt_d);
-        if (z > mx) {
-          sm = sm * exp(mx - z) + 1.0;
-          mx = z;
-        } else {
-          sm += exp(z - mx);
-        }
-      }
-    }
-  }
-  {
-    const double om = __shfl_xor(mx, 32), os = __shfl_xor(sm, 32);
-    const double mm = fmax(mx, om);
-    const double tot = (mx == -INFINITY ? 0.0 : sm * exp(mx - mm)) + (om == -INFINITY ? 0.0 : os * exp(om - mm));
-    if (hh == 0) {
-      s.lse[wave][pi][0] = mm;
-      s.lse[wave][pi][1] = tot;
-    }
-  }
+  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qbase + 64 * hh + 8 * st);
   __syncthreads();
-  double L;
-  {
-    double mm = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) mm = fmax(mm, s.lse[w][pi][0]);
-    double tot = 0.0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      if (s.lse[w][pi][0] != -INFINITY) tot += s.lse[w][pi][1] * exp(s.lse[w][pi][0] - mm);
-    L = mm + log(tot);
-  }
   float u[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) u[i] = s.u[pi][i];
+  const double L = (double)s.L[pi];
+  const uint16_t* rkh = p.rk + (long long)h * p.HP * 4 * kHeadDim;
+  const float c2 = kLog2e / sqrtf((float)kHeadDim);    // logits in log2 units
+  constexpr float kLn2 = 0.69314718055994531f;
 
-  // ---- pass 2: readout, summary approximation, mixtures, candidate endpoints
   double accH[16], accT[16], accB[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) accH[e] = accT[e] = accB[e] = 0.0;
   double sH = 0.0, sT = 0.0, sB = 0.0, lmax = -INFINITY;
   const long long row_id = ((long long)hs * p.T + tq) * 16 + m;
-  for (int tile = wave; tile < ntiles; tile += 4) {
+  float* cw = &s.coef[wave][0][0];
+  double* mw = &s.md[wave][0][0];
+  for (int tile = tile0 + wave; tile < tile1; tile += 4) {
+    // stage this tile's 8 pages: coefficients (bf16 -> fp32) and meanB | detailB
+    {
+      const int pl = lane >> 3, c = lane & 7;
+      const int page = min(tile * 8 + pl, P - 1);
+      const uint16_t* cf = p.coef + ((long long)h * p.EP + page) * kCoefStride + 16 * c;
+      const u32x4 a = ldg16(cf), b = ldg16(cf + 8);
+      float* d = cw + pl * 128 + 16 * c;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        d[2 * k] = bf16_lo(a[k]);
+        d[2 * k + 1] = bf16_hi(a[k]);
+        d[8 + 2 * k] = bf16_lo(b[k]);
+        d[8 + 2 * k + 1] = bf16_hi(b[k]);
+      }
+      const double* src = c < 2 ? p.mean_b + ((long long)h * p.EP + page) * 16 + 8 * c
+                                 : p.detail_b + ((long long)h * p.EP + page) * 48 + 8 * (c - 2);
+      double* md = mw + pl * 64 + 8 * c;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) md[k] = src[k];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     f32x16 S;
     rep_tile(rkh, tile, P, lane, qop, S);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int page = tile * 8 + 2 * j + hh;
+      const int pl = 2 * j + hh;
+      const int page = tile * 8 + pl;
       if (page >= P) continue;
-      float z[4];
+      // rep softmax of the page (fp32), page log mass in fp64
+      float z[4], w[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = S[4 * j + r] * inv_sqrt_d;
-      double w[4];
-      const double lm = page_lse(z, w) - L;
-      const double c0 = w[0] + w[1] - w[2] - w[3];
-      const double c1 = w[0] - w[1] + w[2] - w[3];
-      const double c2 = w[0] - w[1] - w[2] + w[3];
-      // reader readout (fp32)
-      const uint16_t* cf = p.coef + ((long long)h * p.EP + page) * kCoefStride;
-      float co[88];
+      for (int r = 0; r < 4; ++r) z[r] = S[4 * j + r] * c2;
+      const float zm = fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
+      float sw = 0.f;
 #pragma unroll
-      for (int c = 0; c < 11; ++c) {
-        const u32x4 v = ldg16(cf + 8 * c);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          co[8 * c + 2 * k] = bf16_lo(v[k]);
-          co[8 * c + 2 * k + 1] = bf16_hi(v[k]);
-        }
+      for (int r = 0; r < 4; ++r) {
+        w[r] = __builtin_amdgcn_exp2f(z[r] - zm);
+        sw += w[r];
       }
-      float A[32];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 v = ldg16(cf + kCoefA + 8 * c);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          A[8 * c + 2 * k] = bf16_lo(v[k]);
-          A[8 * c + 2 * k + 1] = bf16_hi(v[k]);
-        }
-      }
+      const double lm = (double)((zm + __log2f(sw)) * kLn2) - L;
+      const float isw = 1.0f / sw;
+      const float c0 = (w[0] + w[1] - w[2] - w[3]) * isw;
+      const float c1 = (w[0] - w[1] + w[2] - w[3]) * isw;
+      const float cc2 = (w[0] - w[1] - w[2] + w[3]) * isw;
+      // readout: F_j = tanh(u . A_j), val = co_0 + sum_j F_j co_{j+1}
+      const float* cf = cw + pl * 128;
       float F[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(u[i], A[i * 4 + jj], acc);
+        for (int i = 0; i < 8; ++i) acc = fmaf(u[i], cf[kCoefA + 4 * i + jj], acc);
         F[jj] = tanhf(acc);
       }
       float val[17];
@@ -471,8 +471,8 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
       for (int k = 0; k < 17; ++k) {
         float acc = 0.f;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) acc = fmaf(F[jj], co[(jj + 1) * 17 + k], acc);
-        val[k] = co[k] + acc;
+        for (int jj = 0; jj < 4; ++jj) acc = fmaf(F[jj], cf[(jj + 1) * 17 + k], acc);
+        val[k] = cf[k] + acc;
       }
       const double beta = (double)val[16];
       const bool sel = s.sel[blk][page];
@@ -480,20 +480,21 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
       const double le = lm + beta;
       const double lg = sel ? le : lm;
       lmax = fmax(lmax, lg);
-      const double ex = exp(lg), et = exp(le);
+      const double ex = (double)__builtin_amdgcn_exp2f((float)lg * kLog2e);
+      const double et = (double)__builtin_amdgcn_exp2f((float)le * kLog2e);
       sH += ex;
       sT += et;
       if (sl < 0) sB += ex;
-      const double* mb = p.mean_b + ((long long)h * p.EP + page) * 16;
-      const double* db = p.detail_b + ((long long)h * p.EP + page) * 48;
+      const double* md = mw + pl * 64;
       double* cd = (sl >= 0 && blk < nrow) ? p.cand + (row_id * kCand + sl) * kCandVals : nullptr;
       if (cd) {
         cd[0] = lm;
         cd[1] = beta;
       }
+      const double d0 = c0, d1 = c1, d2 = cc2;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const double ap = mb[e] + (c0 * db[e] + c1 * db[16 + e] + c2 * db[32 + e]);
+        const double ap = md[e] + (d0 * md[16 + e] + d1 * md[32 + e] + d2 * md[48 + e]);
         const double rp = (double)val[e];
         const double cur = sel ? ap + rp : ap;
         accH[e] += ex * cur;
@@ -505,6 +506,7 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
         }
       }
     }
+    __builtin_amdgcn_wave_barrier();
   }
   // reduce over the two page halves of a lane pair, then over waves
 #pragma unroll
@@ -531,61 +533,60 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
     pw[51] = lmax;
   }
   __syncthreads();
-  for (int i = tid; i < 32 * 16; i += 256) {
-    const int pr = i >> 4, e = i & 15;
-    const int b = pr >> 4;
-    if (b >= nrow) continue;
-    double aH = 0.0, aT = 0.0, aB = 0.0, zH = 0.0, zT = 0.0, zB = 0.0, lx = -INFINITY;
+  for (int i = tid; i < 32 * kRowPart; i += 256) {
+    const int pr = i / kRowPart, e = i % kRowPart;
+    if ((pr >> 4) >= nrow) continue;
+    double v = e == 51 ? -INFINITY : 0.0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const double* pw = s.part[w][pr];
-      aH += pw[e];
-      aT += pw[16 + e];
-      aB += pw[32 + e];
-      zH += pw[48];
-      zT += pw[49];
-      zB += pw[50];
-      lx = fmax(lx, pw[51]);
-    }
-    const double Hv = aH / zH;
-    double* ro = p.rows + (((long long)hs * p.T + t0 + b) * 16 + (pr & 15)) * kRowVals;
-    ro[e] = Hv;
-    ro[16 + e] = aT / zT - Hv;
-    ro[32 + e] = aB / zB;
-    if (e == 0) {
-      ro[48] = log(zB);
-      ro[49] = lx;
-      ro[50] = log(zH);
-      ro[51] = 0.0;
-    }
+    for (int w = 0; w < 4; ++w) v = e == 51 ? fmax(v, s.part[w][pr][e]) : v + s.part[w][pr][e];
+    p.rows[((((long long)hs * p.T + t0 + (pr >> 4)) * 16 + (pr & 15)) * kSplit + sp) * kRowPart + e] = v;
   }
 }
 
 // --------------------------------------------------------------- scores ----
 
 struct ScoreSmem {
-  double cand[kCand][kCandVals];
-  double row[kRowVals];
-  double rx[16], ro[16][16], ax[32], ao[32][16];
+  double cand[4][kCand][kCandVals];      // per wave: one probe's candidate endpoints
+  double V[4][kCand][16];                // endpoint vectors D(c - H) + e^(e-M) rp
+  double S[4][kCand];                    // S_r (removes) / T_a (adds), shifted by the row max
+  double Hs[4][48];                      // H[16] | E[16] | ob[16] of the probe
+  double sc[4][3];                       // B, shift M, unused
+  double acc[4][512];
+  uint32_t legal[16];
+  int page[kCand];
   float risk[kMaxPages];
   uint8_t sel[kMaxPages];
-  int page[kCand];
-  uint32_t legal[16];
   double best[4];
-  int besti[4];
-  int bad[4];
+  int besti[4], bad[4];
 };
 
-__device__ __forceinline__ double logaddexp(double a, double b) {
-  if (a == -INFINITY) return b;
-  if (b == -INFINITY) return a;
-  const double mx = fmax(a, b);
-  return mx + log1p(exp(-fabs(a - b)));
+// Leave-one-out mixture fallback: the mixture after the swap (remove i, add
+// j) built from the background and every candidate, minus H.
+__device__ __noinline__ double fallback_delta(const ScoreSmem& s, int w, int i, int j, int e, double B, double M) {
+  const double* Hw = s.Hs[w];
+  double nw = B * Hw[32 + e];
+  for (int k = 0; k < 16; ++k) {
+    const double* c = s.cand[w][k];
+    const double em = exp(c[0] - M);
+    nw += k == i ? em * c[2 + e] : exp(c[0] + c[1] - M) * (c[2 + e] + c[18 + e]);
+  }
+  for (int k = 16; k < kCand; ++k) {
+    const double* c = s.cand[w][k];
+    nw += k == 16 + j ? exp(c[0] + c[1] - M) * (c[2 + e] + c[18 + e]) : exp(c[0] - M) * c[2 + e];
+  }
+  const double den = s.S[w][i] + s.S[w][16 + j];
+  return nw / den - Hw[e];
 }
 
+// One workgroup per scoped (head, block); wave w takes probes w, w+4, ...
+// With every log mass shifted by the row max M, e^(-den) of a swap is
+// 1/(S_r + T_a) where S_r = B + sum_{k!=r} e^(er_k-M) + e^(lr_r-M) and
+// T_a = sum_{k!=a} e^(la_k-M) + e^(ea_a-M) (VR/scores.py:72-73), and each
+// endpoint delta of VR/scores.py:81-88 factors into e^(-den) times a
+// per-candidate vector, so delta(r,a) = (V_a - V_r) / (S_r + T_a).
 __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
   __shared__ ScoreSmem s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int hs = blockIdx.x / p.T, t = blockIdx.x % p.T;
   const int h = p.heads[hs];
   const int P = p.P;
@@ -598,104 +599,95 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
     s.risk[i] = p.risk[r];
     s.sel[i] = p.mask[r] ? 1 : 0;
   }
-  // pairs (i, j) = (tid / 32, tid % 32) and (8 + tid / 32, tid % 32)
-  double acc[2] = {0.0, 0.0};
-  for (int m = 0; m < 16; ++m) {
-    __syncthreads();
+  for (int i = lane; i < 512; i += 64) s.acc[w][i] = 0.0;
+  for (int m = w; m < 16; m += 4) {
+    // stage the probe's candidates and row state
     const double* cd = p.cand + (rowbase * 16 + m) * kCand * kCandVals;
-    for (int i = tid; i < kCand * kCandVals; i += 256) (&s.cand[0][0])[i] = cd[i];
-    if (tid < kRowVals) s.row[tid] = p.rows[(rowbase * 16 + m) * kRowVals + tid];
-    __syncthreads();
-    // leave-one-out groups (VR/scores.py:34-47): removes over er = lm + beta
-    // with values c + rp, adds over la = lm with values c
-    if (tid < kCand) {
-      const bool rm = tid < 16;
-      const int j = rm ? tid : tid - 16;
-      const int k0 = rm ? 0 : 16, kn = rm ? 16 : 32;
-      double mx = -INFINITY;
-      for (int k = 0; k < kn; ++k) {
-        if (k == j) continue;
-        const double l = s.cand[k0 + k][0] + (rm ? s.cand[k0 + k][1] : 0.0);
-        mx = fmax(mx, l);
+    for (int i = lane; i < kCand * kCandVals; i += 64) (&s.cand[w][0][0])[i] = cd[i];
+    const double* rs = p.rows + (rowbase * 16 + m) * kSplit * kRowPart;
+    double aH = 0.0, aT = 0.0, aB = 0.0, zH = 0.0, zT = 0.0, zB = 0.0, lx = -INFINITY;
+    if (lane < 16) {
+#pragma unroll
+      for (int k = 0; k < kSplit; ++k) {
+        const double* r = rs + k * kRowPart;
+        aH += r[lane];
+        aT += r[16 + lane];
+        aB += r[32 + lane];
+        zH += r[48];
+        zT += r[49];
+        zB += r[50];
+        lx = fmax(lx, r[51]);
       }
-      double sum = 0.0, v[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = 0.0;
-      for (int k = 0; k < kn; ++k) {
-        if (k == j) continue;
-        const double l = s.cand[k0 + k][0] + (rm ? s.cand[k0 + k][1] : 0.0);
-        const double w = exp(l - mx);
-        sum += w;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] += w * (s.cand[k0 + k][2 + e] + (rm ? s.cand[k0 + k][18 + e] : 0.0));
-      }
-      const double lse = mx + log(sum);
-      if (rm) {
-        s.rx[j] = lse;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s.ro[j][e] = v[e] / sum;
-      } else {
-        s.ax[j] = lse;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s.ao[j][e] = v[e] / sum;
+      const double Hv = aH / zH;
+      s.Hs[w][lane] = Hv;
+      s.Hs[w][16 + lane] = aT / zT - Hv;
+      s.Hs[w][32 + lane] = aB / zB;
+      if (lane == 0) {
+        s.sc[w][0] = zB * exp(-lx);
+        s.sc[w][1] = lx;
       }
     }
-    __syncthreads();
-    const double lb = s.row[48], logmax = s.row[49];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const double B = s.sc[w][0], M = s.sc[w][1];
+    // per candidate: endpoint vector and its share of the swap denominator
+    if (lane < kCand) {
+      const double* c = s.cand[w][lane];
+      const double lmk = c[0], bk = c[1];
+      const double EX = exp(lmk + bk - M), LM = exp(lmk - M);
+      const double D = fabs(bk) < 0.5 ? LM * expm1(fmin(fmax(bk, -0.5), 0.5)) : EX - LM;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int i = (tid >> 5) + 8 * q, j = tid & 31;
-      const double* cr = s.cand[i];
-      const double* ca = s.cand[16 + j];
-      const double lr = cr[0], br = cr[1], er = lr + br;
-      const double la = ca[0], ba = ca[1], ea = la + ba;
-      double den = logaddexp(lb, s.rx[i]);
-      den = logaddexp(den, s.ax[j]);
-      den = logaddexp(den, lr);
-      den = logaddexp(den, ea);
-      // endpoint deltas; expm1 keeps beta near zero distinguishable
-      const double xa = exp(ea - den), aa = exp(la - den);
-      const double da = fabs(ba) < 0.5 ? aa * expm1(fmin(fmax(ba, -0.5), 0.5)) : xa - aa;
-      const double xr = exp(er - den), ar = exp(lr - den);
-      const double dr = fabs(br) < 0.5 ? ar * expm1(fmin(fmax(br, -0.5), 0.5)) : xr - ar;
+      for (int e = 0; e < 16; ++e) s.V[w][lane][e] = D * (c[2 + e] - s.Hs[w][e]) + EX * c[18 + e];
+      double loo = 0.0;
+      if (lane < 16) {
+        for (int k = 0; k < 16; ++k)
+          if (k != lane) loo += exp(s.cand[w][k][0] + s.cand[w][k][1] - M);
+        s.S[w][lane] = B + loo + LM;
+      } else {
+        for (int k = 16; k < kCand; ++k)
+          if (k != lane) loo += exp(s.cand[w][k][0] - M);
+        s.S[w][lane] = loo + EX;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll 1
+    for (int q = 0; q < 8; ++q) {
+      const int pr = lane + 64 * q, i = pr >> 5, j = pr & 31;
+      const double den = s.S[w][i] + s.S[w][16 + j];
+      const double inv = 1.0 / den;
       double delta[16];
-      bool finite = true;
+      bool finite = isfinite(inv);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const double Hv = s.row[e];
-        delta[e] = (da * (ca[2 + e] - Hv) + xa * ca[18 + e]) - (dr * (cr[2 + e] - Hv) + xr * cr[18 + e]);
+        delta[e] = (s.V[w][16 + j][e] - s.V[w][i][e]) * inv;
         finite = finite && isfinite(delta[e]);
       }
-      if (logmax - den > 80.0 || !finite) {
-        const double wb = exp(lb - den), wrx = exp(s.rx[i] - den), wax = exp(s.ax[j] - den);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          double nw = wb * s.row[32 + e];
-          nw += wrx * s.ro[i][e];
-          nw += wax * s.ao[j][e];
-          nw += ar * cr[2 + e];
-          nw += xa * (ca[2 + e] + ca[18 + e]);
-          delta[e] = nw - s.row[e];
-        }
+      // the reference's "bad" branch: max logs - den > 80, or a non-finite delta
+      if (den < 1.8048513878454153e-35 || !finite) {
+        for (int e = 0; e < 16; ++e) delta[e] = fallback_delta(s, w, i, j, e, B, M);
       }
       double ed = 0.0, dd = 0.0;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        ed += s.row[16 + e] * delta[e];
+        ed += s.Hs[w][16 + e] * delta[e];
         dd += delta[e] * delta[e];
       }
-      acc[q] += 2.0 * ed - dd;
+      s.acc[w][pr] += 2.0 * ed - dd;
     }
+    __builtin_amdgcn_wave_barrier();
   }
+  __syncthreads();
   // legality, argmax (ties -> lowest pair index), finiteness
   double best = -INFINITY;
   int besti = 0x7fffffff;
   int bad = 0;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const int i = (tid >> 5) + 8 * q, j = tid & 31;
-    const int flat = i * 32 + j;
-    double sc = acc[q] / 16.0;
+    const int flat = tid + 256 * q, i = flat >> 5, j = flat & 31;
+    double sc = (((s.acc[0][flat] + s.acc[1][flat]) + s.acc[2][flat]) + s.acc[3][flat]) / 16.0;
     if (!((s.legal[i] >> j) & 1u)) sc = -1e30;
     if (!isfinite(sc)) bad += 1;
     else if (sc > best || (sc == best && flat < besti)) {
@@ -715,20 +707,20 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
     }
   }
   if (lane == 0) {
-    s.best[wave] = best;
-    s.besti[wave] = besti;
-    s.bad[wave] = bad;
+    s.best[w] = best;
+    s.besti[w] = besti;
+    s.bad[w] = bad;
   }
   __syncthreads();
   best = s.best[0];
   besti = s.besti[0];
   bad = s.bad[0];
-  for (int w = 1; w < 4; ++w) {
-    if (s.best[w] > best || (s.best[w] == best && s.besti[w] < besti)) {
-      best = s.best[w];
-      besti = s.besti[w];
+  for (int k = 1; k < 4; ++k) {
+    if (s.best[k] > best || (s.best[k] == best && s.besti[k] < besti)) {
+      best = s.best[k];
+      besti = s.besti[k];
     }
-    bad += s.bad[w];
+    bad += s.bad[k];
   }
   const bool exec = bad == 0 && best > 0.0;
   if (tid == 0) {
@@ -805,14 +797,14 @@ int ssa_encode(const void* keys, const void* mean, const void* detail, const voi
 
 int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
              int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
-             const double* detail_b, int enc_pages, const float* wq, const float* risk, uint8_t* mask,
-             int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand, double* rows,
-             int32_t* pool, double* gain, int32_t* info, double* scores, int total_heads, int blocks, int pages,
-             int count, hipStream_t stream) {
+             const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,
+             uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand,
+             double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, int total_heads, int blocks,
+             int pages, int count, hipStream_t stream) {
   if (n_heads <= 0 || n_heads > total_heads || blocks <= 0 || pages > kMaxPages || pages <= kAnchors + kCurrent ||
       head_pages < pages || enc_pages < pages || count < 1 || count > pages || pages - count < 64 ||
-      heads == nullptr || cand == nullptr || rows == nullptr || pool == nullptr || gain == nullptr ||
-      info == nullptr)
+      heads == nullptr || probe_lse == nullptr || cand == nullptr || rows == nullptr || pool == nullptr ||
+      gain == nullptr || info == nullptr)
     return (int)hipErrorInvalidValue;
   PsetParams p;
   p.q = (const uint16_t*)q;
@@ -828,6 +820,7 @@ int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, l
   p.EP = enc_pages;
   p.wq = wq;
   p.risk = risk;
+  p.lse = probe_lse;
   p.mask = mask;
   p.ids = ids;
   p.own = own;
@@ -844,7 +837,8 @@ int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, l
   p.P = pages;
   p.C = count;
   const int np = (blocks + 1) / 2;
-  hipLaunchKernelGGL(pset_rows_kernel, dim3(n_heads * np), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(pset_pool_kernel, dim3(n_heads * blocks), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(pset_rows_kernel, dim3(n_heads * np * kSplit), dim3(256), 0, stream, p);
   hipLaunchKernelGGL(pset_scores_kernel, dim3(n_heads * blocks), dim3(256), 0, stream, p);
   return (int)hipGetLastError();
 }

@@ -44,6 +44,7 @@ struct RouteParams {
   float* risk;                 // [H, T, P]
   int32_t* ids;                // [H, T, C] or null
   uint8_t* mask;               // [H, T, P] or null
+  float* lse;                  // [H, T, 16] LSE of each probe over all reps (natural log), or null
   int H, T, P, HP, C, mode, total;
 };
 
@@ -191,6 +192,8 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) DEN += s.part[w][pi][1] * __builtin_amdgcn_exp2f(s.part[w][pi][0] - MX);
   const float inv_den = 1.0f / DEN;
+  if (p.lse && wave == 0 && hh == 0 && t0 + blk < p.T)
+    p.lse[((long long)h * p.T + t0 + blk) * 16 + m] = (MX + __log2f(DEN)) * 0.69314718055994531f;
   const float bmax = fmaxf(fmaxf(s.bmax_w[0], s.bmax_w[1]), fmaxf(s.bmax_w[2], s.bmax_w[3]));
   const float th0 = p.theta[h * 4 + 0], th1 = p.theta[h * 4 + 1], th2 = p.theta[h * 4 + 2], th3 = p.theta[h * 4 + 3];
 
@@ -349,8 +352,8 @@ extern "C" {
 // 2 fixed top-C with own forced.
 int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
-              const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, int heads, int blocks, int pages,
-              int head_pages, int count, int mode, int total, hipStream_t stream) {
+              const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
+              int pages, int head_pages, int count, int mode, int total, hipStream_t stream) {
   if (heads <= 0 || blocks <= 0 || pages <= 0 || pages > kMaxPages || head_pages < pages || mode < -1 ||
       mode > 2)
     return (int)hipErrorInvalidValue;
@@ -372,6 +375,7 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
   p.risk = risk;
   p.ids = ids;
   p.mask = mask;
+  p.lse = lse;
   p.H = heads;
   p.T = blocks;
   p.P = pages;

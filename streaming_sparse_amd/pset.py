@@ -22,6 +22,7 @@ COEF_A = 96
 CAND = 48
 CAND_VALS = 34
 ROW_VALS = 52
+ROW_SPLIT = 4          # page ranges per pair of query blocks in the rows kernel
 POOL_INTS = 64
 
 
@@ -103,12 +104,14 @@ def encode(summary: Summary, basis: torch.Tensor, reader: Reader, out: Encoding 
 
 
 @torch.no_grad()
-def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, mask, ids, own, heads,
+def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, lse, mask, ids, own, heads,
             workspace=None, want_scores=False):
     """Full_Pset correction of the scoped `heads` in place on `mask` (uint8 or
-    bool storage, [H,T,P]) and `ids` [H,T,C] from the intersection router.
-    q [1,N,H,128] bf16 (probe rows at the reference offsets).  Returns
-    (stats int64 [3] = executed, rows, non-finite scores; per-row dict)."""
+    bool storage, [H,T,P]) and `ids` [H,T,C] from the intersection router,
+    whose `risk` and per-probe `lse` ([H,T,16], route(..., lse_out=...)) it
+    reads.  q [1,N,H,128] bf16 (probe rows at the reference offsets).
+    Returns (stats int64 [3] = executed, rows, non-finite scores; per-row
+    dict)."""
     _, nq, h, d = q.shape
     t = nq // 64
     p = risk.shape[-1]
@@ -127,6 +130,8 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, mask,
     hp = _summary_ok(summary)
     if encoding.coef.shape[1] < p:
         raise ValueError("encoding does not cover the window")
+    if lse is None or lse.shape != (h, t, 16) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("lse must be the router's contiguous [H,T,16] float32 probe log-sum-exp")
 
     def buf(name, shape, dtype):
         if workspace is None:
@@ -134,7 +139,7 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, mask,
         return workspace.tensor('pset_' + name, shape, dev, dtype)
 
     cand = buf('cand', (n, t, 16, CAND, CAND_VALS), torch.float64)
-    rows = buf('rows', (n, t, 16, ROW_VALS), torch.float64)
+    rows = buf('rows', (n, t, 16, ROW_SPLIT, ROW_VALS), torch.float64)
     pool = buf('pool', (n, t, POOL_INTS), torch.int32)
     gain = buf('gain', (n, t), torch.float64)
     info = buf('info', (n, t, 3), torch.int32)
@@ -144,7 +149,7 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, mask,
     _lib.check(_lib.lib().ssa_pset(
         _lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys), hp, _lib.ptr(encoding.coef),
         _lib.ptr(encoding.mean), _lib.ptr(encoding.detail), encoding.coef.shape[1], _lib.ptr(reader.wq),
-        _lib.ptr(risk), _lib.ptr(mask_u8), _lib.ptr(ids), _lib.ptr(ow), _lib.ptr(hs), n, _lib.ptr(cand),
+        _lib.ptr(risk), _lib.ptr(lse), _lib.ptr(mask_u8), _lib.ptr(ids), _lib.ptr(ow), _lib.ptr(hs), n, _lib.ptr(cand),
         _lib.ptr(rows), _lib.ptr(pool), _lib.ptr(gain), _lib.ptr(info), _lib.ptr(scores), h, t, p,
         ids.shape[-1], _lib.stream_handle(dev)), "ssa_pset")
     stats = info.sum((0, 1), dtype=torch.int64)

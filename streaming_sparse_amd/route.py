@@ -45,12 +45,13 @@ def tier_count(tier: str, pages: int, n: int | None = None) -> int:
 
 @torch.no_grad()
 def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=None, workspace=None,
-          want_mask=True, full_pset=None, encoding=None, reader=None):
+          want_mask=True, full_pset=None, encoding=None, reader=None, lse_out=None):
     """q [1,N,H,128] bf16 queries of the current chunk; summary over the P
     window pages; theta [H,4]; own [H,T] (default: page P-T+t).  For the
     intersection tier pass current_slots [H] (A per head, >= 1) and n = A+B.
     full_pset: head ids to correct with `encoding` (pset.Encoding over the
-    window) and `reader` (pset.Reader)."""
+    window) and `reader` (pset.Reader).  lse_out: optional [H,T,16] fp32
+    tensor that receives each probe's log-sum-exp over all reps."""
     _, nq, h, d = q.shape
     if d != HEAD_DIM or q.dtype != torch.bfloat16 or not q.is_contiguous():
         raise ValueError("q must be contiguous [1,N,H,128] bf16")
@@ -89,13 +90,18 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
     ids = buf('ids', (h, t, count), torch.int32)
     mask = buf('mask', (h, t, p), torch.uint8) if want_mask else None
     th = theta.float().contiguous()
+    lse = lse_out
+    if lse is None and correcting:
+        lse = buf('lse', (h, t, 16), torch.float32)
+    if lse is not None and (lse.shape != (h, t, 16) or lse.dtype != torch.float32 or not lse.is_contiguous()):
+        raise ValueError("lse_out must be a contiguous [H,T,16] float32 tensor")
     _lib.check(_lib.lib().ssa_route(_lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys),
                                     _lib.ptr(summary.stats), _lib.ptr(th), _lib.ptr(cur), _lib.ptr(ow),
-                                    _lib.ptr(risk), _lib.ptr(ids), _lib.ptr(mask), h, t, p, hp, count, mode, total,
-                                    _lib.stream_handle(dev)), "ssa_route")
+                                    _lib.ptr(risk), _lib.ptr(ids), _lib.ptr(mask), _lib.ptr(lse), h, t, p, hp, count,
+                                    mode, total, _lib.stream_handle(dev)), "ssa_route")
     if correcting:
         from . import pset
-        stats, _ = pset.correct(q, summary, encoding, reader, risk, mask, ids, ow, full_pset, workspace)
+        stats, _ = pset.correct(q, summary, encoding, reader, risk, lse, mask, ids, ow, full_pset, workspace)
     elif workspace is None:
         stats = torch.zeros(3, device=dev, dtype=torch.int64)
     else:

@@ -74,15 +74,20 @@ def test_pset_matches_oracle(device):
     x, w, a, n = inputs()
     g, reader, enc = gpu_encoding(x, w, device)
     ws = Workspace()
+    lse = torch.empty(12, 72, 16, device=device)
     ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='intersection', own=g.own, current_slots=a, n=n,
-                               workspace=ws)
+                               workspace=ws, lse_out=lse)
     mask0 = mask.clone()
     ids0 = ids.clone()
-    stats, rows = pset.correct(g.q, g.summary, enc, reader, risk, mask, ids, g.own, HEADS, want_scores=True)
+    stats, rows = pset.correct(g.q, g.summary, enc, reader, risk, lse, mask, ids, g.own, HEADS, want_scores=True)
     torch.cuda.synchronize()
     # oracle on the same selection, risk and encodings
     pr = ref.probes(x.q)
     z = ref.route_logits(pr, x.summary.keys)
+    want_lse = ref.route_logits(pr, x.summary.keys, torch.float64).flatten(-2).logsumexp(-1)
+    lse_err = float((lse.cpu().double() - want_lse).abs().max())
+    print(f"probe lse max abs err {lse_err:.2e}", flush=True)
+    assert lse_err < 1e-5
     enc_o = dict(co=enc.co.cpu(), A=enc.A.cpu(), mean=enc.mean.cpu(), detail=enc.detail.cpu())
     m0 = mask0.cpu()
     want_mask, orow, ostats = opset.correct(pr.bfloat16().float(), z, risk.cpu(), m0, x.own, enc_o, w['wq'], HEADS)
