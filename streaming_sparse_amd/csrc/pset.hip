@@ -114,6 +114,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
     for (int i = 0; i < kEncPages; ++i) ar[i] = ap[i] = 0.f;
     const float* wr = p.w1t + tid;
     const float* wp = p.w1t + H + tid;
+#pragma unroll 8
     for (int k = 0; k < kFeatures; ++k) {
       const float a = wr[(long long)k * 2 * H], b = wp[(long long)k * 2 * H];
       const f32x4 x0 = *reinterpret_cast<const f32x4*>(&f[k][0]);
@@ -380,8 +381,22 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
     const int tb = min(t0 + (pr >> 4), p.T - 1);
     const long long rr = p.gathered ? (pr & 15) : kProbeOffsets[pr & 15];
     const uint16_t* qq = p.q + (long long)h * p.q_head + (long long)tb * p.q_block + rr * p.q_row;
+    const f32x4* wr = reinterpret_cast<const f32x4*>(p.wq + i * 128);
+    u32x4 qv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) qv[c] = ldg16(qq + 8 * c);
     float acc = 0.f;
-    for (int d = 0; d < 128; ++d) acc = fmaf(bf16_to_f32(qq[d]), p.wq[i * 128 + d], acc);
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const f32x4 w0 = wr[2 * c], w1 = wr[2 * c + 1];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        acc = fmaf(bf16_lo(qv[c][k]), w0[2 * k], acc);
+        acc = fmaf(bf16_hi(qv[c][k]), w0[2 * k + 1], acc);
+        acc = fmaf(bf16_lo(qv[c][2 + k]), w1[2 * k], acc);
+        acc = fmaf(bf16_hi(qv[c][2 + k]), w1[2 * k + 1], acc);
+      }
+    }
     s.u[pr][i] = acc;
     if (i == 0) s.L[pr] = p.lse[((long long)h * p.T + tb) * 16 + (pr & 15)];
   }
@@ -415,7 +430,11 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
       const int pl = lane >> 3, c = lane & 7;
       const int page = min(tile * 8 + pl, P - 1);
       const uint16_t* cf = p.coef + ((long long)h * p.EP + page) * kCoefStride + 16 * c;
+      const double* src = c < 2 ? p.mean_b + ((long long)h * p.EP + page) * 16 + 8 * c
+                                 : p.detail_b + ((long long)h * p.EP + page) * 48 + 8 * (c - 2);
       const u32x4 a = ldg16(cf), b = ldg16(cf + 8);
+      const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+      const u32x4 m0 = s4[0], m1 = s4[1], m2 = s4[2], m3 = s4[3];
       float* d = cw + pl * 128 + 16 * c;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -424,11 +443,11 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
         d[8 + 2 * k] = bf16_lo(b[k]);
         d[8 + 2 * k + 1] = bf16_hi(b[k]);
       }
-      const double* src = c < 2 ? p.mean_b + ((long long)h * p.EP + page) * 16 + 8 * c
-                                 : p.detail_b + ((long long)h * p.EP + page) * 48 + 8 * (c - 2);
-      double* md = mw + pl * 64 + 8 * c;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) md[k] = src[k];
+      u32x4* md = reinterpret_cast<u32x4*>(mw + pl * 64 + 8 * c);
+      md[0] = m0;
+      md[1] = m1;
+      md[2] = m2;
+      md[3] = m3;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -546,37 +565,21 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
 // --------------------------------------------------------------- scores ----
 
 struct ScoreSmem {
-  double cand[4][kCand][kCandVals];      // per wave: one probe's candidate endpoints
-  double V[4][kCand][16];                // endpoint vectors D(c - H) + e^(e-M) rp
+  alignas(16) double cand[4][kCand][kCandVals];   // per wave: one probe's candidate endpoints
+  double V[4][16][kCand];                // endpoint vectors D(c - H) + e^(e-M) rp, [dim][candidate]
   double S[4][kCand];                    // S_r (removes) / T_a (adds), shifted by the row max
+  double ex[4][kCand][2];                // e^(lm+beta-M), e^(lm-M) of each candidate
   double Hs[4][48];                      // H[16] | E[16] | ob[16] of the probe
   double sc[4][3];                       // B, shift M, unused
   double acc[4][512];
+  alignas(16) double part[4][kSplit * kRowPart];   // the probe's split row partials
   uint32_t legal[16];
-  int page[kCand];
+  int page[kMaxPages];                   // pool pages, then the compacted selection
   float risk[kMaxPages];
   uint8_t sel[kMaxPages];
   double best[4];
   int besti[4], bad[4];
 };
-
-// Leave-one-out mixture fallback: the mixture after the swap (remove i, add
-// j) built from the background and every candidate, minus H.
-__device__ __noinline__ double fallback_delta(const ScoreSmem& s, int w, int i, int j, int e, double B, double M) {
-  const double* Hw = s.Hs[w];
-  double nw = B * Hw[32 + e];
-  for (int k = 0; k < 16; ++k) {
-    const double* c = s.cand[w][k];
-    const double em = exp(c[0] - M);
-    nw += k == i ? em * c[2 + e] : exp(c[0] + c[1] - M) * (c[2 + e] + c[18 + e]);
-  }
-  for (int k = 16; k < kCand; ++k) {
-    const double* c = s.cand[w][k];
-    nw += k == 16 + j ? exp(c[0] + c[1] - M) * (c[2 + e] + c[18 + e]) : exp(c[0] - M) * c[2 + e];
-  }
-  const double den = s.S[w][i] + s.S[w][16 + j];
-  return nw / den - Hw[e];
-}
 
 // One workgroup per scoped (head, block); wave w takes probes w, w+4, ...
 // With every log mass shifted by the row max M, e^(-den) of a swap is
@@ -602,14 +605,35 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
   for (int i = lane; i < 512; i += 64) s.acc[w][i] = 0.0;
   for (int m = w; m < 16; m += 4) {
     // stage the probe's candidates and row state
-    const double* cd = p.cand + (rowbase * 16 + m) * kCand * kCandVals;
-    for (int i = lane; i < kCand * kCandVals; i += 64) (&s.cand[w][0][0])[i] = cd[i];
-    const double* rs = p.rows + (rowbase * 16 + m) * kSplit * kRowPart;
-    double aH = 0.0, aT = 0.0, aB = 0.0, zH = 0.0, zT = 0.0, zB = 0.0, lx = -INFINITY;
+    {
+      // 48 x 34 doubles = 816 16-byte chunks: all loads in flight, then stores
+      const u32x4* cd = reinterpret_cast<const u32x4*>(p.cand + (rowbase * 16 + m) * kCand * kCandVals);
+      u32x4 v[13];
+#pragma unroll
+      for (int k = 0; k < 13; ++k) v[k] = cd[min(lane + 64 * k, 815)];
+      u32x4* dst = reinterpret_cast<u32x4*>(&s.cand[w][0][0]);
+#pragma unroll
+      for (int k = 0; k < 13; ++k) {
+        const int c = lane + 64 * k;
+        if (c < 816) dst[c] = v[k];
+      }
+    }
+    {
+      // kSplit x 52 doubles = 104 16-byte chunks
+      const u32x4* rs = reinterpret_cast<const u32x4*>(p.rows + (rowbase * 16 + m) * kSplit * kRowPart);
+      const u32x4 r0 = rs[lane], r1 = rs[min(64 + lane, 103)];
+      u32x4* dst = reinterpret_cast<u32x4*>(s.part[w]);
+      dst[lane] = r0;
+      if (lane < 40) dst[64 + lane] = r1;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane < 16) {
+      double aH = 0.0, aT = 0.0, aB = 0.0, zH = 0.0, zT = 0.0, zB = 0.0, lx = -INFINITY;
 #pragma unroll
       for (int k = 0; k < kSplit; ++k) {
-        const double* r = rs + k * kRowPart;
+        const double* r = s.part[w] + k * kRowPart;
         aH += r[lane];
         aT += r[16 + lane];
         aB += r[32 + lane];
@@ -638,44 +662,72 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
       const double EX = exp(lmk + bk - M), LM = exp(lmk - M);
       const double D = fabs(bk) < 0.5 ? LM * expm1(fmin(fmax(bk, -0.5), 0.5)) : EX - LM;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s.V[w][lane][e] = D * (c[2 + e] - s.Hs[w][e]) + EX * c[18 + e];
+      for (int e = 0; e < 16; ++e) s.V[w][e][lane] = D * (c[2 + e] - s.Hs[w][e]) + EX * c[18 + e];
+      s.ex[w][lane][0] = EX;
+      s.ex[w][lane][1] = LM;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < kCand) {
+      // leave-one-out sums over the other candidates of the same group
       double loo = 0.0;
       if (lane < 16) {
         for (int k = 0; k < 16; ++k)
-          if (k != lane) loo += exp(s.cand[w][k][0] + s.cand[w][k][1] - M);
-        s.S[w][lane] = B + loo + LM;
+          if (k != lane) loo += s.ex[w][k][0];
+        s.S[w][lane] = B + loo + s.ex[w][lane][1];
       } else {
         for (int k = 16; k < kCand; ++k)
-          if (k != lane) loo += exp(s.cand[w][k][0] - M);
-        s.S[w][lane] = loo + EX;
+          if (k != lane) loo += s.ex[w][k][1];
+        s.S[w][lane] = loo + s.ex[w][lane][0];
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t badmask = 0u;
 #pragma unroll 1
     for (int q = 0; q < 8; ++q) {
       const int pr = lane + 64 * q, i = pr >> 5, j = pr & 31;
       const double den = s.S[w][i] + s.S[w][16 + j];
       const double inv = 1.0 / den;
-      double delta[16];
+      double ed = 0.0, dd = 0.0;
       bool finite = isfinite(inv);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        delta[e] = (s.V[w][16 + j][e] - s.V[w][i][e]) * inv;
-        finite = finite && isfinite(delta[e]);
+        const double d = (s.V[w][e][16 + j] - s.V[w][e][i]) * inv;
+        finite = finite && isfinite(d);
+        ed += s.Hs[w][16 + e] * d;
+        dd += d * d;
       }
       // the reference's "bad" branch: max logs - den > 80, or a non-finite delta
-      if (den < 1.8048513878454153e-35 || !finite) {
-        for (int e = 0; e < 16; ++e) delta[e] = fallback_delta(s, w, i, j, e, B, M);
+      if (den < 1.8048513878454153e-35 || !finite) badmask |= 1u << q;
+      else s.acc[w][pr] += 2.0 * ed - dd;
+    }
+    if (__any(badmask != 0u)) {
+      // rare: the mixture after the swap rebuilt from the background and every
+      // candidate (VR/scores.py:75-79), minus H
+#pragma unroll 1
+      for (int q = 0; q < 8; ++q) {
+        if (!((badmask >> q) & 1u)) continue;
+        const int pr = lane + 64 * q, i = pr >> 5, j = pr & 31;
+        const double den = s.S[w][i] + s.S[w][16 + j];
+        double ed = 0.0, dd = 0.0;
+#pragma unroll 1
+        for (int e = 0; e < 16; ++e) {
+          double nw = B * s.Hs[w][32 + e];
+#pragma unroll 1
+          for (int k = 0; k < kCand; ++k) {
+            const double* c = s.cand[w][k];
+            const bool exact = k < 16 ? k != i : k == 16 + j;      // selected after the swap
+            nw += exact ? s.ex[w][k][0] * (c[2 + e] + c[18 + e]) : s.ex[w][k][1] * c[2 + e];
+          }
+          const double d = nw / den - s.Hs[w][e];
+          ed += s.Hs[w][16 + e] * d;
+          dd += d * d;
+        }
+        s.acc[w][pr] += 2.0 * ed - dd;
       }
-      double ed = 0.0, dd = 0.0;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        ed += s.Hs[w][16 + e] * delta[e];
-        dd += delta[e] * delta[e];
-      }
-      s.acc[w][pr] += 2.0 * ed - dd;
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -740,17 +792,31 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
     p.mask[base + apg] = 1;
   }
   __syncthreads();
-  // LUT of the new selection: own first, then descending risk, ties -> lower page
+  // LUT of the new selection: own first, then the other selected pages by
+  // descending risk, ties -> lower page (compact list, then rank within it)
   if (!p.ids) return;
   const int own = own_page(p, h, t);
   int32_t* ids = p.ids + ((long long)h * p.T + t) * p.C;
+  if (w == 0) {
+    int cnt = 0;
+    for (int base = 0; base < P; base += 64) {
+      const int pg = base + lane;
+      const bool on = pg < P && s.sel[pg] && pg != own;
+      const unsigned long long bal = __ballot(on);
+      if (on) s.page[cnt + __popcll(bal & ((1ull << lane) - 1ull))] = pg;   // pool pages no longer needed
+      cnt += __popcll(bal);
+    }
+    if (lane == 0) s.besti[0] = cnt;
+  }
+  __syncthreads();
+  const int nsel = s.besti[0];
   if (tid == 0) ids[0] = own;
-  for (int x = tid; x < P; x += 256) {
-    if (!s.sel[x] || x == own) continue;
+  for (int i = tid; i < nsel; i += 256) {
+    const int x = s.page[i];
     const uint32_t kx = orderable(s.risk[x]);
     int rank = 0;
-    for (int y = 0; y < P; ++y) {
-      if (!s.sel[y] || y == own) continue;
+    for (int k = 0; k < nsel; ++k) {
+      const int y = s.page[k];
       const uint32_t ky = orderable(s.risk[y]);
       rank += (ky > kx) || (ky == kx && y < x);
     }
