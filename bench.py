@@ -9,8 +9,9 @@ inputs, all resident in HBM.
 Also measured in the same run:
 * the intersection tier: 24 anchors + A current + B history pages per head,
   (A, B) from a seeded per-(step, layer, head) quota table;
-* the same with the Full_Pset swap correction on heads {3, 4, 9}, plus the
-  encodings of the 72 current pages x 12 heads that a denoise step refreshes;
+* the same with the Full_Pset swap correction on heads {3, 4, 9}, plus what a
+  denoise step refreshes first: the summaries (4-iteration k-means) and the
+  encodings of the 72 current pages x 12 heads;
 * torch's dense scaled_dot_product_attention over the whole window.
 
 Prints ONE JSON line; `value` is ms per call (lower is better).  The
@@ -204,7 +205,7 @@ def intersection_lines(args, dense_ms, iters):
     table) and the same call with Full_Pset on heads {3,4,9} plus the
     current-page encodings."""
     import torch
-    from streaming_sparse_amd import pset, workload
+    from streaming_sparse_amd import pset, summary, workload
     from streaming_sparse_amd.attention import Workspace
     from streaming_sparse_amd.legacy_components import attention
     from streaming_sparse_amd.route import route
@@ -222,6 +223,8 @@ def intersection_lines(args, dense_ms, iters):
     ws = Workspace()
     reader = pset.Reader(workload.reader_weights(), dev)
     enc = pset.encode(g.summary, basis, reader)
+    init = workload.kmeans_init(12, 72, torch.Generator().manual_seed(workload.seed_for(2, 3, 0, 9))).to(dev)
+    recompute = lambda: summary.build(g.k, g.v, basis, init, g.summary, P - 72, 72)
 
     def plain():
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
@@ -229,6 +232,7 @@ def intersection_lines(args, dense_ms, iters):
         return attention(g.q, g.k, g.v, g.summary, basis, ids, ws)
 
     def corrected():
+        recompute()
         pset.encode(g.summary, basis, reader, out=enc, first=P - 72, pages=72)
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
                              full_pset=PSET_HEADS, encoding=enc, reader=reader)
@@ -252,6 +256,7 @@ def intersection_lines(args, dense_ms, iters):
     ids, mask, risk, _ = route_i()
     out["pset_correction_ms"] = round(time_loop(
         lambda: pset.correct(g.q, g.summary, enc, reader, risk, lse, mask, ids, None, PSET_HEADS, ws), iters, stream), 4)
+    out["summary_current_72x12_ms"] = round(time_loop(recompute, iters, stream), 4)
     out["encode_current_72x12_ms"] = round(time_loop(
         lambda: pset.encode(g.summary, basis, reader, out=enc, first=P - 72, pages=72), iters, stream), 4)
     out["full_pset_heads"] = list(PSET_HEADS)

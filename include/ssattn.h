@@ -21,6 +21,9 @@
  *                      VR/legacy_components.py:14-22 risk(probes,z,summary,theta)
  *   ssa_encode      <- VR/page.py:6-14 encode(summary,reader,phi,B) and
  *                      VideoRuntime.encode (VR/runtime.py:160-164)
+ *   ssa_summary     <- the current-chunk summary recompute of VideoRuntime.forward
+ *                      (VR/runtime.py:213-227; VR/summary_moments.py:113-137), with
+ *                      k-means clusters as the token groups of RV/ops.py:43-76
  *   ssa_pset        <- the Full_Pset branch of BatchGraphs.compute
  *                      (VB/graph.py:169-208): quota_pool.pool, read /
  *                      compact_scores (VR/page.py:17-21, VR/reader_reduce.py:150-190,
@@ -75,6 +78,16 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
               int pages, int head_pages, int count, int mode, int total, hipStream_t stream);
+
+/* Page summaries of pages [first_page, first_page + pages) of the resident
+ * cache (k, v addressed as in ssa_attention): a 4-way k-means of each page's
+ * 64 keys from init [H, pages, 4] (token indices 0..63), `iters` >= 1 Lloyd
+ * iterations (ties -> lower cluster), then keys [H,head_pages,4,128], mean
+ * [H,head_pages,128], detail [H,head_pages,3,8], stats [H,head_pages,4,12]
+ * (bf16) of those pages, with basis [H,128,8] bf16. */
+int ssa_summary(const void* k, const void* v, long long kv_token_stride, long long kv_head_stride,
+                const int32_t* init, const void* basis, void* keys, void* mean, void* detail, void* stats,
+                int head_pages, int heads, int first_page, int pages, int iters, hipStream_t stream);
 
 /* Full_Pset page encodings of pages [first_page, first_page + pages) of the
  * summary slab (keys/mean/detail/stats as in ssa_route, capacity head_pages):

@@ -1,0 +1,46 @@
+"""Current-chunk page summaries on the HIP library (4-iteration k-means reps,
+V mean, Haar/rank-8 detail, routing stats), written into a summary slab.
+
+The reference recomputes the current chunk's summaries on every denoise
+input (local_experiments/video_runtime_v1/runtime.py:213-227, fused kernels in
+local_experiments/video_runtime_v1/summary_moments.py:113-137) and writes them
+into its [H, Pcap, ...] slabs; ``build`` does the same for pages
+[first, first + pages) of the resident K/V cache.  Nothing here computes on
+the CPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .legacy_components import HEAD_DIM, kv_strides
+from .ops import Summary
+
+
+@torch.no_grad()
+def build(k, v, basis, init, out: Summary, first: int, pages: int, iters: int = 4) -> Summary:
+    """k, v [1, 64P, H, 128] bf16 cache; basis [H,128,8]; init [H, pages, 4]
+    initial k-means tokens (0..63) per page; out: a summary slab (or prefix
+    slice) whose pages [first, first + pages) are overwritten."""
+    _, L, h, d = k.shape
+    if d != HEAD_DIM or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or k.shape != v.shape:
+        raise ValueError("k, v must be bf16 [1, 64P, H, 128]")
+    if first < 0 or pages <= 0 or (first + pages) * 64 > L:
+        raise ValueError("page range outside the K/V window")
+    hp = out.head_pages
+    for name, t, inner in (('keys', out.keys, 512), ('mean', out.mean, 128), ('detail', out.detail, 24),
+                           ('stats', out.stats, 48)):
+        if t.dtype != torch.bfloat16 or t.shape[0] != h or t.stride(0) != hp * inner or not t[0].is_contiguous():
+            raise ValueError(f"out.{name} must be a page slice of a contiguous bf16 [H,Pcap,...] slab")
+        if first + pages > t.shape[1]:
+            raise ValueError(f"out.{name} does not cover pages [{first}, {first + pages})")
+    ini = init if (init.dtype == torch.int32 and init.is_contiguous()) else init.to(torch.int32).contiguous()
+    if ini.shape != (h, pages, 4):
+        raise ValueError("init must be [H, pages, 4]")
+    b = basis if (basis.dtype == torch.bfloat16 and basis.is_contiguous()) else basis.to(torch.bfloat16).contiguous()
+    tok, head = kv_strides(k, v)
+    _lib.check(_lib.lib().ssa_summary(_lib.ptr(k), _lib.ptr(v), tok, head, _lib.ptr(ini), _lib.ptr(b),
+                                      _lib.ptr(out.keys), _lib.ptr(out.mean), _lib.ptr(out.detail),
+                                      _lib.ptr(out.stats), hp, h, first, pages, iters,
+                                      _lib.stream_handle(k.device)), "ssa_summary")
+    return out

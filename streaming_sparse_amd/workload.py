@@ -90,11 +90,18 @@ def pca_basis(v_pages: torch.Tensor, rank: int = 8) -> torch.Tensor:
     return (basis * sign).float()
 
 
+def kmeans_init(heads: int, pages: int, generator: torch.Generator) -> torch.Tensor:
+    """Seeded distinct initial tokens [H, P, 4] (int64) of each page's 4-way
+    k-means."""
+    return torch.rand(heads * pages, 64, generator=generator).argsort(-1)[:, :4].reshape(heads, pages, 4)
+
+
 def kmeans_summaries(k: torch.Tensor, v: torch.Tensor, basis: torch.Tensor,
-                     generator: torch.Generator, iters: int = 4) -> Summary:
+                     generator, iters: int = 4) -> Summary:
     """Page summaries from a seeded 4-way k-means of each page's 64 keys.
 
-    k, v: [H, P, 64, D] (bf16-rounded values); basis [H, D, 8].
+    k, v: [H, P, 64, D] (bf16-rounded values); basis [H, D, 8]; generator: a
+    torch.Generator for kmeans_init, or the [H, P, 4] initial tokens.
     Reps are the cluster key means re-centred so their mean equals the page key
     mean (local_experiments/review_v1/ops.py:60); detail is the Haar contrast of
     cluster V means projected on the bf16 basis (ops.py:63-64); stats use each
@@ -107,7 +114,7 @@ def kmeans_summaries(k: torch.Tensor, v: torch.Tensor, basis: torch.Tensor,
     kb = kf.reshape(B, T, D)
     vb = vf.reshape(B, T, D)
     # seeded distinct initial tokens per page
-    init = torch.rand(B, T, generator=generator).argsort(-1)[:, :4]
+    init = (generator if isinstance(generator, torch.Tensor) else kmeans_init(H, P, generator)).reshape(B, 4)
     cent = kb.gather(1, init[..., None].expand(-1, -1, D)).clone()
     assign = None
     for _ in range(iters):

@@ -1,0 +1,45 @@
+"""Current-chunk summary recompute on the HIP path vs. the oracle
+(oracle/summary.py) on identical seeded inputs: the 72 current pages x 12
+heads of a 432-page window, written into the window's summary slab.
+
+Bar: outputs bit-exact except one-ulp bf16 roundings (fp32 accumulation
+order), on every page whose k-means has no near tie (best and second-best
+centroid distance within 1e-5 relative in some iteration)."""
+import pytest
+import torch
+
+from oracle import summary as osum
+from streaming_sparse_amd import summary, workload
+from streaming_sparse_amd.ops import Summary
+
+pytestmark = pytest.mark.gpu
+
+
+def test_current_chunk_summaries_match_oracle(device):
+    x = workload.make_call(cfg=3, frames=18)
+    P = x.pages
+    g = x.to(device)
+    init = workload.kmeans_init(12, 72, torch.Generator().manual_seed(workload.seed_for(3, 1, 0, 9)))
+    slab = Summary(*(getattr(g.summary, f).clone() for f in Summary.FIELDS))
+    for f in Summary.FIELDS:
+        getattr(slab, f)[:, P - 72:].zero_()
+    summary.build(g.k, g.v, g.basis, init.to(device), slab, P - 72, 72)
+    torch.cuda.synchronize()
+    kp = x.k[0].transpose(0, 1).reshape(12, P, 64, 128)[:, P - 72:]
+    vp = x.v[0].transpose(0, 1).reshape(12, P, 64, 128)[:, P - 72:]
+    want = osum.summaries(kp, vp, x.basis, init)
+    ok = want['margin'] > 1e-5
+    print(f"{int(ok.sum())}/{ok.numel()} pages without a k-means near tie", flush=True)
+    assert int(ok.sum()) >= ok.numel() * 0.95
+    for name in ('keys', 'mean', 'detail', 'stats'):
+        got = getattr(slab, name)[:, P - 72:].cpu().float()[ok]
+        ref = want[name].float()[ok]
+        err = (got - ref).abs()
+        bound = ref.abs() * 2.0 ** -7 + 1e-6
+        diff = int((got != ref).sum())
+        print(f"{name}: {diff} of {ref.numel()} values differ, max abs {float(err.max()):.2e}", flush=True)
+        assert bool((err <= bound).all()), name
+        assert diff <= ref.numel() * 1e-3, name
+    # pages outside the range are untouched
+    for f in Summary.FIELDS:
+        assert torch.equal(getattr(slab, f)[:, :P - 72].cpu(), getattr(x.summary, f)[:, :P - 72])
