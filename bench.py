@@ -44,6 +44,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the intersection / Full_Pset lines")
+    ap.add_argument("--no-chunk", action="store_true", help="skip the per-chunk 30-layer line")
     ap.add_argument("--cpu-sample-blocks", type=int, default=4)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (scales rocprof FETCH/WRITE_SIZE)")
@@ -153,6 +154,8 @@ def main():
         dense_ms = time_loop(dense, max(5, iters // 5), stream)
 
     extra = None if args.no_extra else intersection_lines(args, dense_ms, iters)
+    if extra is not None and not args.no_chunk:
+        extra["chunk"] = chunk_line(args)
 
     # algorithmic work of the fused kernel (exact + compensation), per call
     exact_flop = 4.0 * N * H * D * 64 * C
@@ -261,6 +264,33 @@ def intersection_lines(args, dense_ms, iters):
         lambda: pset.encode(g.summary, basis, reader, out=enc, first=P - 72, pages=72), iters, stream), 4)
     out["full_pset_heads"] = list(PSET_HEADS)
     return out
+
+
+def chunk_line(args, chunks=2):
+    """Total attention time of one 3-frame chunk of a 30-layer stack: 4
+    denoise steps (layer 0 dense, layers 1-29 intersection route, Full_Pset on
+    layers {3,4,5,8,14,17,27} x heads {3,4,9} at step 0, current-page
+    summaries each call) and the dense clean commit pass, against the same
+    chunk fully dense (this library's kernel with every page exact, and
+    torch scaled_dot_product_attention)."""
+    import torch
+    from streaming_sparse_amd.runtime import ChunkConfig, ChunkRuntime
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    t0 = time.time()
+    rt = ChunkRuntime(ChunkConfig(frames=args.frames), dev)
+    setup_s = time.time() - t0
+    rt.run_chunk()
+    torch.cuda.synchronize()
+    chunk_ms = time_loop(rt.run_chunk, chunks, stream)
+    dense_kernel_ms = time_loop(lambda: rt.run_dense_chunk(False), 1, stream)
+    dense_sdpa_ms = time_loop(lambda: rt.run_dense_chunk(True), 1, stream)
+    calls = rt.calls_per_chunk()
+    return {"workload": "30 layers x (4 denoise steps + clean commit), 432-page window, 12 heads",
+            "calls": calls, "chunk_ms": round(chunk_ms, 3),
+            "dense_chunk_ms_this_kernel": round(dense_kernel_ms, 3),
+            "dense_chunk_ms_sdpa": round(dense_sdpa_ms, 3),
+            "ratio_vs_dense_sdpa": round(chunk_ms / dense_sdpa_ms, 4), "setup_s": round(setup_s, 2)}
 
 
 def cpu_baseline(x, count, blocks):
