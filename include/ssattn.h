@@ -115,14 +115,16 @@ int ssa_encode(const void* keys, const void* mean, const void* detail, const voi
  * n_heads*blocks*16*4*52 fp64, pool n_heads*blocks*64 int32.  Per-row outputs:
  * gain [n_heads,blocks] fp64, info [n_heads,blocks,3] int32 = (executed, best
  * pair index remove*32+add, non-finite legal scores); scores
- * [n_heads,blocks,16,32] fp64 (illegal pairs -1e30) or NULL.
+ * [n_heads,blocks,16,32] fp64 (illegal pairs -1e30) or NULL; stats [3]
+ * int64 = (executed swaps, corrected rows, non-finite legal scores),
+ * overwritten.
  * Requires 96 < pages <= 512 and pages - count >= 64. */
 int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
              int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
              const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,
              uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand,
-             double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, int total_heads, int blocks,
-             int pages, int count, hipStream_t stream);
+             double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
+             int total_heads, int blocks, int pages, int count, hipStream_t stream);
 
 #ifdef __cplusplus
 }

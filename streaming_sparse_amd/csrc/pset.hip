@@ -198,6 +198,7 @@ struct PsetParams {
   double* gain;
   int32_t* info;
   double* scores;
+  long long* stats;            // [3] executed swaps, corrected rows, non-finite legal scores
   int H, T, P, C;
 };
 
@@ -229,6 +230,7 @@ __global__ __launch_bounds__(256) void pset_pool_kernel(PsetParams p) {
   const int P = p.P;
   const long long rowoff = ((long long)h * p.T + t) * P;
   const int own = own_page(p, h, t);
+  if (blockIdx.x == 0 && tid < 3) p.stats[tid] = tid == 1 ? (long long)p.HS * p.T : 0ll;
   for (int i = tid; i < kMaxPages; i += 256) {
     s.risk[i] = i < P ? p.risk[rowoff + i] : 0.f;
     s.sel[i] = i < P ? (p.mask[rowoff + i] ? 1 : 0) : 1;
@@ -780,6 +782,8 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
     p.info[rowbase * 3 + 0] = exec ? 1 : 0;
     p.info[rowbase * 3 + 1] = besti;
     p.info[rowbase * 3 + 2] = bad;
+    if (exec) atomicAdd((unsigned long long*)&p.stats[0], 1ull);
+    if (bad) atomicAdd((unsigned long long*)&p.stats[2], (unsigned long long)bad);
   }
   if (!exec) return;
   const int rpg = s.page[besti >> 5], apg = s.page[16 + (besti & 31)];
@@ -865,12 +869,12 @@ int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, l
              int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
              const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,
              uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand,
-             double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, int total_heads, int blocks,
-             int pages, int count, hipStream_t stream) {
+             double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
+             int total_heads, int blocks, int pages, int count, hipStream_t stream) {
   if (n_heads <= 0 || n_heads > total_heads || blocks <= 0 || pages > kMaxPages || pages <= kAnchors + kCurrent ||
       head_pages < pages || enc_pages < pages || count < 1 || count > pages || pages - count < 64 ||
       heads == nullptr || probe_lse == nullptr || cand == nullptr || rows == nullptr || pool == nullptr ||
-      gain == nullptr || info == nullptr)
+      gain == nullptr || info == nullptr || stats == nullptr)
     return (int)hipErrorInvalidValue;
   PsetParams p;
   p.q = (const uint16_t*)q;
@@ -898,6 +902,7 @@ int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, l
   p.gain = gain;
   p.info = info;
   p.scores = scores;
+  p.stats = stats;
   p.H = total_heads;
   p.T = blocks;
   p.P = pages;

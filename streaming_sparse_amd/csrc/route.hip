@@ -55,6 +55,7 @@ struct Smem {
   uint8_t sel[2][kMaxPages];
   int list[2][kMaxPages];
   float bmax_w[4];
+  alignas(16) uint16_t stats[kMaxPages * 48];   // the head's page stats, staged once
 };
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -63,15 +64,17 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-__device__ __forceinline__ void rep_logits(const uint16_t* rkh, int tile, int P, int lane, const u32x4 (&qop)[8],
-                                           f32x16& S) {
-  // A operand: rep row tile*32 + lane%32, dims 64*hh + 8*st + [0,8)
+// A operand of a tile of 32 reps (8 pages): rep row tile*32 + lane%32, dims
+// 64*hh + 8*st + [0,8).  Tiles past the window re-read the last rep.
+__device__ __forceinline__ void load_reps(const uint16_t* rkh, int tile, int P, int lane, u32x4 (&av)[8]) {
   const int hh = lane >> 5;
   const int row = min(tile * 32 + (lane & 31), P * 4 - 1);
   const uint16_t* a = rkh + (long long)row * kHeadDim + 64 * hh;
-  u32x4 av[8];
 #pragma unroll
   for (int st = 0; st < 8; ++st) av[st] = ldg16(a + 8 * st);
+}
+
+__device__ __forceinline__ void rep_logits(const u32x4 (&av)[8], const u32x4 (&qop)[8], f32x16& S) {
   S = f32x16{};
 #pragma unroll
   for (int st = 0; st < 8; ++st) S = mfma32(av[st], qop[st], S);
@@ -139,8 +142,22 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   for (int g = 0; g < 8; ++g) qsum += q2[g];
   const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
 
+  // stage the head's page stats in LDS (P x 96 B, all loads in flight)
+  {
+    const u32x4* src = reinterpret_cast<const u32x4*>(p.stats + (long long)h * p.HP * 48);
+    u32x4* dst = reinterpret_cast<u32x4*>(s.stats);
+    const int n16 = P * 6;                        // 16-byte chunks
+    constexpr int kPer = (kMaxPages * 6 + kThreads - 1) / kThreads;
+    u32x4 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) v[k] = src[min(tid + kThreads * k, n16 - 1)];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+      if (tid + kThreads * k < n16) dst[tid + kThreads * k] = v[k];
+  }
+  __syncthreads();
+  const uint16_t* sth = s.stats;
   // per-head bound of the page value norm: max_p stats[p,1,11]
-  const uint16_t* sth = p.stats + (long long)h * p.HP * 48;
   {
     float b = -INFINITY;
     for (int i = tid; i < P; i += kThreads) b = fmaxf(b, bf16_to_f32(sth[i * 48 + 12 + 11]));
@@ -155,9 +172,12 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
 
   // pass 1: max and sum of exp over all reps, per probe
   float mx = -INFINITY, den = 0.f;
+  u32x4 av[8];
+  load_reps(rkh, wave, P, lane, av);
   for (int tile = wave; tile < ntiles; tile += 4) {
     f32x16 S;
-    rep_logits(rkh, tile, P, lane, qop, S);
+    rep_logits(av, qop, S);
+    load_reps(rkh, tile + 4 < ntiles ? tile + 4 : wave, P, lane, av);   // next tile (pass 2's first at the end)
     float tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -200,7 +220,8 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   // pass 2: probabilities -> four features -> theta-weighted value -> probe mean
   for (int tile = wave; tile < ntiles; tile += 4) {
     f32x16 S;
-    rep_logits(rkh, tile, P, lane, qop, S);
+    rep_logits(av, qop, S);
+    if (tile + 4 < ntiles) load_reps(rkh, tile + 4, P, lane, av);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int page = tile * 8 + 2 * j + hh;
@@ -209,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
       uint32_t sw[24];
 #pragma unroll
       for (int c = 0; c < 6; ++c) {
-        const u32x4 v4 = ldg16(sp + 8 * c);
+        const u32x4 v4 = *reinterpret_cast<const u32x4*>(sp + 8 * c);
         sw[4 * c + 0] = v4[0];
         sw[4 * c + 1] = v4[1];
         sw[4 * c + 2] = v4[2];

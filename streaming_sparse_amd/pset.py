@@ -144,15 +144,14 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, lse, 
     gain = buf('gain', (n, t), torch.float64)
     info = buf('info', (n, t, 3), torch.int32)
     scores = buf('scores', (n, t, 16, 32), torch.float64) if want_scores else None
+    stats = buf('stats', (3,), torch.int64)
     mask_u8 = mask.view(torch.uint8) if mask.dtype == torch.bool else mask
     ow = None if own is None else own.to(device=dev, dtype=torch.int32).contiguous()
     _lib.check(_lib.lib().ssa_pset(
         _lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys), hp, _lib.ptr(encoding.coef),
         _lib.ptr(encoding.mean), _lib.ptr(encoding.detail), encoding.coef.shape[1], _lib.ptr(reader.wq),
         _lib.ptr(risk), _lib.ptr(lse), _lib.ptr(mask_u8), _lib.ptr(ids), _lib.ptr(ow), _lib.ptr(hs), n, _lib.ptr(cand),
-        _lib.ptr(rows), _lib.ptr(pool), _lib.ptr(gain), _lib.ptr(info), _lib.ptr(scores), h, t, p,
+        _lib.ptr(rows), _lib.ptr(pool), _lib.ptr(gain), _lib.ptr(info), _lib.ptr(scores), _lib.ptr(stats), h, t, p,
         ids.shape[-1], _lib.stream_handle(dev)), "ssa_pset")
-    stats = info.sum((0, 1), dtype=torch.int64)
-    stats[1] = n * t
     return stats, dict(gain=gain, executed=info[..., 0], argmax=info[..., 1], nonfinite=info[..., 2],
                        scores=scores, pool=pool)
