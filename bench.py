@@ -226,7 +226,8 @@ def intersection_lines(args, dense_ms, iters):
     ws = Workspace()
     reader = pset.Reader(workload.reader_weights(), dev)
     enc = pset.encode(g.summary, basis, reader)
-    init = workload.kmeans_init(12, 72, torch.Generator().manual_seed(workload.seed_for(2, 3, 0, 9))).to(dev)
+    init = workload.kmeans_init(12, 72, torch.Generator().manual_seed(workload.seed_for(2, 3, 0, 9))).to(
+        device=dev, dtype=torch.int32)
     recompute = lambda: summary.build(g.k, g.v, basis, init, g.summary, P - 72, 72)
 
     def plain():

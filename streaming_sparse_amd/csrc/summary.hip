@@ -12,17 +12,19 @@
 // where km_r / vm_r are the cluster key / value means (an empty cluster
 // keeps its centroid and takes the page V mean).
 //
-// One workgroup (256 threads) per (page, head); the page's K and V are
-// staged in LDS as fp32 rows padded to 129 floats (conflict-free column
-// walks).  Distances and the assignment use thread (token, cluster);
-// centroid updates use thread (cluster, dim).
+// One workgroup (256 threads, 4 waves) per (page, head).  Thread (token
+// t = lane, quarter q = wave) keeps dims 32q..32q+31 of its key in registers
+// for the distance passes; the page's K and V are also staged in LDS as bf16
+// pairs for the per-cluster sums, which thread (cluster r = wave, dims
+// 2 lane, 2 lane + 1) accumulates over the cluster's member tokens in
+// ascending token order, from a wave-uniform membership mask.  LDS stays
+// under 40 KB so four workgroups share a CU.
 #include "common.h"
 
 using namespace ssa;
 
 namespace {
 
-constexpr int kStride = 129;
 constexpr float kHaar[3][4] = {{1, 1, -1, -1}, {1, -1, 1, -1}, {1, -1, -1, 1}};
 
 struct SummaryParams {
@@ -35,19 +37,21 @@ struct SummaryParams {
 };
 
 struct SumSmem {
-  float K[64 * kStride];
-  float V[64 * kStride];
-  float cent[4][128];
-  float vm[4][128];
+  // row t = token, 64 words (bf16 pairs); 16 B chunk c of row t sits at
+  // chunk c ^ (t & 15), so both the row-wise 16 B writes and the per-word
+  // column walks are bank-conflict free
+  alignas(16) uint32_t K[64 * 64];
+  alignas(16) uint32_t V[64 * 64];
+  alignas(16) float cent[4][128];
+  union {
+    f32x4 dist[4][64];                 // [quarter][token] partial distances to the 4 centroids
+    float vnp[4][64];                  // [quarter][token] partial |v|^2 (before the first distance pass)
+  } u;
   float kmean[128], vmean[128];
-  float bas[128][8];
   float code[4][8];
-  float det[3][8];
-  float red[4][128];            // scratch per-cluster partials
-  int assign[64];
-  int cnt[4];
-  float vnorm[64];
 };
+
+__device__ __forceinline__ int word(int t, int w) { return t * 64 + (w ^ ((t & 15) << 2)); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -55,193 +59,274 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Word `lane` of up to 4 member tokens of m (removed from m), 0 for absent
+// slots (a bf16 pair of +0, which changes no sum).
+__device__ __forceinline__ void next4(const uint32_t* rows, uint64_t& m, int lane, uint32_t (&w)[4]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    w[u] = 0u;
+    if (m) {
+      const int t = __builtin_ctzll(m);
+      m &= m - 1;
+      w[u] = rows[word(t, lane)];
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p) {
   __shared__ SumSmem s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int pl = blockIdx.x, h = blockIdx.y;
   const int page = p.first + pl;
   const long long base = (long long)page * 64 * p.kv_tok + (long long)h * p.kv_head;
-  // stage K and V (fp32)
-  for (int i = tid; i < 64 * 16; i += 256) {
-    const int t = i >> 4, c = i & 15;
-    const u32x4 a = ldg16(p.k + base + t * p.kv_tok + 8 * c);
-    const u32x4 b = ldg16(p.v + base + t * p.kv_tok + 8 * c);
+  const int d0 = 2 * lane, d1 = 2 * lane + 1;
+  // global reads up front: this thread's key/value quarter, its two basis
+  // rows, the initial token of centroid `wave`
+  const int init_tok = p.init[((long long)h * p.pages + pl) * 4 + wave] & 63;
+  float bas0[8], bas1[8];
+  {
+    const u32x4 b0 = ldg16(p.basis + (long long)h * 1024 + d0 * 8);
+    const u32x4 b1 = ldg16(p.basis + (long long)h * 1024 + d1 * 8);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      s.K[t * kStride + 8 * c + 2 * w] = bf16_lo(a[w]);
-      s.K[t * kStride + 8 * c + 2 * w + 1] = bf16_hi(a[w]);
-      s.V[t * kStride + 8 * c + 2 * w] = bf16_lo(b[w]);
-      s.V[t * kStride + 8 * c + 2 * w + 1] = bf16_hi(b[w]);
+      bas0[2 * w] = bf16_lo(b0[w]);
+      bas0[2 * w + 1] = bf16_hi(b0[w]);
+      bas1[2 * w] = bf16_lo(b1[w]);
+      bas1[2 * w + 1] = bf16_hi(b1[w]);
     }
   }
-  for (int i = tid; i < 128 * 8; i += 256) s.bas[i >> 3][i & 7] = bf16_to_f32(p.basis[(long long)h * 1024 + i]);
-  __syncthreads();
-  const int32_t* ini = p.init + ((long long)h * p.pages + pl) * 4;
-  for (int i = tid; i < 512; i += 256) {
-    const int r = i >> 7, d = i & 127;
-    s.cent[r][d] = s.K[ini[r] * kStride + d];
-  }
-  if (tid < 128) {
-    float ks = 0.f, vs = 0.f;
-    for (int t = 0; t < 64; ++t) {
-      ks += s.K[t * kStride + tid];
-      vs += s.V[t * kStride + tid];
-    }
-    s.kmean[tid] = ks / 64.f;
-    s.vmean[tid] = vs / 64.f;
-  }
-  if (tid < 64) {
-    float n = 0.f;
-    for (int d = 0; d < 128; ++d) n = fmaf(s.V[tid * kStride + d], s.V[tid * kStride + d], n);
-    s.vnorm[tid] = sqrtf(n);
-  }
-  __syncthreads();
-
-  // Lloyd iterations: assign each token to its nearest centroid (ties ->
-  // lower cluster), then move every non-empty centroid to its cluster mean
-  for (int it = 0; it < p.iters; ++it) {
-    {
-      const int t = tid >> 2, r = tid & 3;
-      float dist = 0.f;
-      for (int d = 0; d < 128; ++d) {
-        const float x = s.K[t * kStride + d] - s.cent[r][d];
-        dist = fmaf(x, x, dist);
-      }
-      // argmin over the 4 lanes of this token (lanes 4t..4t+3 of the wave)
-      float best = dist;
-      int bi = r;
-#pragma unroll
-      for (int o = 1; o < 4; o <<= 1) {
-        const float ob = __shfl_xor(best, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ob < best || (ob == best && oi < bi)) {
-          best = ob;
-          bi = oi;
-        }
-      }
-      if (r == 0) s.assign[t] = bi;
-    }
-    __syncthreads();
-    for (int i = tid; i < 512; i += 256) {
-      const int r = i >> 7, d = i & 127;
-      float sum = 0.f;
-      int c = 0;
-      for (int t = 0; t < 64; ++t) {
-        if (s.assign[t] == r) {
-          sum += s.K[t * kStride + d];
-          ++c;
-        }
-      }
-      if (c > 0) s.cent[r][d] = sum / (float)c;
-      if (d == 0) s.cnt[r] = c;
-    }
-    __syncthreads();
-  }
-
-  // cluster V means (empty cluster -> page V mean) and the key variance
-  for (int i = tid; i < 512; i += 256) {
-    const int r = i >> 7, d = i & 127;
-    const int c = s.cnt[r];
-    float sum = 0.f, var = 0.f;
-    for (int t = 0; t < 64; ++t) {
-      if (s.assign[t] == r) {
-        sum += s.V[t * kStride + d];
-        const float x = s.K[t * kStride + d] - s.cent[r][d];
-        var = fmaf(x, x, var);
-      }
-    }
-    s.vm[r][d] = c > 0 ? sum / (float)c : s.vmean[d];
-    s.red[r][d] = var / (float)max(c, 1);
-  }
-  __syncthreads();
-  // code = vm . bf16(basis), detail = bf16(HAAR . code / 4)
-  if (tid < 32) {
-    const int r = tid >> 3, kk = tid & 7;
-    float acc = 0.f;
-    for (int d = 0; d < 128; ++d) acc = fmaf(s.vm[r][d], s.bas[d][kk], acc);
-    s.code[r][kk] = acc;
-  }
-  __syncthreads();
-  const long long pg = (long long)h * p.HP + page;
-  if (tid < 24) {
-    const int a = tid >> 3, kk = tid & 7;
-    const float v = (kHaar[a][0] * s.code[0][kk] + kHaar[a][1] * s.code[1][kk] + kHaar[a][2] * s.code[2][kk] +
-                     kHaar[a][3] * s.code[3][kk]) / 4.f;
-    const uint16_t b = to_bf16(v);
-    s.det[a][kk] = bf16_to_f32(b);
-    p.detail[pg * 24 + tid] = b;
-  }
-  __syncthreads();
-  // wave r handles cluster r: reps, reconstruction error, spreads, stats
+  float kr[32];
   {
-    const int r = wave;
-    float kmm[2], pk[2], rec[2];
-    float e8 = 0.f, e9 = 0.f, gvar[2];
+    const uint16_t* kp = p.k + base + lane * p.kv_tok + 32 * wave;
+    const uint16_t* vp = p.v + base + lane * p.kv_tok + 32 * wave;
+    u32x4 a[4], b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[j] = ldg16(kp + 8 * j);
+      b[j] = ldg16(vp + 8 * j);
+    }
+    float vn = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int chunk = (4 * wave + j) ^ (lane & 15);
+      *reinterpret_cast<u32x4*>(&s.K[lane * 64 + 4 * chunk]) = a[j];
+      *reinterpret_cast<u32x4*>(&s.V[lane * 64 + 4 * chunk]) = b[j];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        kr[8 * j + 2 * w] = bf16_lo(a[j][w]);
+        kr[8 * j + 2 * w + 1] = bf16_hi(a[j][w]);
+        const float x0 = bf16_lo(b[j][w]), x1 = bf16_hi(b[j][w]);
+        vn = fmaf(x0, x0, vn);
+        vn = fmaf(x1, x1, vn);
+      }
+    }
+    s.u.vnp[wave][lane] = vn;
+  }
+  __syncthreads();
+  // initial centroids, page K / V means, max token |v| (wave 1 keeps it)
+  {
+    const uint32_t w = s.K[word(init_tok, lane)];
+    s.cent[wave][d0] = bf16_lo(w);
+    s.cent[wave][d1] = bf16_hi(w);
+  }
+  float vmax = 0.f;
+  if (wave < 2) {
+    const uint32_t* rows = wave == 0 ? s.K : s.V;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll 16
+    for (int t = 0; t < 64; ++t) {
+      const uint32_t w = rows[word(t, lane)];
+      a0 += bf16_lo(w);
+      a1 += bf16_hi(w);
+    }
+    float* dst = wave == 0 ? s.kmean : s.vmean;
+    dst[d0] = a0 / 64.f;
+    dst[d1] = a1 / 64.f;
+  }
+  if (wave == 1) {
+    vmax = sqrtf(((s.u.vnp[0][lane] + s.u.vnp[1][lane]) + s.u.vnp[2][lane]) + s.u.vnp[3][lane]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o));
+  }
+  __syncthreads();
+
+  // Lloyd iterations: assign each token to its nearest centroid (squared
+  // distance, ties -> lower cluster), then move every non-empty centroid to
+  // its cluster mean
+  uint64_t mr = 0;   // member tokens of cluster `wave` (wave-uniform)
+  for (int it = 0; it < p.iters; ++it) {
+    float d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const f32x4 c = *reinterpret_cast<const f32x4*>(&s.cent[r][32 * wave + 4 * j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = kr[4 * j + e] - c[e];
+          d[r] = fmaf(x, x, d[r]);
+        }
+      }
+    }
+    s.u.dist[wave][lane] = f32x4{d[0], d[1], d[2], d[3]};
+    __syncthreads();
+    // every wave: token lane's distances over the 4 quarters, nearest centroid
+    f32x4 tot = s.u.dist[0][lane];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) tot += s.u.dist[q][lane];
+    int best = 0;
+    float bv = tot[0];
+#pragma unroll
+    for (int r = 1; r < 4; ++r) {
+      if (tot[r] < bv) {
+        bv = tot[r];
+        best = r;
+      }
+    }
+    mr = __ballot(best == wave);
+    // thread (cluster wave, dims 2 lane, 2 lane + 1): the new centroid
+    if (mr) {
+      float a0 = 0.f, a1 = 0.f;
+      uint64_t m = mr;
+      while (m) {
+        uint32_t w[4];
+        next4(s.K, m, lane, w);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          a0 += bf16_lo(w[u]);
+          a1 += bf16_hi(w[u]);
+        }
+      }
+      const float c = (float)__popcll(mr);
+      s.cent[wave][d0] = a0 / c;
+      s.cent[wave][d1] = a1 / c;
+    }
+    __syncthreads();
+  }
+
+  // thread (cluster r = wave, dims 2 lane, 2 lane + 1): cluster V mean (empty
+  // cluster -> page V mean), key variance, V spread
+  const int r = wave;
+  const int cnt = __popcll(mr);
+  const float div = (float)max(cnt, 1);
+  const float c0 = s.cent[r][d0], c1 = s.cent[r][d1];
+  float vm0, vm1, var0 = 0.f, var1 = 0.f, spread = 0.f;
+  {
+    float v0 = 0.f, v1 = 0.f;
+    uint64_t mk = mr, mv = mr;
+    while (mk) {
+      uint32_t wk[4], wv[4];
+      const uint64_t m0 = mk;
+      next4(s.K, mk, lane, wk);
+      next4(s.V, mv, lane, wv);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v0 += bf16_lo(wv[u]);
+        v1 += bf16_hi(wv[u]);
+        // absent slots: skip, as (0 - c)^2 is not 0
+        if (u < __popcll(m0)) {
+          const float x0 = bf16_lo(wk[u]) - c0, x1 = bf16_hi(wk[u]) - c1;
+          var0 = fmaf(x0, x0, var0);
+          var1 = fmaf(x1, x1, var1);
+        }
+      }
+    }
+    vm0 = cnt > 0 ? v0 / (float)cnt : s.vmean[d0];
+    vm1 = cnt > 0 ? v1 / (float)cnt : s.vmean[d1];
+    var0 /= div;
+    var1 /= div;
+    uint64_t m = mr;
+    while (m) {
+      const uint64_t m0 = m;
+      uint32_t wv[4];
+      next4(s.V, m, lane, wv);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (u < __popcll(m0)) {
+          const float x0 = bf16_lo(wv[u]) - vm0, x1 = bf16_hi(wv[u]) - vm1;
+          spread = fmaf(x0, x0, fmaf(x1, x1, spread));
+        }
+      }
+    }
+    spread = wave_sum(spread);
+  }
+  // code[r][kk] = vm_r . bf16(basis)[:, kk]
+  {
+    float cd[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) cd[kk] = wave_sum(fmaf(vm1, bas1[kk], vm0 * bas0[kk]));
+    if (lane == 0) {
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) s.code[r][kk] = cd[kk];
+    }
+  }
+  __syncthreads();
+  // detail = bf16(HAAR . code / 4), every wave
+  float det[3][8];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const float v = (kHaar[a][0] * s.code[0][kk] + kHaar[a][1] * s.code[1][kk] + kHaar[a][2] * s.code[2][kk] +
+                       kHaar[a][3] * s.code[3][kk]) / 4.f;
+      det[a][kk] = bf16_to_f32(to_bf16(v));
+    }
+  }
+  const long long pg = (long long)h * p.HP + page;
+  if (wave == 0 && lane < 24) p.detail[pg * 24 + lane] = to_bf16(
+      (kHaar[lane >> 3][0] * s.code[0][lane & 7] + kHaar[lane >> 3][1] * s.code[1][lane & 7] +
+       kHaar[lane >> 3][2] * s.code[2][lane & 7] + kHaar[lane >> 3][3] * s.code[3][lane & 7]) / 4.f);
+  // reps, reconstruction error, stats of cluster r
+  float e8 = 0.f, e9 = 0.f;
+  uint32_t pk_pair;
+  {
+    float pk[2];
+    const float vm[2] = {vm0, vm1};
+#pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int d = lane + 64 * j;
+      const int d = d0 + j;
       const float mk = 0.25f * (((s.cent[0][d] + s.cent[1][d]) + s.cent[2][d]) + s.cent[3][d]);
-      kmm[j] = s.cent[r][d];
-      const uint16_t b = to_bf16(s.cent[r][d] - mk + s.kmean[d]);
-      pk[j] = bf16_to_f32(b);
-      p.keys[(pg * 4 + r) * 128 + d] = b;
+      const float km = s.cent[r][d];
+      pk[j] = bf16_to_f32(to_bf16(km - mk + s.kmean[d]));
       const float mu = bf16_to_f32(to_bf16(s.vmean[d]));
       float acc = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
-        const float c = kHaar[0][r] * s.det[0][kk] + kHaar[1][r] * s.det[1][kk] + kHaar[2][r] * s.det[2][kk];
-        acc = fmaf(c, s.bas[d][kk], acc);
+        const float c = kHaar[0][r] * det[0][kk] + kHaar[1][r] * det[1][kk] + kHaar[2][r] * det[2][kk];
+        acc = fmaf(c, j == 0 ? bas0[kk] : bas1[kk], acc);
       }
-      rec[j] = mu + acc;
-      const float x8 = kmm[j] - pk[j], x9 = s.vm[r][d] - rec[j];
+      const float x8 = km - pk[j], x9 = vm[j] - (mu + acc);
       e8 = fmaf(x8, x8, e8);
       e9 = fmaf(x9, x9, e9);
-      gvar[j] = s.red[r][d];
     }
-    e8 = wave_sum(e8);
-    e9 = wave_sum(e9);
-    // [r, 0:8]: mean of the variance over each 16-dim group (lanes 16g..16g+15
-    // hold dims 16g.. for g < 4, and 64 + 16g.. for g >= 4)
-    float g0 = gvar[0], g1 = gvar[1];
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) {
-      g0 += __shfl_xor(g0, o);
-      g1 += __shfl_xor(g1, o);
-    }
-    // V spread: sqrt(sum_t in cluster |v_t - vm_r|^2 / max(n, 1))
-    float spread = 0.f;
-    for (int t = 0; t < 64; ++t) {
-      if (s.assign[t] != r) continue;
-      const float x0 = s.V[t * kStride + lane] - s.vm[r][lane];
-      const float x1 = s.V[t * kStride + 64 + lane] - s.vm[r][64 + lane];
-      spread = fmaf(x0, x0, fmaf(x1, x1, spread));
-    }
-    spread = wave_sum(spread);
-    uint16_t* st = p.stats + (pg * 4 + r) * 12;
-    if ((lane & 15) == 0) {
-      st[lane >> 4] = to_bf16(g0 / 16.f);
-      st[4 + (lane >> 4)] = to_bf16(g1 / 16.f);
-    }
-    if (lane == 0) {
-      st[8] = to_bf16(sqrtf(e8));
-      st[9] = to_bf16(sqrtf(e9));
-      st[10] = to_bf16(sqrtf(spread / (float)max(s.cnt[r], 1)));
-    }
-    if (lane == 1) {
-      float v11 = 0.f;
-      if (r == 0) {
-        float e = 0.f;
-        for (int d = 0; d < 128; ++d) {
-          const float x = s.vmean[d] - bf16_to_f32(to_bf16(s.vmean[d]));
-          e = fmaf(x, x, e);
-        }
-        v11 = sqrtf(e);
-      } else if (r == 1) {
-        for (int t = 0; t < 64; ++t) v11 = fmaxf(v11, s.vnorm[t]);
-      }
-      st[11] = to_bf16(v11);
-    }
+    pk_pair = pack_bf16(pk[0], pk[1]);
   }
-  if (tid < 128) p.mean[pg * 128 + tid] = to_bf16(s.vmean[tid]);
+  reinterpret_cast<uint32_t*>(p.keys)[(pg * 4 + r) * 64 + lane] = pk_pair;
+  e8 = wave_sum(e8);
+  e9 = wave_sum(e9);
+  // [r, 0:8]: mean of the key variance over each 16-dim group (lanes 8g..8g+7)
+  float gv = var0 + var1;
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) gv += __shfl_xor(gv, o);
+  uint16_t* st = p.stats + (pg * 4 + r) * 12;
+  if ((lane & 7) == 0) st[lane >> 3] = to_bf16(gv / 16.f);
+  // [0, 11] = |mean v - bf16(mean v)|, [1, 11] = max token |v|, [2..3, 11] = 0
+  float v11 = 0.f;
+  if (r == 0) {
+    const float x0 = s.vmean[d0] - bf16_to_f32(to_bf16(s.vmean[d0]));
+    const float x1 = s.vmean[d1] - bf16_to_f32(to_bf16(s.vmean[d1]));
+    v11 = sqrtf(wave_sum(fmaf(x0, x0, x1 * x1)));
+    reinterpret_cast<uint32_t*>(p.mean)[pg * 64 + lane] = pack_bf16(s.vmean[d0], s.vmean[d1]);
+  } else if (r == 1) {
+    v11 = vmax;
+  }
+  if (lane == 0) {
+    st[8] = to_bf16(sqrtf(e8));
+    st[9] = to_bf16(sqrtf(e9));
+    st[10] = to_bf16(sqrtf(spread / div));
+    st[11] = to_bf16(v11);
+  }
 }
 
 }  // namespace

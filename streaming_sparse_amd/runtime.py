@@ -116,7 +116,7 @@ class ChunkRuntime:
         self.q = [[_rope_on_device(torch.randn(self.N, H, D, generator=g, device=dev), cfg.frames - 3, freqs)
                    .to(torch.bfloat16)[None].contiguous() for _ in range(cfg.layers)] for _ in range(cfg.steps + 1)]
         self.init_current = workload.kmeans_init(H, CURRENT, torch.Generator().manual_seed(
-            workload.seed_for(cfg.seed, 0, 0, 9))).to(dev)
+            workload.seed_for(cfg.seed, 0, 0, 9))).to(device=dev, dtype=torch.int32)
         quotas = workload.quota_table(cfg.seed, layers=max(cfg.layers - 1, 1), steps=cfg.steps, heads=H,
                                       mean_total=cfg.quota_mean)
         self.quota_a = quotas[..., 0].to(torch.int32).to(dev)           # [steps, layers-1, H]

@@ -17,6 +17,11 @@ from .legacy_components import HEAD_DIM, kv_strides
 from .ops import Summary
 
 
+# field -> (inner shape, page / inner strides) of a contiguous [H, Pcap, ...] bf16 slab
+_SLAB = (('keys', (4, 128), (512, 128, 1)), ('mean', (128,), (128, 1)), ('detail', (3, 8), (24, 8, 1)),
+         ('stats', (4, 12), (48, 12, 1)))
+
+
 @torch.no_grad()
 def build(k, v, basis, init, out: Summary, first: int, pages: int, iters: int = 4) -> Summary:
     """k, v [1, 64P, H, 128] bf16 cache; basis [H,128,8]; init [H, pages, 4]
@@ -28,9 +33,10 @@ def build(k, v, basis, init, out: Summary, first: int, pages: int, iters: int = 
     if first < 0 or pages <= 0 or (first + pages) * 64 > L:
         raise ValueError("page range outside the K/V window")
     hp = out.head_pages
-    for name, t, inner in (('keys', out.keys, 512), ('mean', out.mean, 128), ('detail', out.detail, 24),
-                           ('stats', out.stats, 48)):
-        if t.dtype != torch.bfloat16 or t.shape[0] != h or t.stride(0) != hp * inner or not t[0].is_contiguous():
+    for name, shape, strides in _SLAB:
+        t = getattr(out, name)
+        if t.dtype != torch.bfloat16 or t.stride() != (hp * strides[0],) + strides or t.shape[0] != h or \
+                t.shape[2:] != shape:
             raise ValueError(f"out.{name} must be a page slice of a contiguous bf16 [H,Pcap,...] slab")
         if first + pages > t.shape[1]:
             raise ValueError(f"out.{name} does not cover pages [{first}, {first + pages})")
