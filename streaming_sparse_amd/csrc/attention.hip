@@ -97,33 +97,26 @@ __device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long lon
   return o;
 }
 
-// Enqueue the global->LDS loads of unit e (page e >= 0, rep tile -1-e < 0).
-__device__ __forceinline__ void issue_unit(const AttnParams& p, int e, int h, int wave, int lane,
-                                           const UnitOffsets& page_off, const UnitOffsets& rep_off,
-                                           lds_u8* kbuf, lds_u8* vbuf) {
-  const uint16_t* kb;
-  const uint16_t* vb;
+// Enqueue the global->LDS loads of the K rows (kv = 0) or V rows (kv = 1)
+// of unit e (page e >= 0, rep tile -1-e < 0) into `buf`.
+__device__ __forceinline__ void issue_rows(const AttnParams& p, int e, int kv, int h, int wave, int lane,
+                                           const UnitOffsets& page_off, const UnitOffsets& rep_off, lds_u8* buf) {
+  const uint16_t* base;
   UnitOffsets o;
   if (e >= 0) {
-    const long long b = (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head;
-    kb = p.k + b;
-    vb = p.v + b;
+    base = (kv ? p.v : p.k) + (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head;
     o = page_off;
   } else {
     const int rt = -1 - e;
-    kb = p.rk + ((long long)h * p.HP * 4 + rt * 64) * kHeadDim;
-    vb = p.rv + ((long long)h * p.HPV * 4 + rt * 64) * kHeadDim;
+    base = kv ? p.rv + ((long long)h * p.HPV * 4 + rt * 64) * kHeadDim
+              : p.rk + ((long long)h * p.HP * 4 + rt * 64) * kHeadDim;
     // rows of pages >= P re-read the last valid rep (masked in compute)
     const int last = p.P * 4 - rt * 64 - 1;
     o = last >= 63 ? rep_off : unit_offsets(wave, lane, kHeadDim, last);
   }
-  const uint32_t kl = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)kbuf + wave * 4096);
-  const uint32_t vl = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)vbuf + wave * 4096);
+  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)buf + wave * 4096);
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    dma16(kb, o.k[jj], kl + jj * 1024);
-    dma16(vb, o.v[jj], vl + jj * 1024);
-  }
+  for (int jj = 0; jj < 4; ++jj) dma16(base, kv ? o.v[jj] : o.k[jj], l + jj * 1024);
 }
 
 // V^T operand for O^T += V^T P^T: dims 32*dt + lane%32, keys (MFMA k order)
@@ -139,38 +132,57 @@ __device__ __forceinline__ u32x4 v_operand(const lds_u8* vbuf, int pair, int ks,
   return u32x4{ua[0], ua[1], ub[0], ub[1]};
 }
 
-template <bool PRECISE>
-__device__ __forceinline__ void compute_unit(const lds_u8* kbuf, const lds_u8* vbuf, const AttnParams& p, int e,
-                                             const uint32_t* maskw, int pair, int lane, const u32x4 (&qop)[8],
-                                             float& m, float& l, f32x16 (&O)[4]) {
+// S^T = K . Q^T for this pair's 32 keys of the unit in `kbuf`; S[i] is key
+// 32*pair + 8*(i/4) + 4*hh + i%4, query lane%32.  All 8 K operands are read
+// before the first MFMA.
+__device__ __forceinline__ f32x16 s_tile(const lds_u8* kbuf, int pair, int lane, const u32x4 (&qop)[8]) {
   const int r = lane & 31, hh = lane >> 5;
+  u32x4 a[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) a[st] = *(lds_u32x4*)(kbuf + k_off(32 * pair + r, 2 * st + hh));
   f32x16 S = {};
 #pragma unroll
-  for (int st = 0; st < 8; ++st) {
-    const u32x4 a = *(lds_u32x4*)(kbuf + k_off(32 * pair + r, 2 * st + hh));
-    S = mfma32(a, qop[st], S);
-  }
-  // S[i]: key 32*pair + 8*(i/4) + 4*hh + i%4 of the unit, query lane%32
+  for (int st = 0; st < 8; ++st) S = mfma32(a[st], qop[st], S);
+  return S;
+}
+
+// Row max of S in log2 units (+ bias); rep tiles first drop the reps of
+// selected pages and of pages >= P.  Returns the bias of the unit.
+__device__ __forceinline__ float unit_max(f32x16& S, int e, const uint32_t* maskw, int P, int pair, int lane,
+                                          float scale_log2, float& mloc) {
   float bias = 0.0f;
   if (e < 0) {
     bias = 4.0f;
-    const int rt = -1 - e;
+    const int rt = -1 - e, hh = lane >> 5;
+    // bit b of `drop`: page 16 rt + b is selected or beyond the window
+    const uint32_t sel = (maskw[rt >> 1] >> (16 * (rt & 1))) & 0xffffu;
+    const int valid = P - 16 * rt;
+    const uint32_t inside = valid >= 16 ? 0xffffu : ((1u << valid) - 1u);
+    const uint32_t drop = (sel | ~inside) >> (8 * pair + hh);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int page = 16 * rt + 8 * pair + 2 * j + hh;
-      const bool drop = page >= p.P || ((maskw[page >> 5] >> (page & 31)) & 1u);
+      const bool d = (drop >> (2 * j)) & 1u;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (drop) S[4 * j + i] = -INFINITY;
+      for (int i = 0; i < 4; ++i) S[4 * j + i] = d ? -INFINITY : S[4 * j + i];
     }
   }
   float mx = S[0];
 #pragma unroll
   for (int i = 1; i < 15; i += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, S[i]), S[i + 1]);
   mx = fmaxf(mx, S[15]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float mloc = mx * p.scale_log2 + bias;     // -inf stays -inf
-  if (__any(mloc > m)) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+  mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));   // max over lanes l and l ^ 32
+  mloc = mx * scale_log2 + bias;     // -inf stays -inf
+  return bias;
+}
+
+// Running-max update with a lazy threshold: the accumulator is rescaled only
+// when some lane's unit max exceeds its running max by more than kSlack
+// (log2 units), so probabilities stay below 2^kSlack and the rescale is rare.
+constexpr float kSlack = 8.0f;
+
+__device__ __forceinline__ void update_max(float mloc, float& m, float& l, f32x16 (&O)[4]) {
+  if (__any(mloc > m + kSlack)) {
     const float mnew = fmaxf(m, mloc);
     const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
     l *= alpha;
@@ -178,24 +190,28 @@ __device__ __forceinline__ void compute_unit(const lds_u8* kbuf, const lds_u8* v
     for (int dt = 0; dt < 4; ++dt) O[dt] *= alpha;
     m = mnew;
   }
-  const float nb = bias - (m == -INFINITY ? 0.0f : m);
-  float sum = 0.0f;
+}
+
+// P = 2^(S*scale + nb), l += sum P, O^T += V^T P^T.
+template <bool PRECISE>
+__device__ __forceinline__ void softmax_pv(const f32x16& S, float nb, float scale_log2, const lds_u8* vbuf,
+                                           int pair, int lane, float& l, f32x16 (&O)[4]) {
+  float P[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    S[i] = __builtin_amdgcn_exp2f(fmaf(S[i], p.scale_log2, nb));
-    sum += S[i];
-  }
-  l += sum;
+  for (int i = 0; i < 16; ++i) P[i] = __builtin_amdgcn_exp2f(fmaf(S[i], scale_log2, nb));
+  float s0 = (P[0] + P[1]) + (P[2] + P[3]), s1 = (P[4] + P[5]) + (P[6] + P[7]);
+  float s2 = (P[8] + P[9]) + (P[10] + P[11]), s3 = (P[12] + P[13]) + (P[14] + P[15]);
+  l += (s0 + s1) + (s2 + s3);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const int o = 8 * ks;
-    const u32x4 pb = {pack_bf16(S[o + 0], S[o + 1]), pack_bf16(S[o + 2], S[o + 3]), pack_bf16(S[o + 4], S[o + 5]),
-                      pack_bf16(S[o + 6], S[o + 7])};
+    const u32x4 pb = {pack_bf16(P[o + 0], P[o + 1]), pack_bf16(P[o + 2], P[o + 3]), pack_bf16(P[o + 4], P[o + 5]),
+                      pack_bf16(P[o + 6], P[o + 7])};
     u32x4 pl = {};
     if (PRECISE) {
 #pragma unroll
       for (int w = 0; w < 4; ++w)
-        pl[w] = pack_bf16(S[o + 2 * w] - bf16_lo(pb[w]), S[o + 2 * w + 1] - bf16_hi(pb[w]));
+        pl[w] = pack_bf16(P[o + 2 * w] - bf16_lo(pb[w]), P[o + 2 * w + 1] - bf16_hi(pb[w]));
     }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
@@ -208,8 +224,11 @@ __device__ __forceinline__ void compute_unit(const lds_u8* kbuf, const lds_u8* v
 
 template <bool PRECISE>
 __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
-  __shared__ alignas(16) uint8_t kv0[2 * kBuf];   // ring slot 0: K | V
-  __shared__ alignas(16) uint8_t kv1[2 * kBuf];   // ring slot 1: K | V
+  // LDS ring: K rows of units i (slot i & 1) run two units ahead of use, V
+  // rows one unit ahead.  Iteration i reads K slot (i+1)&1 and V slot i&1
+  // while the loads of K unit i+2 and V unit i+1 land in the other slots.
+  __shared__ alignas(16) uint8_t kring[2 * kBuf];
+  __shared__ alignas(16) uint8_t vring[2 * kBuf];
   __shared__ int units[kMaxCount + kMaxRepTiles];
   __shared__ uint32_t maskw[16];
   __shared__ float xm[2][64], xl[2][64];
@@ -250,10 +269,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st);
   __syncthreads();
   const int nunits = nunits_s;
-  lds_u8* k0 = (lds_u8*)kv0;
-  lds_u8* v0 = (lds_u8*)kv0 + kBuf;
-  lds_u8* k1 = (lds_u8*)kv1;
-  lds_u8* v1 = (lds_u8*)kv1 + kBuf;
+  lds_u8* const kbase = (lds_u8*)kring;
+  lds_u8* const vbase = (lds_u8*)vring;
+  auto kslot = [&](int slot) { return kbase + slot * kBuf; };
+  auto vslot = [&](int slot) { return vbase + slot * kBuf; };
 
   float m = -INFINITY, l = 0.0f;
   f32x16 O[4];
@@ -261,25 +280,49 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
   const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63);
   const UnitOffsets rep_off = unit_offsets(wave, lane, kHeadDim, 63);
-  issue_unit(p, __builtin_amdgcn_readfirstlane(units[0]), h, wave, lane, page_off, rep_off, k0, v0);
+  auto unit = [&](int i) { return __builtin_amdgcn_readfirstlane(units[i]); };
+  // prologue: K0, V0, K1 in flight; S of unit 0 and its max
+  issue_rows(p, unit(0), 0, h, wave, lane, page_off, rep_off, kslot(0));
+  issue_rows(p, unit(0), 1, h, wave, lane, page_off, rep_off, vslot(0));
+  issue_rows(p, unit(min(1, nunits - 1)), 0, h, wave, lane, page_off, rep_off, kslot(1));
   wait_loads();
   __syncthreads();
-  for (int u = 0; u < nunits; u += 2) {
-    if (u + 1 < nunits)
-      issue_unit(p, __builtin_amdgcn_readfirstlane(units[u + 1]), h, wave, lane, page_off, rep_off, k1, v1);
-    compute_unit<PRECISE>(k0, v0, p, units[u], maskw, pair, lane, qop, m, l, O);
+  f32x16 S0 = s_tile(kslot(0), pair, lane, qop), S1;
+  float mloc;
+  float bias = unit_max(S0, unit(0), maskw, p.P, pair, lane, p.scale_log2, mloc);
+  update_max(mloc, m, l, O);
+  __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
+  // One unit with a successor: loads of K unit i+2 (clamped to the last
+  // unit; a surplus load lands in a slot nobody reads again) and V unit i+1,
+  // S of unit i+1, softmax and P.V of unit i, then the max of unit i+1.
+  auto step = [&](int i, f32x16& Sc, f32x16& Sn) {
+    const int cur = i & 1, nxt = cur ^ 1;
+    issue_rows(p, unit(min(i + 2, nunits - 1)), 0, h, wave, lane, page_off, rep_off, kslot(cur));
+    issue_rows(p, unit(i + 1), 1, h, wave, lane, page_off, rep_off, vslot(nxt));
+    const float nb = bias - (m == -INFINITY ? 0.0f : m);
+    Sn = s_tile(kslot(nxt), pair, lane, qop);
+    softmax_pv<PRECISE>(Sc, nb, p.scale_log2, vslot(cur), pair, lane, l, O);
+    bias = unit_max(Sn, unit(i + 1), maskw, p.P, pair, lane, p.scale_log2, mloc);
+    update_max(mloc, m, l, O);
     wait_loads();
     __syncthreads();
-    if (u + 1 >= nunits) break;
-    if (u + 2 < nunits)
-      issue_unit(p, __builtin_amdgcn_readfirstlane(units[u + 2]), h, wave, lane, page_off, rep_off, k0, v0);
-    compute_unit<PRECISE>(k1, v1, p, units[u + 1], maskw, pair, lane, qop, m, l, O);
-    wait_loads();
-    __syncthreads();
+  };
+  int i = 0;
+  for (; i + 2 < nunits; i += 2) {
+    step(i, S0, S1);
+    step(i + 1, S1, S0);
   }
+  if (i + 1 < nunits) {
+    step(i, S0, S1);
+    ++i;
+    S0 = S1;
+  }
+  // last unit
+  softmax_pv<PRECISE>(S0, bias - (m == -INFINITY ? 0.0f : m), p.scale_log2, vslot(i & 1), pair, lane, l, O);
+  __syncthreads();
   // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS
   l += __shfl_xor(l, 32);
-  float* xo = reinterpret_cast<float*>(kv0);     // [qw][64 lanes][64] fp32 = 32 KB
+  float* xo = reinterpret_cast<float*>(kring);     // [qw][64 lanes][64] fp32 = 32 KB
   if (pair == 1) {
     float* d = xo + (qw * 64 + lane) * 64;
 #pragma unroll
