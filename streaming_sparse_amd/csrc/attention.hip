@@ -101,22 +101,25 @@ __device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long lon
 // of unit e (page e >= 0, rep tile -1-e < 0) into `buf`.
 __device__ __forceinline__ void issue_rows(const AttnParams& p, int e, int kv, int h, int wave, int lane,
                                            const UnitOffsets& page_off, const UnitOffsets& rep_off, lds_u8* buf) {
-  const uint16_t* base;
-  UnitOffsets o;
+  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)buf + wave * 4096);
+  // each path issues with its own offset registers (no copies into a common set)
+  auto issue = [&](const uint16_t* base, const UnitOffsets& o) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) dma16(base, kv ? o.v[jj] : o.k[jj], l + jj * 1024);
+  };
   if (e >= 0) {
-    base = (kv ? p.v : p.k) + (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head;
-    o = page_off;
+    issue((kv ? p.v : p.k) + (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head, page_off);
   } else {
     const int rt = -1 - e;
-    base = kv ? p.rv + ((long long)h * p.HPV * 4 + rt * 64) * kHeadDim
-              : p.rk + ((long long)h * p.HP * 4 + rt * 64) * kHeadDim;
+    const uint16_t* base = kv ? p.rv + ((long long)h * p.HPV * 4 + rt * 64) * kHeadDim
+                              : p.rk + ((long long)h * p.HP * 4 + rt * 64) * kHeadDim;
     // rows of pages >= P re-read the last valid rep (masked in compute)
     const int last = p.P * 4 - rt * 64 - 1;
-    o = last >= 63 ? rep_off : unit_offsets(wave, lane, kHeadDim, last);
+    if (last >= 63)
+      issue(base, rep_off);
+    else
+      issue(base, unit_offsets(wave, lane, kHeadDim, last));
   }
-  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)buf + wave * 4096);
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) dma16(base, kv ? o.v[jj] : o.k[jj], l + jj * 1024);
 }
 
 // V^T operand for O^T += V^T P^T: dims 32*dt + lane%32, keys (MFMA k order)
@@ -181,27 +184,31 @@ __device__ __forceinline__ float unit_max(f32x16& S, int e, const uint32_t* mask
 // (log2 units), so probabilities stay below 2^kSlack and the rescale is rare.
 constexpr float kSlack = 8.0f;
 
-__device__ __forceinline__ void update_max(float mloc, float& m, float& l, f32x16 (&O)[4]) {
+__device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, f32x16 (&O)[4]) {
   if (__any(mloc > m + kSlack)) {
     const float mnew = fmaxf(m, mloc);
     const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
-    l *= alpha;
+    L *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) O[dt] *= alpha;
     m = mnew;
   }
 }
 
-// P = 2^(S*scale + nb), l += sum P, O^T += V^T P^T.
+// bf16 1.0 in both halves: the A operand whose product with P^T puts the
+// row sums of P in every row of the accumulator.
+constexpr uint32_t kOnes = 0x3F803F80u;
+
+// P = 2^(S*scale + nb); O^T += V^T P^T and L += 1 P^T (the softmax
+// denominator of lane's query over the pair's 32 keys, summed by the matrix
+// pipe from the same bf16 P that multiplies V).
 template <bool PRECISE>
 __device__ __forceinline__ void softmax_pv(const f32x16& S, float nb, float scale_log2, const lds_u8* vbuf,
-                                           int pair, int lane, float& l, f32x16 (&O)[4]) {
+                                           int pair, int lane, f32x16& L, f32x16 (&O)[4]) {
   float P[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) P[i] = __builtin_amdgcn_exp2f(fmaf(S[i], scale_log2, nb));
-  float s0 = (P[0] + P[1]) + (P[2] + P[3]), s1 = (P[4] + P[5]) + (P[6] + P[7]);
-  float s2 = (P[8] + P[9]) + (P[10] + P[11]), s3 = (P[12] + P[13]) + (P[14] + P[15]);
-  l += (s0 + s1) + (s2 + s3);
+  const u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const int o = 8 * ks;
@@ -213,6 +220,8 @@ __device__ __forceinline__ void softmax_pv(const f32x16& S, float nb, float scal
       for (int w = 0; w < 4; ++w)
         pl[w] = pack_bf16(P[o + 2 * w] - bf16_lo(pb[w]), P[o + 2 * w + 1] - bf16_hi(pb[w]));
     }
+    L = mfma32(ones, pb, L);
+    if (PRECISE) L = mfma32(ones, pl, L);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const u32x4 va = v_operand(vbuf, pair, ks, dt, lane);
@@ -274,8 +283,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   auto kslot = [&](int slot) { return kbase + slot * kBuf; };
   auto vslot = [&](int slot) { return vbase + slot * kBuf; };
 
-  float m = -INFINITY, l = 0.0f;
-  f32x16 O[4];
+  float m = -INFINITY;
+  f32x16 L = {}, O[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
   const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63);
@@ -290,7 +299,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   f32x16 S0 = s_tile(kslot(0), pair, lane, qop), S1;
   float mloc;
   float bias = unit_max(S0, unit(0), maskw, p.P, pair, lane, p.scale_log2, mloc);
-  update_max(mloc, m, l, O);
+  update_max(mloc, m, L, O);
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
   // One unit with a successor: loads of K unit i+2 (clamped to the last
   // unit; a surplus load lands in a slot nobody reads again) and V unit i+1,
@@ -301,9 +310,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
     issue_rows(p, unit(i + 1), 1, h, wave, lane, page_off, rep_off, vslot(nxt));
     const float nb = bias - (m == -INFINITY ? 0.0f : m);
     Sn = s_tile(kslot(nxt), pair, lane, qop);
-    softmax_pv<PRECISE>(Sc, nb, p.scale_log2, vslot(cur), pair, lane, l, O);
+    softmax_pv<PRECISE>(Sc, nb, p.scale_log2, vslot(cur), pair, lane, L, O);
     bias = unit_max(Sn, unit(i + 1), maskw, p.P, pair, lane, p.scale_log2, mloc);
-    update_max(mloc, m, l, O);
+    update_max(mloc, m, L, O);
     wait_loads();
     __syncthreads();
   };
@@ -318,17 +327,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
     S0 = S1;
   }
   // last unit
-  softmax_pv<PRECISE>(S0, bias - (m == -INFINITY ? 0.0f : m), p.scale_log2, vslot(i & 1), pair, lane, l, O);
+  softmax_pv<PRECISE>(S0, bias - (m == -INFINITY ? 0.0f : m), p.scale_log2, vslot(i & 1), pair, lane, L, O);
   __syncthreads();
   // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS
-  l += __shfl_xor(l, 32);
-  float* xo = reinterpret_cast<float*>(kring);     // [qw][64 lanes][64] fp32 = 32 KB
+  const float l = L[0];
+  float* xo = reinterpret_cast<float*>(kring);     // [qw][64 items][64 lanes] fp32 = 32 KB
   if (pair == 1) {
-    float* d = xo + (qw * 64 + lane) * 64;
+    float* d = xo + qw * 4096 + lane;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) d[16 * dt + i] = O[dt][i];
+      for (int i = 0; i < 16; ++i) d[(16 * dt + i) * 64] = O[dt][i];
     xm[qw][lane] = m;
     xl[qw][lane] = l;
   }
@@ -339,7 +348,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   const float mu = mt == -INFINITY ? 0.0f : mt;
   const float a0 = __builtin_amdgcn_exp2f(m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
   const float inv = 1.0f / (l * a0 + l1 * a1);
-  const float* d = xo + (qw * 64 + lane) * 64;
+  const float* d = xo + qw * 4096 + lane;
   uint16_t* op = p.out + qrow * p.q_tok + (long long)h * p.q_head + 4 * hh;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
@@ -347,7 +356,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
     for (int j = 0; j < 4; ++j) {
       float o[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) o[c] = (O[dt][4 * j + c] * a0 + d[16 * dt + 4 * j + c] * a1) * inv;
+      for (int c = 0; c < 4; ++c) o[c] = (O[dt][4 * j + c] * a0 + d[(16 * dt + 4 * j + c) * 64] * a1) * inv;
       const u32x2 w = {pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
       *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * j) = w;
     }

@@ -217,45 +217,55 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   const float bmax = fmaxf(fmaxf(s.bmax_w[0], s.bmax_w[1]), fmaxf(s.bmax_w[2], s.bmax_w[3]));
   const float th0 = p.theta[h * 4 + 0], th1 = p.theta[h * 4 + 1], th2 = p.theta[h * 4 + 2], th3 = p.theta[h * 4 + 3];
 
-  // pass 2: probabilities -> four features -> theta-weighted value -> probe mean
+  // pass 2: probabilities -> four features -> theta-weighted value -> probe mean.
+  // The per-rep stats reach the lane layout of S through the matrix pipe:
+  // U^T = ST . (q2_hi | q2_lo)^T gives u_r = sum_g q2_g st[r,g] (stats in both
+  // k halves, q2 split into two bf16 terms); B^T = st[r,8] (qn_hi + qn_lo)
+  // gives beta_r; unit-vector products give st[r,9] and st[r,10].
+  u32x4 bq, bqn, bone;
+  {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float a = q2[2 * w], b = q2[2 * w + 1];
+      const float ah = bf16_lo(pack_bf16(a, 0.f)), bh = bf16_lo(pack_bf16(b, 0.f));
+      bq[w] = hh == 0 ? pack_bf16(a, b) : pack_bf16(a - ah, b - bh);
+    }
+    const float qh = bf16_lo(pack_bf16(qn, 0.f));
+    bqn = u32x4{hh == 0 ? pack_bf16(qh, qn - qh) : 0u, 0u, 0u, 0u};
+    bone = u32x4{hh == 0 ? 0x3F80u : 0u, 0u, 0u, 0u};
+  }
   for (int tile = wave; tile < ntiles; tile += 4) {
     f32x16 S;
     rep_logits(av, qop, S);
     if (tile + 4 < ntiles) load_reps(rkh, tile + 4, P, lane, av);
+    // stats of rep row tile*32 + lane%32: words (st0,st1)..(st6,st7), (st8,st9), (st10,st11)
+    const int rrow = min(tile * 32 + pi, P * 4 - 1);
+    const uint32_t* sr = reinterpret_cast<const uint32_t*>(sth + rrow * 12);
+    const u32x2 w01 = *reinterpret_cast<const u32x2*>(sr), w23 = *reinterpret_cast<const u32x2*>(sr + 2);
+    const u32x2 w45 = *reinterpret_cast<const u32x2*>(sr + 4);
+    const u32x4 ag = {w01[0], w01[1], w23[0], w23[1]};
+    const uint32_t st8 = w45[0] & 0xffffu, st9 = w45[0] >> 16, st10 = w45[1] & 0xffffu;
+    const uint32_t lo_only = hh == 0 ? 0xffffffffu : 0u;
+    const f32x16 U = mfma32(ag, bq, f32x16{});
+    const f32x16 Bt = mfma32(u32x4{(st8 | (st8 << 16)) & lo_only, 0u, 0u, 0u}, bqn, f32x16{});
+    const f32x16 F9 = mfma32(u32x4{st9 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
+    const f32x16 F10 = mfma32(u32x4{st10 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int page = tile * 8 + 2 * j + hh;
-      const int pc = min(page, P - 1);
-      const uint16_t* sp = sth + pc * 48;
-      uint32_t sw[24];
-#pragma unroll
-      for (int c = 0; c < 6; ++c) {
-        const u32x4 v4 = *reinterpret_cast<const u32x4*>(sp + 8 * c);
-        sw[4 * c + 0] = v4[0];
-        sw[4 * c + 1] = v4[1];
-        sw[4 * c + 2] = v4[2];
-        sw[4 * c + 3] = v4[3];
-      }
-      // stats[p, r, f] = element r*12 + f of the 48 bf16 values
-      auto st = [&](int r, int f) -> float {
-        const int e = r * 12 + f;
-        return (e & 1) ? bf16_hi(sw[e >> 1]) : bf16_lo(sw[e >> 1]);
-      };
       float prob[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) prob[i] = __builtin_amdgcn_exp2f(fmaf(S[4 * j + i], c2, -MX)) * inv_den;
       const float alpha = ((prob[0] + prob[1]) + prob[2]) + prob[3];
-      const float c = st(1, 11) + bmax;
-      float x0 = alpha * st(0, 11), x1 = 0.f, x2 = 0.f, x3 = 0.f;
+      const uint16_t* sp = sth + min(page, P - 1) * 48;
+      const float c = bf16_to_f32(sp[12 + 11]) + bmax;            // stats[p,1,11] + max_p stats[p,1,11]
+      float x0 = alpha * bf16_to_f32(sp[11]), x1 = 0.f, x2 = 0.f, x3 = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float u = 0.f;
-#pragma unroll
-        for (int g = 0; g < 8; ++g) u = fmaf(q2[g], st(i, g), u);
-        u = fmaxf(u, 0.f);
-        const float beta = qn * st(i, 8);
-        x0 += fabsf(prob[i] - alpha * 0.25f) * st(i, 9);
-        x1 += prob[i] * __builtin_amdgcn_sqrtf(u) * st(i, 10);
+        const float u = fmaxf(U[4 * j + i], 0.f);
+        const float beta = Bt[4 * j + i];
+        x0 += fabsf(prob[i] - alpha * 0.25f) * F9[4 * j + i];
+        x1 += prob[i] * __builtin_amdgcn_sqrtf(u) * F10[4 * j + i];
         x2 += prob[i] * beta;
         x3 += prob[i] * (u + beta * beta);
       }
