@@ -249,6 +249,17 @@ def near_tie_rows(risk_, boundary, rel=1e-3):
     return tie & torch.isfinite(nxt)
 
 
+def near_tie_order_rows(risk_, ids, start, rel=1e-3):
+    """Rows whose risk-ordered LUT part ids[..., start:] holds two consecutive
+    pages whose scores differ by at most `rel` relative: the order of those
+    two is a rounding matter (it only changes the accumulation order of the
+    attention that follows).  risk_ [H,T,P], ids [H,T,C].  Returns bool [H,T]."""
+    r = risk_.gather(-1, ids[..., start:].long())
+    a, b = r[..., :-1], r[..., 1:]
+    scale = torch.maximum(a.abs(), b.abs())
+    return ((a - b).abs() <= rel * scale).any(-1)
+
+
 def rel_l2(a, b):
     a = a.double()
     b = b.double()

@@ -64,19 +64,6 @@ __device__ __forceinline__ int k_off(int row, int chunk) { return row * 256 + ((
 __device__ __forceinline__ int vswz(int row) { return (0xEA40 >> (4 * (row & 3))) & 15; }   // 0, 4, 10, 14
 __device__ __forceinline__ int v_off(int row, int chunk) { return row * 256 + ((chunk ^ vswz(row)) << 4); }
 
-// s_waitcnt vmcnt(0) (expcnt/lgkmcnt left at their maxima) as the intrinsic,
-// so the compiler's own wait-count tracking sees it.
-__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// 16-byte global->LDS load of one wave: lane l's 16 bytes at base + off
-// (bytes; base wave-uniform in SGPRs, off per lane) land at lds + 16*l.
-// Issued from inline asm so the compiler does not fence later LDS reads of
-// the other ring slot on it; wait_loads() before the barrier orders it.
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-               : "memory", "m0");
-}
-
 // Per-lane byte offsets of this wave's 4 K and 4 V rows of a unit (wave w
 // loads rows 16w..16w+15, 1 KB per instruction) for a row stride `rs`
 // (elements) and rows clamped to `last`.

@@ -56,4 +56,17 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
   return (b % 8) * (total / 8) + b / 8;
 }
 
+// s_waitcnt vmcnt(0) (expcnt/lgkmcnt left at their maxima) as the intrinsic,
+// so the compiler's own wait-count tracking sees it.
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// 16-byte global->LDS load of one wave: lane l's 16 bytes at base + off
+// (bytes; base wave-uniform in SGPRs, off per lane) land at lds + 16*l.
+// Issued from inline asm so the compiler does not fence later LDS reads on
+// it; wait_loads() (and a barrier, for other waves' loads) orders it.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
 }  // namespace ssa

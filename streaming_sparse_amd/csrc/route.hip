@@ -30,6 +30,11 @@ constexpr int kMaxPages = 512;
 constexpr int kAnchors = 24;
 constexpr int kCurrent = 72;
 
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
+typedef __attribute__((address_space(3))) const uint16_t lds_u16;
+
 __constant__ int kProbeOffsets[16] = {0, 4, 8, 13, 17, 21, 25, 29, 34, 38, 42, 46, 50, 55, 59, 63};
 
 struct RouteParams {
@@ -48,15 +53,31 @@ struct RouteParams {
   int H, T, P, HP, C, mode, total;
 };
 
-struct Smem {
-  float part[4][32][2];        // per-wave (max, sum) of each probe
-  float risk[2][kMaxPages];
+constexpr int kSlotBytes = 9 * 1024;   // a rep tile: 32 rows x 256 B (swizzled) + its pages' stats (768 B)
+
+struct Sel {                   // selection state, aliasing the tile ring once both passes are done
   unsigned long long key[2][kMaxPages];
   uint8_t sel[2][kMaxPages];
   int list[2][kMaxPages];
-  float bmax_w[4];
-  alignas(16) uint16_t stats[kMaxPages * 48];   // the head's page stats, staged once
 };
+
+struct Smem {
+  alignas(16) uint8_t ring[4][2][kSlotBytes];   // per-wave double buffer of rep tiles
+  float part[4][32][2];        // per-wave (max, sum) of each probe
+  float risk[2][kMaxPages];
+  float bmax_w[4];
+};
+static_assert(sizeof(Sel) <= sizeof(Smem::ring), "selection state must fit in the tile ring");
+
+// Sum over each 16-lane row, left in the row's lane 15 (DPP row shifts,
+// out-of-row sources read as 0).
+__device__ __forceinline__ float row_sum16(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xf, 0xf, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xf, 0xf, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xf, 0xf, true));
+  return v;
+}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -64,14 +85,21 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// A operand of a tile of 32 reps (8 pages): rep row tile*32 + lane%32, dims
-// 64*hh + 8*st + [0,8).  Tiles past the window re-read the last rep.
-__device__ __forceinline__ void load_reps(const uint16_t* rkh, int tile, int P, int lane, u32x4 (&av)[8]) {
-  const int hh = lane >> 5;
-  const int row = min(tile * 32 + (lane & 31), P * 4 - 1);
-  const uint16_t* a = rkh + (long long)row * kHeadDim + 64 * hh;
+// Rep tiles reach LDS by 16-byte global->LDS loads, 1 KB per wave
+// instruction: load jj fills rows 4jj..4jj+3 of the tile, lane l the 16 bytes
+// of row 4jj + l/16 at physical chunk l%16, which holds logical chunk
+// (l%16) ^ (row & 15).  The MFMA operand reads (row lane%32, chunk 2st+hh)
+// are then bank-conflict free.  Rows past the window re-read the last rep.
+__device__ __forceinline__ uint32_t tile_row_off(int jj, int lane, int last_row) {
+  const int row = 4 * jj + (lane >> 4);
+  return (uint32_t)(min(row, last_row) * 256 + (((lane & 15) ^ (row & 15)) << 4));
+}
+
+// A operand of the tile in `slot`: rep row lane%32, dims 16*st + 8*hh + [0,8).
+__device__ __forceinline__ void read_reps(const lds_u8* slot, int lane, u32x4 (&av)[8]) {
+  const int r = lane & 31, hh = lane >> 5;
 #pragma unroll
-  for (int st = 0; st < 8; ++st) av[st] = ldg16(a + 8 * st);
+  for (int st = 0; st < 8; ++st) av[st] = *(const lds_u32x4*)(slot + r * 256 + (((2 * st + hh) ^ (r & 15)) << 4));
 }
 
 __device__ __forceinline__ void rep_logits(const u32x4 (&av)[8], const u32x4 (&qop)[8], f32x16& S) {
@@ -102,9 +130,9 @@ __device__ __forceinline__ void bitonic_desc(unsigned long long* key, int bt) {
   }
 }
 
-__global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
+__global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   __shared__ Smem s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int NP = (p.T + 1) >> 1;
   const int work = xcd_remap(blockIdx.x, p.H * NP);
   const int h = work / NP, t0 = 2 * (work % NP);
@@ -113,20 +141,23 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   const int blk = pi >> 4, m = pi & 15;
   const int tq = min(t0 + blk, p.T - 1);
 
-  // probe operand (B): dims 64*hh + 8*st + [0,8); and its moments
+  // probe operand (B): dims 16*st + 8*hh + [0,8) (the k order of read_reps).
+  // q2[g] = sum of q^2 over dims 16g..16g+15 / D, summed in one lane per
+  // group from the dims 64*hh + [0,64) of this lane half
   const long long row = p.gathered ? m : kProbeOffsets[m];
-  const uint16_t* qp = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row + 64 * hh;
+  const uint16_t* qp = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
   u32x4 qop[8];
   float q2[8];
 #pragma unroll
-  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 8 * st);
+  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st + 8 * hh);
   {
     float g4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
+      const u32x4 v = ldg16(qp + 64 * hh + 8 * st);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const float a = bf16_lo(qop[st][w]), b = bf16_hi(qop[st][w]);
+        const float a = bf16_lo(v[w]), b = bf16_hi(v[w]);
         g4[st >> 1] += a * a + b * b;
       }
     }
@@ -142,22 +173,12 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   for (int g = 0; g < 8; ++g) qsum += q2[g];
   const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
 
-  // stage the head's page stats in LDS (P x 96 B, all loads in flight)
-  {
-    const u32x4* src = reinterpret_cast<const u32x4*>(p.stats + (long long)h * p.HP * 48);
-    u32x4* dst = reinterpret_cast<u32x4*>(s.stats);
-    const int n16 = P * 6;                        // 16-byte chunks
-    constexpr int kPer = (kMaxPages * 6 + kThreads - 1) / kThreads;
-    u32x4 v[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) v[k] = src[min(tid + kThreads * k, n16 - 1)];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k)
-      if (tid + kThreads * k < n16) dst[tid + kThreads * k] = v[k];
-  }
-  __syncthreads();
-  const uint16_t* sth = s.stats;
-  // per-head bound of the page value norm: max_p stats[p,1,11]
+  const uint16_t* rkh = p.rk + (long long)h * p.HP * 4 * kHeadDim;
+  const uint16_t* sth = p.stats + (long long)h * p.HP * 48;
+  const int ntiles = (P + 7) >> 3;
+  // logits in log2 units: z2 = q.k * log2(e) / sqrt(D); prob = 2^(z2 - max2) / den
+  const float c2 = kLog2e / sqrtf((float)kHeadDim);
+  // per-head bound of the page value norm: max_p stats[p,1,11] (read after pass 1)
   {
     float b = -INFINITY;
     for (int i = tid; i < P; i += kThreads) b = fmaxf(b, bf16_to_f32(sth[i * 48 + 12 + 11]));
@@ -165,19 +186,53 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
     if (lane == 0) s.bmax_w[wave] = b;
   }
 
-  const uint16_t* rkh = p.rk + (long long)h * p.HP * 4 * kHeadDim;
-  const int ntiles = (P + 7) >> 3;
-  // logits in log2 units: z2 = q.k * log2(e) / sqrt(D); prob = 2^(z2 - max2) / den
-  const float c2 = kLog2e / sqrtf((float)kHeadDim);
+  // Each wave owns tiles wave + 4 j (j < nmine) and a double buffer of them
+  // in LDS: no other wave reads its slots, so its own load counter orders
+  // them.  A wave without tiles (P < 32) re-reads tile `wave` and skips it.
+  const int nmine = __builtin_amdgcn_readfirstlane(max((ntiles - wave + 3) >> 2, 0));
+  auto mine = [&](int jj) { return wave + 4 * max(min(jj, nmine - 1), 0); };
+  lds_u8* const ring = (lds_u8*)&s.ring[wave][0][0];
+  const uint32_t ring_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring);
+  uint32_t koff[8];
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) koff[jj] = tile_row_off(jj, lane, 31);
+  // the stats of the tile's 8 pages: 768 contiguous bytes; lanes 48..63 land
+  // past them in the slot's 1 KB stats region (a clamped re-read)
+  auto issue_tile = [&](int tile_in, int slot, bool stats) {
+    const int tile = __builtin_amdgcn_readfirstlane(tile_in);
+    const uint32_t l = ring_addr + slot * kSlotBytes;
+    const uint16_t* kb = rkh + (long long)tile * 32 * kHeadDim;
+    const int last_row = P * 4 - 1 - tile * 32;
+    if (last_row >= 31) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) dma16(kb, koff[jj], l + jj * 1024);
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) dma16(kb, tile_row_off(jj, lane, last_row), l + jj * 1024);
+    }
+    if (stats)
+      dma16(sth + (long long)tile * 8 * 48, (uint32_t)min(16 * lane, (P - tile * 8) * 96 - 16), l + 8192);
+  };
+  // wait until at most n of this wave's global->LDS loads are outstanding
+  auto wait_tile = [&](int n) {
+    if (n == 8) __builtin_amdgcn_s_waitcnt(0x0F78);
+    else __builtin_amdgcn_s_waitcnt(0x0F79);
+  };
+  auto wait_lds = [&]() { __builtin_amdgcn_s_waitcnt(0xC07F); };   // lgkmcnt(0)
 
   // pass 1: max and sum of exp over all reps, per probe
   float mx = -INFINITY, den = 0.f;
-  u32x4 av[8];
-  load_reps(rkh, wave, P, lane, av);
-  for (int tile = wave; tile < ntiles; tile += 4) {
+  issue_tile(mine(0), 0, false);
+  issue_tile(mine(1), 1, false);
+  for (int j = 0; j < nmine; ++j) {
+    const int tile = mine(j);
+    wait_tile(8);                                    // tile j landed (tile j+1 may be in flight)
+    u32x4 av[8];
+    read_reps(ring + (j & 1) * kSlotBytes, lane, av);
+    wait_lds();
+    issue_tile(mine(j + 2), j & 1, false);
     f32x16 S;
     rep_logits(av, qop, S);
-    load_reps(rkh, tile + 4 < ntiles ? tile + 4 : wave, P, lane, av);   // next tile (pass 2's first at the end)
     float tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -193,6 +248,9 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
     den = den * __builtin_amdgcn_exp2f(mx - muse) + acc;
     mx = mnew;
   }
+  wait_loads();                                      // surplus loads of the clamped tail
+  issue_tile(mine(0), 0, true);                      // pass 2's first two tiles
+  issue_tile(mine(1), 1, true);
   {
     const float omx = __shfl_xor(mx, 32), oden = __shfl_xor(den, 32);
     const float mm = fmaxf(mx, omx);
@@ -234,15 +292,27 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
     bqn = u32x4{hh == 0 ? pack_bf16(qh, qn - qh) : 0u, 0u, 0u, 0u};
     bone = u32x4{hh == 0 ? 0x3F80u : 0u, 0u, 0u, 0u};
   }
-  for (int tile = wave; tile < ntiles; tile += 4) {
+  for (int j = 0; j < nmine; ++j) {
+    const int tile = mine(j);
+    wait_tile(9);
+    const lds_u8* slot = ring + (j & 1) * kSlotBytes;
+    u32x4 av[8];
+    read_reps(slot, lane, av);
+    // stats of rep row lane%32: words (st0,st1)..(st6,st7), (st8,st9), (st10,st11)
+    const lds_u8* sr = slot + 8192 + pi * 24;
+    const u32x2 w01 = *(lds_u32x2*)sr, w23 = *(lds_u32x2*)(sr + 8), w45 = *(lds_u32x2*)(sr + 16);
+    // stats[p,0,11] and stats[p,1,11] of this lane's 4 pages (2 jj + hh of the tile)
+    float s011[4], s111[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const lds_u16* sp = (lds_u16*)(slot + 8192) + (2 * jj + hh) * 48;
+      s011[jj] = bf16_to_f32(sp[11]);
+      s111[jj] = bf16_to_f32(sp[23]);
+    }
+    wait_lds();
+    issue_tile(mine(j + 2), j & 1, true);
     f32x16 S;
     rep_logits(av, qop, S);
-    if (tile + 4 < ntiles) load_reps(rkh, tile + 4, P, lane, av);
-    // stats of rep row tile*32 + lane%32: words (st0,st1)..(st6,st7), (st8,st9), (st10,st11)
-    const int rrow = min(tile * 32 + pi, P * 4 - 1);
-    const uint32_t* sr = reinterpret_cast<const uint32_t*>(sth + rrow * 12);
-    const u32x2 w01 = *reinterpret_cast<const u32x2*>(sr), w23 = *reinterpret_cast<const u32x2*>(sr + 2);
-    const u32x2 w45 = *reinterpret_cast<const u32x2*>(sr + 4);
     const u32x4 ag = {w01[0], w01[1], w23[0], w23[1]};
     const uint32_t st8 = w45[0] & 0xffffu, st9 = w45[0] >> 16, st10 = w45[1] & 0xffffu;
     const uint32_t lo_only = hh == 0 ? 0xffffffffu : 0u;
@@ -251,33 +321,32 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
     const f32x16 F9 = mfma32(u32x4{st9 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
     const f32x16 F10 = mfma32(u32x4{st10 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int page = tile * 8 + 2 * j + hh;
+    for (int jj = 0; jj < 4; ++jj) {
+      const int page = tile * 8 + 2 * jj + hh;
       float prob[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) prob[i] = __builtin_amdgcn_exp2f(fmaf(S[4 * j + i], c2, -MX)) * inv_den;
+      for (int i = 0; i < 4; ++i) prob[i] = __builtin_amdgcn_exp2f(fmaf(S[4 * jj + i], c2, -MX)) * inv_den;
       const float alpha = ((prob[0] + prob[1]) + prob[2]) + prob[3];
-      const uint16_t* sp = sth + min(page, P - 1) * 48;
-      const float c = bf16_to_f32(sp[12 + 11]) + bmax;            // stats[p,1,11] + max_p stats[p,1,11]
-      float x0 = alpha * bf16_to_f32(sp[11]), x1 = 0.f, x2 = 0.f, x3 = 0.f;
+      const float c = s111[jj] + bmax;                    // stats[p,1,11] + max_p stats[p,1,11]
+      float x0 = alpha * s011[jj], x1 = 0.f, x2 = 0.f, x3 = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float u = fmaxf(U[4 * j + i], 0.f);
-        const float beta = Bt[4 * j + i];
-        x0 += fabsf(prob[i] - alpha * 0.25f) * F9[4 * j + i];
-        x1 += prob[i] * __builtin_amdgcn_sqrtf(u) * F10[4 * j + i];
+        const float u = fmaxf(U[4 * jj + i], 0.f);
+        const float beta = Bt[4 * jj + i];
+        x0 += fabsf(prob[i] - alpha * 0.25f) * F9[4 * jj + i];
+        x1 += prob[i] * __builtin_amdgcn_sqrtf(u) * F10[4 * jj + i];
         x2 += prob[i] * beta;
         x3 += prob[i] * (u + beta * beta);
       }
       x2 *= c;
       x3 *= c;
       float val = ((x0 * th0 + x1 * th1) + x2 * th2) + x3 * th3;
-      // sum over the 16 probes of this lane's block (lanes 32*hh + 16*blk + [0,16))
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) val += __shfl_xor(val, o);
-      if (m == 0 && page < P) s.risk[blk][page] = val / 16.0f;
+      // mean over the 16 probes of this lane's block: one DPP row
+      val = row_sum16(val);
+      if (m == 15 && page < P) s.risk[blk][page] = val * 0.0625f;
     }
   }
+  wait_loads();                                      // the ring is reused for selection below
   __syncthreads();
 
   const int nrow = min(2, p.T - t0);
@@ -288,6 +357,7 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   if (p.mode < 0) return;
 
   // ---------------------------------------------------------------- select
+  Sel& sl = *reinterpret_cast<Sel*>(&s.ring[0][0][0]);
   // Row b is sorted by 128 threads (tid / 128 = b) with a bitonic network
   // over 512 64-bit keys, descending.  Key = (group << 62) | (orderable
   // risk << 30) | (1023 - page): risk descending, ties -> lower page, and
@@ -315,27 +385,27 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
         key = pg == own[b] ? ~0ull : ((1ull << 62) | ord | low);
       }
     }
-    s.key[b][pg] = key;
+    sl.key[b][pg] = key;
   }
   __syncthreads();
-  bitonic_desc(s.key[b], bt);
-  // s.key[b] sorted descending; the page of entry i is 1023 - (key & 1023)
-  auto page_at = [&](int i) -> int { return 1023 - (int)(s.key[b][i] & 1023ull); };
+  bitonic_desc(sl.key[b], bt);
+  // sl.key[b] sorted descending; the page of entry i is 1023 - (key & 1023)
+  auto page_at = [&](int i) -> int { return 1023 - (int)(sl.key[b][i] & 1023ull); };
   const bool row_ok = b < nrow;
   int32_t* idsrow = p.ids ? p.ids + ((long long)h * p.T + t0 + b) * p.C : nullptr;
-  for (int pg = bt; pg < P; pg += 128) s.sel[b][pg] = 0;
+  for (int pg = bt; pg < P; pg += 128) sl.sel[b][pg] = 0;
   __syncthreads();
   if (p.mode == 0) {
     // LUT = [own, 0..23, top C-25 candidates], already in order
     for (int i = bt; i < p.C; i += 128) {
       const int pg = i == 0 ? own[b] : (i <= kAnchors ? i - 1 : page_at(i - 1 - kAnchors));
-      s.sel[b][pg] = 1;
+      sl.sel[b][pg] = 1;
       if (row_ok && idsrow) idsrow[i] = pg;
     }
   } else if (p.mode == 2) {
     for (int i = bt; i < p.C; i += 128) {
       const int pg = page_at(i);
-      s.sel[b][pg] = 1;
+      sl.sel[b][pg] = 1;
       if (row_ok && idsrow) idsrow[i] = pg;
     }
   } else {
@@ -344,19 +414,19 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
     const int nh = p.total - A;
     for (int i = bt; i < p.C; i += 128) {
       const int pg = i < A ? page_at(i) : (i < A + nh ? page_at(kCurrent + i - A) : i - A - nh);
-      s.list[b][i] = pg;
-      s.sel[b][pg] = 1;
+      sl.list[b][i] = pg;
+      sl.sel[b][pg] = 1;
     }
     __syncthreads();
     if (idsrow) {
       for (int i = bt; i < p.C; i += 128) {
-        const int pg = s.list[b][i];
+        const int pg = sl.list[b][i];
         int slot = 0;
         if (pg != own[b]) {
           const uint32_t kx = orderable(s.risk[b][pg]);
           int rank = 0;
           for (int j = 0; j < p.C; ++j) {
-            const int y = s.list[b][j];
+            const int y = sl.list[b][j];
             if (y == own[b]) continue;
             const uint32_t ky = orderable(s.risk[b][y]);
             rank += (ky > kx) || (ky == kx && y < pg);
@@ -370,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void route_kernel(RouteParams p) {
   __syncthreads();
   if (p.mask) {
     for (int pg = bt; pg < P; pg += 128)
-      if (row_ok) p.mask[((long long)h * p.T + t0 + b) * P + pg] = s.sel[b][pg];
+      if (row_ok) p.mask[((long long)h * p.T + t0 + b) * P + pg] = sl.sel[b][pg];
   }
 }
 

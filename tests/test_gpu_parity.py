@@ -71,8 +71,15 @@ def test_route_base_matches_oracle(device, cfg, frames):
     ties = ref.near_tie_rows(cand, torch.full(x.own.shape, count - 25))
     got = ids.cpu()
     same = (got == want).all(-1)
-    print(f"P={P}: {int(same.sum())}/{same.numel()} rows identical, {int(ties.sum())} near-tie rows", flush=True)
-    assert bool((same | ties).all())
+    # rows whose ranked part holds near-equal risks may order those pages
+    # differently, with the same page set, in the kernel's own risk order
+    order_ties = ref.near_tie_order_rows(r64, want, 25)
+    same_set = (got.sort(-1).values == want.sort(-1).values).all(-1)
+    print(f"P={P}: {int(same.sum())}/{same.numel()} rows identical, {int(ties.sum())} near-tie rows, "
+          f"{int((order_ties & ~same).sum())} rows reordered among near-equal risks", flush=True)
+    assert bool((same | ties | (order_ties & same_set)).all())
+    ranked = risk.cpu().gather(-1, got[..., 25:].long())
+    assert bool((ranked[..., :-1] >= ranked[..., 1:]).all())
     # near-tie rows still keep the invariants
     assert (got[..., 0] == x.own).all() and (got[..., 1:25] == torch.arange(24)).all()
     assert (got.sort(-1).values.diff(dim=-1) > 0).all()

@@ -233,6 +233,17 @@ def test_select_topk_semantics():
             assert int(mask[hh, tt].sum()) == p // 10
 
 
+def test_near_tie_order_rows():
+    """Consecutive ranked pages within 1e-3 relative flag the row; the
+    unranked prefix (own + anchors) is ignored."""
+    r = torch.tensor([[[5.0, 4.0, 3.0, 2.0, 1.0], [5.0, 4.0, 3.0, 2.9995, 1.0]]])
+    ids = torch.tensor([[[0, 1, 2, 3, 4], [0, 1, 2, 3, 4]]])
+    assert ref.near_tie_order_rows(r, ids, 1).tolist() == [[False, True]]
+    r2 = torch.tensor([[[5.0, 4.9999, 3.0, 2.0, 1.0]]])
+    assert ref.near_tie_order_rows(r2, ids[:, :1], 2).tolist() == [[False]]
+    assert ref.near_tie_order_rows(r2, ids[:, :1], 0).tolist() == [[True]]
+
+
 def test_near_tie_rows():
     r = torch.tensor([[[5.0, 4.0, 3.9999, 1.0], [5.0, 4.0, 3.0, 1.0]]])
     ties = ref.near_tie_rows(r, torch.tensor([[2, 2]]))
