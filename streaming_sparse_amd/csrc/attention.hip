@@ -182,38 +182,48 @@ __device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, f32x
   }
 }
 
+// P = 2^(S*scale + nb) as the bf16 B operands of the two k steps (pb; pl =
+// the low parts bf16(P - bf16(P)) for the two-term product).
+template <bool PRECISE>
+__device__ __forceinline__ void probabilities(const f32x16& S, float nb, float scale_log2, u32x4 (&pb)[2],
+                                              u32x4 (&pl)[2]) {
+  float P[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) P[i] = __builtin_amdgcn_exp2f(fmaf(S[i], scale_log2, nb));
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int o = 8 * ks;
+    pb[ks] = u32x4{pack_bf16(P[o + 0], P[o + 1]), pack_bf16(P[o + 2], P[o + 3]), pack_bf16(P[o + 4], P[o + 5]),
+                   pack_bf16(P[o + 6], P[o + 7])};
+    pl[ks] = u32x4{};
+    if (PRECISE) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        pl[ks][w] = pack_bf16(P[o + 2 * w] - bf16_lo(pb[ks][w]), P[o + 2 * w + 1] - bf16_hi(pb[ks][w]));
+    }
+  }
+}
+
 // bf16 1.0 in both halves: the A operand whose product with P^T puts the
 // row sums of P in every row of the accumulator.
 constexpr uint32_t kOnes = 0x3F803F80u;
 
-// P = 2^(S*scale + nb); O^T += V^T P^T and L += 1 P^T (the softmax
-// denominator of lane's query over the pair's 32 keys, summed by the matrix
-// pipe from the same bf16 P that multiplies V).
+// O^T += V^T P^T and L += 1 P^T (the softmax denominator of lane's query over
+// the pair's 32 keys, summed by the matrix pipe from the same bf16 P that
+// multiplies V).
 template <bool PRECISE>
-__device__ __forceinline__ void softmax_pv(const f32x16& S, float nb, float scale_log2, const lds_u8* vbuf,
-                                           int pair, int lane, f32x16& L, f32x16 (&O)[4]) {
-  float P[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) P[i] = __builtin_amdgcn_exp2f(fmaf(S[i], scale_log2, nb));
+__device__ __forceinline__ void pv(const u32x4 (&pb)[2], const u32x4 (&pl)[2], const lds_u8* vbuf, int pair,
+                                   int lane, f32x16& L, f32x16 (&O)[4]) {
   const u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const int o = 8 * ks;
-    const u32x4 pb = {pack_bf16(P[o + 0], P[o + 1]), pack_bf16(P[o + 2], P[o + 3]), pack_bf16(P[o + 4], P[o + 5]),
-                      pack_bf16(P[o + 6], P[o + 7])};
-    u32x4 pl = {};
-    if (PRECISE) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        pl[w] = pack_bf16(P[o + 2 * w] - bf16_lo(pb[w]), P[o + 2 * w + 1] - bf16_hi(pb[w]));
-    }
-    L = mfma32(ones, pb, L);
-    if (PRECISE) L = mfma32(ones, pl, L);
+    L = mfma32(ones, pb[ks], L);
+    if (PRECISE) L = mfma32(ones, pl[ks], L);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const u32x4 va = v_operand(vbuf, pair, ks, dt, lane);
-      O[dt] = mfma32(va, pb, O[dt]);
-      if (PRECISE) O[dt] = mfma32(va, pl, O[dt]);
+      O[dt] = mfma32(va, pb[ks], O[dt]);
+      if (PRECISE) O[dt] = mfma32(va, pl[ks], O[dt]);
     }
   }
 }
@@ -290,16 +300,24 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
   // One unit with a successor: loads of K unit i+2 (clamped to the last
   // unit; a surplus load lands in a slot nobody reads again) and V unit i+1,
-  // S of unit i+1, softmax and P.V of unit i, then the max of unit i+1.
+  // S of unit i+1, the probabilities of unit i, the max of unit i+1 (before
+  // the P.V products, so it does not wait behind them in the matrix pipe),
+  // then P.V of unit i.  Unit ids run one step ahead in registers.
+  int u1 = unit(min(1, nunits - 1)), u2 = unit(min(2, nunits - 1));
   auto step = [&](int i, f32x16& Sc, f32x16& Sn) {
     const int cur = i & 1, nxt = cur ^ 1;
-    issue_rows(p, unit(min(i + 2, nunits - 1)), 0, h, wave, lane, page_off, rep_off, kslot(cur));
-    issue_rows(p, unit(i + 1), 1, h, wave, lane, page_off, rep_off, vslot(nxt));
+    const int u3 = unit(min(i + 3, nunits - 1));
+    issue_rows(p, u2, 0, h, wave, lane, page_off, rep_off, kslot(cur));
+    issue_rows(p, u1, 1, h, wave, lane, page_off, rep_off, vslot(nxt));
     const float nb = bias - (m == -INFINITY ? 0.0f : m);
     Sn = s_tile(kslot(nxt), pair, lane, qop);
-    softmax_pv<PRECISE>(Sc, nb, p.scale_log2, vslot(cur), pair, lane, L, O);
-    bias = unit_max(Sn, unit(i + 1), maskw, p.P, pair, lane, p.scale_log2, mloc);
+    u32x4 pb[2], pl[2];
+    probabilities<PRECISE>(Sc, nb, p.scale_log2, pb, pl);
+    bias = unit_max(Sn, u1, maskw, p.P, pair, lane, p.scale_log2, mloc);
+    pv<PRECISE>(pb, pl, vslot(cur), pair, lane, L, O);
     update_max(mloc, m, L, O);
+    u1 = u2;
+    u2 = u3;
     wait_loads();
     __syncthreads();
   };
@@ -314,7 +332,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
     S0 = S1;
   }
   // last unit
-  softmax_pv<PRECISE>(S0, bias - (m == -INFINITY ? 0.0f : m), p.scale_log2, vslot(i & 1), pair, lane, L, O);
+  {
+    u32x4 pb[2], pl[2];
+    probabilities<PRECISE>(S0, bias - (m == -INFINITY ? 0.0f : m), p.scale_log2, pb, pl);
+    pv<PRECISE>(pb, pl, vslot(i & 1), pair, lane, L, O);
+  }
   __syncthreads();
   // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS
   const float l = L[0];
