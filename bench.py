@@ -28,6 +28,10 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+# HBM bytes per attn_kernel launch of the base-tier call, keyed by (pages, exact pages), measured with
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this bench (profiles/attn_kernel_base432_traffic.md):
+# 117.4 MB read + 14.2 MB written
+MEASURED_TRAFFIC = {(432, 64): 131.6e6}
 METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
@@ -164,6 +168,10 @@ def main():
     achieved_tflops = (exact_flop + comp_flop) / (attn_ms * 1e-3) / 1e12
     gather_gbs = gather_bytes / (attn_ms * 1e-3) / 1e9
 
+    # HBM bytes per attn_kernel launch (rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors from a copy
+    # kernel), known for the default workload only
+    traffic = MEASURED_TRAFFIC.get((P, C)) if not args.precise_av else None
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(x, C, args.cpu_sample_blocks)
@@ -190,12 +198,14 @@ def main():
         "dense_sdpa_ms": None if dense_ms is None else round(dense_ms, 4),
         "ratio_vs_dense": None if dense_ms is None else round(ms_call / dense_ms, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved_tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "kernel": "attn_kernel (exact + compensation + merge)",
                      "algorithmic_gflop": round((exact_flop + comp_flop) / 1e9, 2),
+                     "hbm_GBps": None if traffic is None else round(traffic / (attn_ms * 1e-3) / 1e9, 1),
+                     "hbm_frac_of_peak": None if traffic is None else
+                     round(traffic / (attn_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                      "page_gather_gb": round(gather_bytes / 1e9, 3),
-                     "page_gather_GBps": round(gather_gbs, 1),
-                     "page_gather_frac_of_hbm_peak": round(gather_gbs / PEAK_HBM_GBS, 4)},
+                     "page_gather_GBps_from_l2": round(gather_gbs, 1)},
         "extra": extra,
         "cpu_baseline": cpu,
         "input_gen_s": round(gen_s, 2),
