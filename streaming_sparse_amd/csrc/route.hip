@@ -108,24 +108,80 @@ __device__ __forceinline__ void rep_logits(const u32x4 (&av)[8], const u32x4 (&q
   for (int st = 0; st < 8; ++st) S = mfma32(av[st], qop[st], S);
 }
 
-// Descending bitonic sort of 512 keys by the 128 threads of one row group;
-// every thread of the workgroup calls it (both rows sort in lockstep).
-__device__ __forceinline__ void bitonic_desc(unsigned long long* key, int bt) {
-  for (int k = 2; k <= kMaxPages; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
+// Value of lane (lane ^ LX) for a 64-bit key: DPP quad permutes for 1 and 2,
+// ds_swizzle bit-mask mode for 4, 8 and 16, the 32-lane swap for 32.
+template <int LX>
+__device__ __forceinline__ uint32_t xlane32(uint32_t v, int lane) {
+  if constexpr (LX == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);   // [1,0,3,2]
+  else if constexpr (LX == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);   // [2,3,0,1]
+  else if constexpr (LX == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return lane < 32 ? r[1] : r[0];
+  } else {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (LX << 10) | 0x1F);
+  }
+}
+
+template <int LX>
+__device__ __forceinline__ unsigned long long xlane64(unsigned long long v, int lane) {
+  const uint32_t lo = xlane32<LX>((uint32_t)v, lane), hi = xlane32<LX>((uint32_t)(v >> 32), lane);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+// Descending bitonic sort of one row's 512 keys, held 4 per thread (element
+// 4*bt + i in key[i]) by the row's 128 threads (two waves): partner distance
+// 1 and 2 inside the thread, 4..128 by cross-lane shuffles inside the wave,
+// 256 through LDS (`xchg`, the row's 512 slots) between the two waves.  Every
+// thread of the workgroup calls it (both rows sort in lockstep; two barriers).
+__device__ __forceinline__ void sort512_desc(unsigned long long (&key)[4], int bt, unsigned long long* xchg) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int i = bt + 128 * r;                        // pair index 0..255
-        const int lo = 2 * i - (i & (j - 1));              // i with a zero bit inserted at j
-        const int hi = lo + j;
-        const bool desc = (lo & k) == 0;
-        const unsigned long long a = key[lo], c = key[hi];
-        if ((a < c) == desc) {
-          key[lo] = c;
-          key[hi] = a;
+  for (int k = 2; k <= kMaxPages; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (i & j) continue;
+          const int e = 4 * bt + i;
+          const bool desc = (e & k) == 0;
+          const unsigned long long x = key[i], y = key[i | j];
+          if ((x < y) == desc) {
+            key[i] = y;
+            key[i | j] = x;
+          }
+        }
+      } else {
+        unsigned long long other[4];
+        if (j <= 128) {
+          const int lane = bt & 63;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            switch (j) {
+              case 4: other[i] = xlane64<1>(key[i], lane); break;
+              case 8: other[i] = xlane64<2>(key[i], lane); break;
+              case 16: other[i] = xlane64<4>(key[i], lane); break;
+              case 32: other[i] = xlane64<8>(key[i], lane); break;
+              case 64: other[i] = xlane64<16>(key[i], lane); break;
+              default: other[i] = xlane64<32>(key[i], lane); break;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xchg[4 * bt + i] = key[i];
+          __syncthreads();
+#pragma unroll
+          for (int i = 0; i < 4; ++i) other[i] = xchg[(4 * bt + i) ^ j];
+          __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * bt + i;
+          const bool desc = (e & k) == 0;
+          const bool keep_max = ((e & j) == 0) == desc;
+          const unsigned long long x = key[i], y = other[i];
+          key[i] = keep_max ? (x > y ? x : y) : (x < y ? x : y);
         }
       }
-      __syncthreads();
     }
   }
 }
@@ -358,10 +414,10 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
 
   // ---------------------------------------------------------------- select
   Sel& sl = *reinterpret_cast<Sel*>(&s.ring[0][0][0]);
-  // Row b is sorted by 128 threads (tid / 128 = b) with a bitonic network
-  // over 512 64-bit keys, descending.  Key = (group << 62) | (orderable
-  // risk << 30) | (1023 - page): risk descending, ties -> lower page, and
-  // the group field orders the partitions (base / top-k: one group).
+  // Row b is sorted by its 128 threads (tid / 128 = b), 512 64-bit keys,
+  // descending.  Key = (group << 62) | (orderable risk << 30) | (1023 - page):
+  // risk descending, ties -> lower page, and the group field orders the
+  // partitions (base / top-k: one group).
   const int b = tid >> 7, bt = tid & 127;
   int own[2];
 #pragma unroll
@@ -370,7 +426,10 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     own[q] = p.own ? p.own[(long long)h * p.T + tb] : P - p.T + tb;
   }
   const int A = p.mode == 1 ? p.current[h] : 0;
-  for (int pg = bt; pg < kMaxPages; pg += 128) {
+  unsigned long long keys[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pg = 4 * bt + i;
     unsigned long long key = 0ull;
     if (pg < P) {
       const unsigned long long ord = (unsigned long long)orderable(s.risk[b][pg]) << 30;
@@ -385,10 +444,12 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
         key = pg == own[b] ? ~0ull : ((1ull << 62) | ord | low);
       }
     }
-    sl.key[b][pg] = key;
+    keys[i] = key;
   }
+  sort512_desc(keys, bt, sl.key[b]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sl.key[b][4 * bt + i] = keys[i];
   __syncthreads();
-  bitonic_desc(sl.key[b], bt);
   // sl.key[b] sorted descending; the page of entry i is 1023 - (key & 1023)
   auto page_at = [&](int i) -> int { return 1023 - (int)(sl.key[b][i] & 1023ull); };
   const bool row_ok = b < nrow;
