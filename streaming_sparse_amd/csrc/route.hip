@@ -197,51 +197,11 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   const int blk = pi >> 4, m = pi & 15;
   const int tq = min(t0 + blk, p.T - 1);
 
-  // probe operand (B): dims 16*st + 8*hh + [0,8) (the k order of read_reps).
-  // q2[g] = sum of q^2 over dims 16g..16g+15 / D, summed in one lane per
-  // group from the dims 64*hh + [0,64) of this lane half
-  const long long row = p.gathered ? m : kProbeOffsets[m];
-  const uint16_t* qp = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
-  u32x4 qop[8];
-  float q2[8];
-#pragma unroll
-  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st + 8 * hh);
-  {
-    float g4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const u32x4 v = ldg16(qp + 64 * hh + 8 * st);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float a = bf16_lo(v[w]), b = bf16_hi(v[w]);
-        g4[st >> 1] += a * a + b * b;
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float other = __shfl_xor(g4[g], 32);
-      q2[4 * hh + g] = g4[g] / kHeadDim;
-      q2[4 * (1 - hh) + g] = other / kHeadDim;
-    }
-  }
-  float qsum = 0.f;
-#pragma unroll
-  for (int g = 0; g < 8; ++g) qsum += q2[g];
-  const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
-
   const uint16_t* rkh = p.rk + (long long)h * p.HP * 4 * kHeadDim;
   const uint16_t* sth = p.stats + (long long)h * p.HP * 48;
   const int ntiles = (P + 7) >> 3;
   // logits in log2 units: z2 = q.k * log2(e) / sqrt(D); prob = 2^(z2 - max2) / den
   const float c2 = kLog2e / sqrtf((float)kHeadDim);
-  // per-head bound of the page value norm: max_p stats[p,1,11] (read after pass 1)
-  {
-    float b = -INFINITY;
-    for (int i = tid; i < P; i += kThreads) b = fmaxf(b, bf16_to_f32(sth[i * 48 + 12 + 11]));
-    b = wave_max(b);
-    if (lane == 0) s.bmax_w[wave] = b;
-  }
-
   // Each wave owns tiles wave + 4 j (j < nmine) and a double buffer of them
   // in LDS: no other wave reads its slots, so its own load counter orders
   // them.  A wave without tiles (P < 32) re-reads tile `wave` and skips it.
@@ -276,17 +236,54 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   };
   auto wait_lds = [&]() { __builtin_amdgcn_s_waitcnt(0xC07F); };   // lgkmcnt(0)
 
-  // pass 1: max and sum of exp over all reps, per probe
-  float mx = -INFINITY, den = 0.f;
-  issue_tile(mine(0), 0, false);
-  issue_tile(mine(1), 1, false);
+  // pass 1's first two tiles are in flight while the probe rows load
+  issue_tile(mine(0), 0, true);
+  issue_tile(mine(1), 1, true);
+
+  // probe operand (B): dims 16*st + 8*hh + [0,8) (the k order of read_reps).
+  // q2[g] = sum of q^2 over dims 16g..16g+15 / D, summed in one lane per
+  // group from the dims 64*hh + [0,64) of this lane half
+  const long long row = p.gathered ? m : kProbeOffsets[m];
+  const uint16_t* qp = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
+  u32x4 qop[8];
+  float q2[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st + 8 * hh);
+  {
+    float g4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const u32x4 v = ldg16(qp + 64 * hh + 8 * st);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float a = bf16_lo(v[w]), b = bf16_hi(v[w]);
+        g4[st >> 1] += a * a + b * b;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float other = __shfl_xor(g4[g], 32);
+      q2[4 * hh + g] = g4[g] / kHeadDim;
+      q2[4 * (1 - hh) + g] = other / kHeadDim;
+    }
+  }
+  float qsum = 0.f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) qsum += q2[g];
+  const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
+
+  // pass 1: max and sum of exp over all reps, per probe, and the per-head
+  // bound of the page value norm max_p stats[p,1,11] from the tiles' stats
+  float mx = -INFINITY, den = 0.f, bmax = -INFINITY;
   for (int j = 0; j < nmine; ++j) {
     const int tile = mine(j);
-    wait_tile(8);                                    // tile j landed (tile j+1 may be in flight)
+    wait_tile(9);                                    // tile j landed (tile j+1 may be in flight)
     u32x4 av[8];
     read_reps(ring + (j & 1) * kSlotBytes, lane, av);
+    if (lane < 8 && tile * 8 + lane < P)
+      bmax = fmaxf(bmax, bf16_to_f32(((lds_u16*)(ring + (j & 1) * kSlotBytes + 8192))[lane * 48 + 23]));
     wait_lds();
-    issue_tile(mine(j + 2), j & 1, false);
+    issue_tile(mine(j + 2), j & 1, true);
     f32x16 S;
     rep_logits(av, qop, S);
     float tmax = -INFINITY;
@@ -317,6 +314,8 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       s.part[wave][pi][0] = mx;
       s.part[wave][pi][1] = den;
     }
+    bmax = wave_max(bmax);
+    if (lane == 0) s.bmax_w[wave] = bmax;
   }
   __syncthreads();
   float MX = -INFINITY;
@@ -328,7 +327,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   const float inv_den = 1.0f / DEN;
   if (p.lse && wave == 0 && hh == 0 && t0 + blk < p.T)
     p.lse[((long long)h * p.T + t0 + blk) * 16 + m] = (MX + __log2f(DEN)) * 0.69314718055994531f;
-  const float bmax = fmaxf(fmaxf(s.bmax_w[0], s.bmax_w[1]), fmaxf(s.bmax_w[2], s.bmax_w[3]));
+  bmax = fmaxf(fmaxf(s.bmax_w[0], s.bmax_w[1]), fmaxf(s.bmax_w[2], s.bmax_w[3]));
   const float th0 = p.theta[h * 4 + 0], th1 = p.theta[h * 4 + 1], th2 = p.theta[h * 4 + 2], th3 = p.theta[h * 4 + 3];
 
   // pass 2: probabilities -> four features -> theta-weighted value -> probe mean.
