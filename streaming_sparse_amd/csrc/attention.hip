@@ -71,12 +71,12 @@ struct UnitOffsets {
   uint32_t k[4], v[4];
 };
 
-__device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long long rs, int last) {
+__device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long long rs, int last, int nb) {
   UnitOffsets o;
-  const int pc = lane & 15;
+  const int pc = lane & 15, rows = 16 / nb;
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
-    const int row = 16 * wave + 4 * jj + (lane >> 4);
+    const int row = rows * wave + 4 * jj + (lane >> 4);
     const uint32_t r = (uint32_t)(min(row, last) * rs);
     o.k[jj] = 2u * (r + 8u * (uint32_t)(pc ^ (row & 15)));
     o.v[jj] = 2u * (r + 8u * (uint32_t)(pc ^ vswz(row)));
@@ -85,14 +85,17 @@ __device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long lon
 }
 
 // Enqueue the global->LDS loads of the K rows (kv = 0) or V rows (kv = 1)
-// of unit e (page e >= 0, rep tile -1-e < 0) into `buf`.
+// of unit e (page e >= 0, rep tile -1-e < 0) into `buf`: wave w of the
+// 4*NB waves loads rows (16/NB) w .. (16/NB) w + 16/NB - 1.
+template <int NB>
 __device__ __forceinline__ void issue_rows(const AttnParams& p, int e, int kv, int h, int wave, int lane,
                                            const UnitOffsets& page_off, const UnitOffsets& rep_off, lds_u8* buf) {
-  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)buf + wave * 4096);
+  constexpr int kLoads = 4 / NB;    // 1 KB loads per wave
+  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)buf + wave * 1024 * kLoads);
   // each path issues with its own offset registers (no copies into a common set)
   auto issue = [&](const uint16_t* base, const UnitOffsets& o) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dma16(base, kv ? o.v[jj] : o.k[jj], l + jj * 1024);
+    for (int jj = 0; jj < kLoads; ++jj) dma16(base, kv ? o.v[jj] : o.k[jj], l + jj * 1024);
   };
   if (e >= 0) {
     issue((kv ? p.v : p.k) + (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head, page_off);
@@ -105,7 +108,7 @@ __device__ __forceinline__ void issue_rows(const AttnParams& p, int e, int kv, i
     if (last >= 63)
       issue(base, rep_off);
     else
-      issue(base, unit_offsets(wave, lane, kHeadDim, last));
+      issue(base, unit_offsets(wave, lane, kHeadDim, last, NB));
   }
 }
 
@@ -228,43 +231,52 @@ __device__ __forceinline__ void pv(const u32x4 (&pb)[2], const u32x4 (&pl)[2], c
   }
 }
 
-template <bool PRECISE>
-__global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
+// NB query blocks per workgroup (4 waves each).  NB = 1: the general call
+// (own page table, rep tiles).  NB = 2: a call that selects every page, so
+// both blocks walk the same units (pages 0..P-1) and share each K/V load.
+template <bool PRECISE, int NB>
+__global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams p) {
   // LDS ring: K rows of units i (slot i & 1) run two units ahead of use, V
   // rows one unit ahead.  Iteration i reads K slot (i+1)&1 and V slot i&1
   // while the loads of K unit i+2 and V unit i+1 land in the other slots.
-  __shared__ alignas(16) uint8_t kring[2 * kBuf];
-  __shared__ alignas(16) uint8_t vring[2 * kBuf];
+  __shared__ alignas(16) uint8_t ring[4 * kBuf];   // K slot 0 | K slot 1 | V slot 0 | V slot 1
   __shared__ int units[kMaxCount + kMaxRepTiles];
   __shared__ uint32_t maskw[16];
-  __shared__ float xm[2][64], xl[2][64];
+  __shared__ float xm[NB][2][64], xl[NB][2][64];
   __shared__ int nunits_s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pair = wave >> 1, qw = wave & 1;
-  const int work = xcd_remap(blockIdx.x, p.H * p.T);
-  const int h = work / p.T, t = work % p.T;
-  if (tid < 16) maskw[tid] = 0u;
-  __syncthreads();
-  const int32_t* ids = p.ids + ((long long)h * p.T + t) * p.C;
-  for (int i = tid; i < p.C; i += kThreads) {
-    const int pg = min(max(ids[i], 0), p.P - 1);
-    units[i] = pg;
-    atomicOr(&maskw[pg >> 5], 1u << (pg & 31));
-  }
-  __syncthreads();
-  if (wave == 0) {
-    const int R = (p.P + 15) >> 4;
-    bool live = false;
-    if (lane < R) {
-      const int p0 = lane * 16;
-      const uint32_t word = (maskw[p0 >> 5] >> (p0 & 31)) & 0xffffu;
-      const int valid = min(16, p.P - p0);
-      const uint32_t vmask = valid >= 16 ? 0xffffu : ((1u << valid) - 1u);
-      live = (~word & vmask) != 0u;
+  const int grp = wave >> 2, pair = (wave >> 1) & 1, qw = wave & 1;
+  const int TB = p.T / NB;
+  const int work = xcd_remap(blockIdx.x, p.H * TB);
+  const int h = work / TB, t = (work % TB) * NB + grp;
+  if (NB == 1) {
+    if (tid < 16) maskw[tid] = 0u;
+    __syncthreads();
+    const int32_t* ids = p.ids + ((long long)h * p.T + t) * p.C;
+    for (int i = tid; i < p.C; i += kThreads) {
+      const int pg = min(max(ids[i], 0), p.P - 1);
+      units[i] = pg;
+      atomicOr(&maskw[pg >> 5], 1u << (pg & 31));
     }
-    const unsigned long long bal = __ballot(live);
-    if (live) units[p.C + __popcll(bal & ((1ull << lane) - 1ull))] = -1 - lane;
-    if (lane == 0) nunits_s = p.C + __popcll(bal);
+    __syncthreads();
+    if (wave == 0) {
+      const int R = (p.P + 15) >> 4;
+      bool live = false;
+      if (lane < R) {
+        const int p0 = lane * 16;
+        const uint32_t word = (maskw[p0 >> 5] >> (p0 & 31)) & 0xffffu;
+        const int valid = min(16, p.P - p0);
+        const uint32_t vmask = valid >= 16 ? 0xffffu : ((1u << valid) - 1u);
+        live = (~word & vmask) != 0u;
+      }
+      const unsigned long long bal = __ballot(live);
+      if (live) units[p.C + __popcll(bal & ((1ull << lane) - 1ull))] = -1 - lane;
+      if (lane == 0) nunits_s = p.C + __popcll(bal);
+    }
+  } else {
+    // every page exact, no rep tiles: units are the pages in order
+    for (int i = tid; i < p.P; i += kThreads * NB) units[i] = i;
+    if (tid == 0) nunits_s = p.P;
   }
   // query operand: lane's query row, dims 16*st + 8*hh + [0,8)
   const int r = lane & 31, hh = lane >> 5;
@@ -275,8 +287,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st);
   __syncthreads();
   const int nunits = nunits_s;
-  lds_u8* const kbase = (lds_u8*)kring;
-  lds_u8* const vbase = (lds_u8*)vring;
+  lds_u8* const kbase = (lds_u8*)ring;
+  lds_u8* const vbase = (lds_u8*)ring + 2 * kBuf;
   auto kslot = [&](int slot) { return kbase + slot * kBuf; };
   auto vslot = [&](int slot) { return vbase + slot * kBuf; };
 
@@ -284,13 +296,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   f32x16 L = {}, O[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
-  const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63);
-  const UnitOffsets rep_off = unit_offsets(wave, lane, kHeadDim, 63);
+  const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63, NB);
+  const UnitOffsets rep_off = unit_offsets(wave, lane, kHeadDim, 63, NB);
   auto unit = [&](int i) { return __builtin_amdgcn_readfirstlane(units[i]); };
   // prologue: K0, V0, K1 in flight; S of unit 0 and its max
-  issue_rows(p, unit(0), 0, h, wave, lane, page_off, rep_off, kslot(0));
-  issue_rows(p, unit(0), 1, h, wave, lane, page_off, rep_off, vslot(0));
-  issue_rows(p, unit(min(1, nunits - 1)), 0, h, wave, lane, page_off, rep_off, kslot(1));
+  issue_rows<NB>(p, unit(0), 0, h, wave, lane, page_off, rep_off, kslot(0));
+  issue_rows<NB>(p, unit(0), 1, h, wave, lane, page_off, rep_off, vslot(0));
+  issue_rows<NB>(p, unit(min(1, nunits - 1)), 0, h, wave, lane, page_off, rep_off, kslot(1));
   wait_loads();
   __syncthreads();
   f32x16 S0 = s_tile(kslot(0), pair, lane, qop), S1;
@@ -307,8 +319,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   auto step = [&](int i, f32x16& Sc, f32x16& Sn) {
     const int cur = i & 1, nxt = cur ^ 1;
     const int u3 = unit(min(i + 3, nunits - 1));
-    issue_rows(p, u2, 0, h, wave, lane, page_off, rep_off, kslot(cur));
-    issue_rows(p, u1, 1, h, wave, lane, page_off, rep_off, vslot(nxt));
+    issue_rows<NB>(p, u2, 0, h, wave, lane, page_off, rep_off, kslot(cur));
+    issue_rows<NB>(p, u1, 1, h, wave, lane, page_off, rep_off, vslot(nxt));
     const float nb = bias - (m == -INFINITY ? 0.0f : m);
     Sn = s_tile(kslot(nxt), pair, lane, qop);
     u32x4 pb[2], pl[2];
@@ -340,19 +352,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_kernel(AttnParams p) {
   __syncthreads();
   // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS
   const float l = L[0];
-  float* xo = reinterpret_cast<float*>(kring);     // [qw][64 items][64 lanes] fp32 = 32 KB
+  // [group][qw][64 items][64 lanes] fp32 = 32 KB per group
+  float* xo = reinterpret_cast<float*>(ring) + grp * 8192;
   if (pair == 1) {
     float* d = xo + qw * 4096 + lane;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) d[(16 * dt + i) * 64] = O[dt][i];
-    xm[qw][lane] = m;
-    xl[qw][lane] = l;
+    xm[grp][qw][lane] = m;
+    xl[grp][qw][lane] = l;
   }
   __syncthreads();
   if (pair == 1) return;
-  const float m1 = xm[qw][lane], l1 = xl[qw][lane];
+  const float m1 = xm[grp][qw][lane], l1 = xl[grp][qw][lane];
   const float mt = fmaxf(m, m1);
   const float mu = mt == -INFINITY ? 0.0f : mt;
   const float a0 = __builtin_amdgcn_exp2f(m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
@@ -435,11 +448,21 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   p.HPV = rep_head_pages;
   p.C = count;
   p.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
-  const dim3 grid(heads * p.T);
-  if (flags & 1)
-    hipLaunchKernelGGL(attn_kernel<true>, grid, dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL(attn_kernel<false>, grid, dim3(kThreads), 0, stream, p);
+  // a call that selects every page with an even number of blocks runs two
+  // blocks per workgroup on one shared K/V stream
+  if (count == pages && p.T % 2 == 0) {
+    const dim3 grid(heads * p.T / 2);
+    if (flags & 1)
+      hipLaunchKernelGGL((attn_kernel<true, 2>), grid, dim3(2 * kThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((attn_kernel<false, 2>), grid, dim3(2 * kThreads), 0, stream, p);
+  } else {
+    const dim3 grid(heads * p.T);
+    if (flags & 1)
+      hipLaunchKernelGGL((attn_kernel<true, 1>), grid, dim3(kThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((attn_kernel<false, 1>), grid, dim3(kThreads), 0, stream, p);
+  }
   return (int)hipGetLastError();
 }
 
