@@ -163,10 +163,12 @@ def test_attention_all_pages_equals_dense(device):
     check_out(out, want, "all pages exact")
 
 
-def test_attention_odd_window_and_slab(device):
+@pytest.mark.parametrize("n", [128, 192])
+def test_attention_odd_window_and_slab(device, n):
     """Window of 100 pages (last rep tile partly beyond P) inside a 128-page
-    summary slab, head-major strided K/V, single-page LUT."""
-    h, p, cap, n = 3, 100, 128, 128
+    summary slab, head-major strided K/V, single-page LUT; random page tables
+    per block, for an even and an odd number of query blocks."""
+    h, p, cap = 3, 100, 128
     gen = torch.Generator().manual_seed(77)
     q = torch.randn(1, n, h, 128, generator=gen).bfloat16()
     kk = torch.randn(h, 64 * p, 128, generator=gen).bfloat16()
@@ -180,7 +182,8 @@ def test_attention_odd_window_and_slab(device):
     k4 = kk.transpose(0, 1)[None]          # [1, L, H, D] view of head-major storage
     v4 = vv.transpose(0, 1)[None]
     for count in (1, 7):
-        ids = torch.stack([torch.randperm(p, generator=gen)[:count] for _ in range(h * 2)]).reshape(h, 2, count).int()
+        t = n // 64
+        ids = torch.stack([torch.randperm(p, generator=gen)[:count] for _ in range(h * t)]).reshape(h, t, count).int()
         sd = slab.slice(0, p)
         gd = Summary(*(getattr(slab, f).to(device) for f in Summary.FIELDS)).slice(0, p)
         kd = kk.to(device).transpose(0, 1)[None]
@@ -188,4 +191,4 @@ def test_attention_odd_window_and_slab(device):
         out = attention(q.to(device), kd, vd, gd, basis.to(device), ids.to(device), Workspace())
         torch.cuda.synchronize()
         want = ref.selected_attention(q, k4.contiguous(), v4.contiguous(), sd, basis, ids).bfloat16()
-        check_out(out, want, f"odd window count={count}")
+        check_out(out, want, f"odd window n={n} count={count}")
