@@ -64,51 +64,103 @@ __device__ __forceinline__ int k_off(int row, int chunk) { return row * 256 + ((
 __device__ __forceinline__ int vswz(int row) { return (0xEA40 >> (4 * (row & 3))) & 15; }   // 0, 4, 10, 14
 __device__ __forceinline__ int v_off(int row, int chunk) { return row * 256 + ((chunk ^ vswz(row)) << 4); }
 
+// A unit is a page p >= 0, or a rep tile rt (pages 16 rt .. 16 rt + 15) as
+// 0x80000000 | drop << 8 | rt, bit b of the 16-bit `drop` set when page
+// 16 rt + b is selected or beyond the window (its reps are masked out).
+__device__ __forceinline__ int rep_unit(int rt, uint32_t drop) { return (int)(0x80000000u | (drop << 8) | (uint32_t)rt); }
+__device__ __forceinline__ int rep_tile(int e) { return e & 0xff; }
+__device__ __forceinline__ uint32_t rep_drop(int e) { return ((uint32_t)e >> 8) & 0xffffu; }
+
 // Per-lane byte offsets of this wave's 4 K and 4 V rows of a unit (wave w
 // loads rows 16w..16w+15, 1 KB per instruction) for a row stride `rs`
-// (elements) and rows clamped to `last`.
+// (elements) and rows clamped to `last`.  With `inst` set, load jj's offset
+// leaves out the jj * 1024 that its instruction offset adds (that offset
+// moves the LDS destination by the same amount); rows >= 4 jj and rs >= 128
+// keep these offsets non-negative.
 struct UnitOffsets {
   uint32_t k[4], v[4];
 };
 
-__device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long long rs, int last, int nb) {
+__device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long long rs, int last, int nb, bool inst) {
   UnitOffsets o;
   const int pc = lane & 15, rows = 16 / nb;
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
     const int row = rows * wave + 4 * jj + (lane >> 4);
     const uint32_t r = (uint32_t)(min(row, last) * rs);
-    o.k[jj] = 2u * (r + 8u * (uint32_t)(pc ^ (row & 15)));
-    o.v[jj] = 2u * (r + 8u * (uint32_t)(pc ^ vswz(row)));
+    const uint32_t sub = inst ? 1024u * jj : 0u;
+    o.k[jj] = 2u * (r + 8u * (uint32_t)(pc ^ (row & 15))) - sub;
+    o.v[jj] = 2u * (r + 8u * (uint32_t)(pc ^ vswz(row))) - sub;
   }
   return o;
 }
 
+// N consecutive 1 KB global->LDS loads of one wave: load jj reads base +
+// off[jj] + jj * 1024 (per lane) into lds + jj * 1024 + 16 * lane, with one
+// M0 write for all of them.
+template <int N>
+__device__ __forceinline__ void dma_rows(const void* base, const uint32_t (&off)[4], uint32_t lds) {
+  if constexpr (N == 4) {
+    asm volatile(
+        "s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %5\n\t"
+        "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
+        "global_load_lds_dwordx4 %2, %5 offset:2048\n\t"
+        "global_load_lds_dwordx4 %3, %5 offset:3072" ::"v"(off[0]),
+        "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(lds), "s"(base)
+        : "memory", "m0");
+  } else {
+    static_assert(N == 2, "2 or 4 loads");
+    asm volatile(
+        "s_mov_b32 m0, %2\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %3 offset:1024" ::"v"(off[0]),
+        "v"(off[1]), "s"(lds), "s"(base)
+        : "memory", "m0");
+  }
+}
+
+// Where a workgroup's units come from: head h's K, V, rep key and rep value
+// rows as byte pointers, and the byte stride of a page.
+struct UnitSources {
+  const uint8_t *k, *v, *rk, *rv;
+  uint32_t page_bytes;
+};
+
+__device__ __forceinline__ UnitSources unit_sources(const AttnParams& p, int h) {
+  UnitSources u;
+  u.k = (const uint8_t*)(p.k + (long long)h * p.kv_head);
+  u.v = (const uint8_t*)(p.v + (long long)h * p.kv_head);
+  u.rk = (const uint8_t*)(p.rk + (long long)h * p.HP * 4 * kHeadDim);
+  u.rv = (const uint8_t*)(p.rv + (long long)h * p.HPV * 4 * kHeadDim);
+  u.page_bytes = (uint32_t)(128 * p.kv_tok);
+  return u;
+}
+
 // Enqueue the global->LDS loads of the K rows (kv = 0) or V rows (kv = 1)
-// of unit e (page e >= 0, rep tile -1-e < 0) into `buf`: wave w of the
-// 4*NB waves loads rows (16/NB) w .. (16/NB) w + 16/NB - 1.
+// of unit e (a page, or a rep tile) into `buf`: wave w of the 4*NB waves
+// loads rows (16/NB) w .. (16/NB) w + 16/NB - 1.  page_off / rep_off are the
+// instruction-offset forms of unit_offsets.
 template <int NB>
-__device__ __forceinline__ void issue_rows(const AttnParams& p, int e, int kv, int h, int wave, int lane,
-                                           const UnitOffsets& page_off, const UnitOffsets& rep_off, lds_u8* buf) {
+__device__ __forceinline__ void issue_rows(const AttnParams& p, const UnitSources& src, int e, int kv, int wave,
+                                           int lane, const UnitOffsets& page_off, const UnitOffsets& rep_off,
+                                           lds_u8* buf) {
   constexpr int kLoads = 4 / NB;    // 1 KB loads per wave
   const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)buf + wave * 1024 * kLoads);
-  // each path issues with its own offset registers (no copies into a common set)
-  auto issue = [&](const uint16_t* base, const UnitOffsets& o) {
-#pragma unroll
-    for (int jj = 0; jj < kLoads; ++jj) dma16(base, kv ? o.v[jj] : o.k[jj], l + jj * 1024);
-  };
   if (e >= 0) {
-    issue((kv ? p.v : p.k) + (long long)e * 64 * p.kv_tok + (long long)h * p.kv_head, page_off);
+    dma_rows<kLoads>((kv ? src.v : src.k) + (uint32_t)e * src.page_bytes, kv ? page_off.v : page_off.k, l);
   } else {
-    const int rt = -1 - e;
-    const uint16_t* base = kv ? p.rv + ((long long)h * p.HPV * 4 + rt * 64) * kHeadDim
-                              : p.rk + ((long long)h * p.HP * 4 + rt * 64) * kHeadDim;
+    const int rt = rep_tile(e);
+    const uint8_t* base = (kv ? src.rv : src.rk) + (uint32_t)rt * (64 * 256);
     // rows of pages >= P re-read the last valid rep (masked in compute)
     const int last = p.P * 4 - rt * 64 - 1;
-    if (last >= 63)
-      issue(base, rep_off);
-    else
-      issue(base, unit_offsets(wave, lane, kHeadDim, last, NB));
+    if (last >= 63) {
+      dma_rows<kLoads>(base, kv ? rep_off.v : rep_off.k, l);
+    } else {
+      const UnitOffsets o = unit_offsets(wave, lane, kHeadDim, last, NB, false);
+#pragma unroll
+      for (int jj = 0; jj < kLoads; ++jj) dma16(base, kv ? o.v[jj] : o.k[jj], l + jj * 1024);
+    }
   }
 }
 
@@ -141,17 +193,11 @@ __device__ __forceinline__ f32x16 s_tile(const lds_u8* kbuf, int pair, int lane,
 
 // Row max of S in log2 units (+ bias); rep tiles first drop the reps of
 // selected pages and of pages >= P.  Returns the bias of the unit.
-__device__ __forceinline__ float unit_max(f32x16& S, int e, const uint32_t* maskw, int P, int pair, int lane,
-                                          float scale_log2, float& mloc) {
+__device__ __forceinline__ float unit_max(f32x16& S, int e, int pair, int lane, float scale_log2, float& mloc) {
   float bias = 0.0f;
   if (e < 0) {
     bias = 4.0f;
-    const int rt = -1 - e, hh = lane >> 5;
-    // bit b of `drop`: page 16 rt + b is selected or beyond the window
-    const uint32_t sel = (maskw[rt >> 1] >> (16 * (rt & 1))) & 0xffffu;
-    const int valid = P - 16 * rt;
-    const uint32_t inside = valid >= 16 ? 0xffffu : ((1u << valid) - 1u);
-    const uint32_t drop = (sel | ~inside) >> (8 * pair + hh);
+    const uint32_t drop = rep_drop(e) >> (8 * pair + (lane >> 5));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bool d = (drop >> (2 * j)) & 1u;
@@ -231,6 +277,39 @@ __device__ __forceinline__ void pv(const u32x4 (&pb)[2], const u32x4 (&pl)[2], c
   }
 }
 
+// Unit list of tile (t, h): its C pages, then the rep tiles holding at least
+// one page the table does not select (each carrying its drop mask); maskw
+// gets the 512-bit page mask.
+// Called by every thread of the workgroup (`nthreads` of them).
+__device__ void own_units(const AttnParams& p, int h, int t, int tid, int nthreads, int* units, uint32_t* maskw,
+                          int* nunits) {
+  if (tid < 16) maskw[tid] = 0u;
+  __syncthreads();
+  const int32_t* ids = p.ids + ((long long)h * p.T + t) * p.C;
+  for (int i = tid; i < p.C; i += nthreads) {
+    const int pg = min(max(ids[i], 0), p.P - 1);
+    units[i] = pg;
+    atomicOr(&maskw[pg >> 5], 1u << (pg & 31));
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int lane = tid, R = (p.P + 15) >> 4;
+    bool live = false;
+    uint32_t drop = 0xffffu;
+    if (lane < R) {
+      const int p0 = lane * 16;
+      const uint32_t word = (maskw[p0 >> 5] >> (p0 & 31)) & 0xffffu;
+      const int valid = min(16, p.P - p0);
+      const uint32_t vmask = valid >= 16 ? 0xffffu : ((1u << valid) - 1u);
+      drop = (word | ~vmask) & 0xffffu;
+      live = drop != 0xffffu;
+    }
+    const unsigned long long bal = __ballot(live);
+    if (live) units[p.C + __popcll(bal & ((1ull << lane) - 1ull))] = rep_unit(lane, drop);
+    if (lane == 0) *nunits = p.C + __popcll(bal);
+  }
+}
+
 // NB query blocks per workgroup (4 waves each).  NB = 1: the general call
 // (own page table, rep tiles).  NB = 2: a call that selects every page, so
 // both blocks walk the same units (pages 0..P-1) and share each K/V load.
@@ -250,29 +329,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const int work = xcd_remap(blockIdx.x, p.H * TB);
   const int h = work / TB, t = (work % TB) * NB + grp;
   if (NB == 1) {
-    if (tid < 16) maskw[tid] = 0u;
-    __syncthreads();
-    const int32_t* ids = p.ids + ((long long)h * p.T + t) * p.C;
-    for (int i = tid; i < p.C; i += kThreads) {
-      const int pg = min(max(ids[i], 0), p.P - 1);
-      units[i] = pg;
-      atomicOr(&maskw[pg >> 5], 1u << (pg & 31));
-    }
-    __syncthreads();
-    if (wave == 0) {
-      const int R = (p.P + 15) >> 4;
-      bool live = false;
-      if (lane < R) {
-        const int p0 = lane * 16;
-        const uint32_t word = (maskw[p0 >> 5] >> (p0 & 31)) & 0xffffu;
-        const int valid = min(16, p.P - p0);
-        const uint32_t vmask = valid >= 16 ? 0xffffu : ((1u << valid) - 1u);
-        live = (~word & vmask) != 0u;
-      }
-      const unsigned long long bal = __ballot(live);
-      if (live) units[p.C + __popcll(bal & ((1ull << lane) - 1ull))] = -1 - lane;
-      if (lane == 0) nunits_s = p.C + __popcll(bal);
-    }
+    own_units(p, h, t, tid, kThreads, units, maskw, &nunits_s);
   } else {
     // every page exact, no rep tiles: units are the pages in order
     for (int i = tid; i < p.P; i += kThreads * NB) units[i] = i;
@@ -296,40 +353,90 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   f32x16 L = {}, O[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
-  const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63, NB);
-  const UnitOffsets rep_off = unit_offsets(wave, lane, kHeadDim, 63, NB);
+  const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63, NB, true);
+  const UnitOffsets rep_off = unit_offsets(wave, lane, kHeadDim, 63, NB, true);
+  const UnitSources src = unit_sources(p, h);
   auto unit = [&](int i) { return __builtin_amdgcn_readfirstlane(units[i]); };
   // prologue: K0, V0, K1 in flight; S of unit 0 and its max
-  issue_rows<NB>(p, unit(0), 0, h, wave, lane, page_off, rep_off, kslot(0));
-  issue_rows<NB>(p, unit(0), 1, h, wave, lane, page_off, rep_off, vslot(0));
-  issue_rows<NB>(p, unit(min(1, nunits - 1)), 0, h, wave, lane, page_off, rep_off, kslot(1));
+  issue_rows<NB>(p, src, unit(0), 0, wave, lane, page_off, rep_off, kslot(0));
+  issue_rows<NB>(p, src, unit(0), 1, wave, lane, page_off, rep_off, vslot(0));
+  issue_rows<NB>(p, src, unit(min(1, nunits - 1)), 0, wave, lane, page_off, rep_off, kslot(1));
   wait_loads();
   __syncthreads();
   f32x16 S0 = s_tile(kslot(0), pair, lane, qop), S1;
   float mloc;
-  float bias = unit_max(S0, unit(0), maskw, p.P, pair, lane, p.scale_log2, mloc);
+  float bias = unit_max(S0, unit(0), pair, lane, p.scale_log2, mloc);
   update_max(mloc, m, L, O);
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
   // One unit with a successor: loads of K unit i+2 (clamped to the last
   // unit; a surplus load lands in a slot nobody reads again) and V unit i+1,
   // S of unit i+1, the probabilities of unit i, the max of unit i+1 (before
   // the P.V products, so it does not wait behind them in the matrix pipe),
-  // then P.V of unit i.  Unit ids run one step ahead in registers.
+  // then P.V of unit i.  Unit ids run ahead in registers; the id of unit
+  // i+3 is read from LDS in step i-1, so the read completes at its barrier.
   int u1 = unit(min(1, nunits - 1)), u2 = unit(min(2, nunits - 1));
+  int u3raw = units[min(3, nunits - 1)];
   auto step = [&](int i, f32x16& Sc, f32x16& Sn) {
     const int cur = i & 1, nxt = cur ^ 1;
-    const int u3 = unit(min(i + 3, nunits - 1));
-    issue_rows<NB>(p, u2, 0, h, wave, lane, page_off, rep_off, kslot(cur));
-    issue_rows<NB>(p, u1, 1, h, wave, lane, page_off, rep_off, vslot(nxt));
+    const int u3 = __builtin_amdgcn_readfirstlane(u3raw);
+    issue_rows<NB>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
+    issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
     const float nb = bias - (m == -INFINITY ? 0.0f : m);
-    Sn = s_tile(kslot(nxt), pair, lane, qop);
-    u32x4 pb[2], pl[2];
-    probabilities<PRECISE>(Sc, nb, p.scale_log2, pb, pl);
-    bias = unit_max(Sn, u1, maskw, p.P, pair, lane, p.scale_log2, mloc);
-    pv<PRECISE>(pb, pl, vslot(cur), pair, lane, L, O);
+    if (PRECISE) {
+      Sn = s_tile(kslot(nxt), pair, lane, qop);
+      u32x4 pb[2], pl[2];
+      probabilities<PRECISE>(Sc, nb, p.scale_log2, pb, pl);
+      bias = unit_max(Sn, u1, pair, lane, p.scale_log2, mloc);
+      pv<PRECISE>(pb, pl, vslot(cur), pair, lane, L, O);
+    } else {
+      // One instruction stream that keeps the matrix pipe fed: the 8
+      // products of S(i+1) each carry two exponentials of unit i and one
+      // operand read 4 products ahead; the P.V products of unit i then
+      // carry the max of unit i+1.  Scheduling barriers hold the order.
+      const lds_u8* kb = kslot(nxt);
+      const lds_u8* vb = vslot(cur);
+      const int r = lane & 31, hh = lane >> 5;
+      u32x4 ka[8], va[2][4], pb[2];
+      float P[16];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) ka[st] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + hh));
+      __builtin_amdgcn_sched_barrier(0);
+      Sn = f32x16{};
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        Sn = mfma32(ka[st], qop[st], Sn);
+        if (st < 4)
+          ka[st + 4] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + 8 + hh));
+        else
+          va[0][st - 4] = v_operand(vb, pair, 0, st - 4, lane);
+        P[2 * st] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st], p.scale_log2, nb));
+        P[2 * st + 1] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st + 1], p.scale_log2, nb));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int o = 8 * ks;
+        pb[ks] = u32x4{pack_bf16(P[o + 0], P[o + 1]), pack_bf16(P[o + 2], P[o + 3]), pack_bf16(P[o + 4], P[o + 5]),
+                       pack_bf16(P[o + 6], P[o + 7])};
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
+      L = mfma32(ones, pb[0], L);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        O[dt] = mfma32(va[0][dt], pb[0], O[dt]);
+        va[1][dt] = v_operand(vb, pair, 1, dt, lane);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      L = mfma32(ones, pb[1], L);
+      bias = unit_max(Sn, u1, pair, lane, p.scale_log2, mloc);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
+    }
     update_max(mloc, m, L, O);
     u1 = u2;
     u2 = u3;
+    u3raw = units[min(i + 4, nunits - 1)];
     wait_loads();
     __syncthreads();
   };
@@ -428,6 +535,9 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
                   hipStream_t stream) {
   if (n_tokens <= 0 || n_tokens % 64 || heads <= 0 || pages <= 0 || pages > 512 || count <= 0 ||
       count > kMaxCount || count > pages || head_pages < pages || rep_head_pages < pages)
+    return (int)hipErrorInvalidValue;
+  // a K/V row is 128 elements; page byte offsets of the window fit 32 bits
+  if (kv_token_stride < kHeadDim || kv_head_stride < 0 || 128.0 * (double)kv_token_stride * pages >= 4294967296.0)
     return (int)hipErrorInvalidValue;
   AttnParams p;
   p.q = (const uint16_t*)q;
