@@ -191,6 +191,19 @@ __device__ __forceinline__ f32x16 s_tile(const lds_u8* kbuf, int pair, int lane,
   return S;
 }
 
+// Maxima without the sNaN-quieting canonicalization the compiler adds
+// around fmaxf of values it cannot prove canonical.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max2f(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // Row max of S in log2 units (+ bias); rep tiles first drop the reps of
 // selected pages and of pages >= P.  Returns the bias of the unit.
 __device__ __forceinline__ float unit_max(f32x16& S, int e, int pair, int lane, float scale_log2, float& mloc) {
@@ -205,12 +218,12 @@ __device__ __forceinline__ float unit_max(f32x16& S, int e, int pair, int lane, 
       for (int i = 0; i < 4; ++i) S[4 * j + i] = d ? -INFINITY : S[4 * j + i];
     }
   }
-  float mx = S[0];
-#pragma unroll
-  for (int i = 1; i < 15; i += 2) mx = __builtin_fmaxf(__builtin_fmaxf(mx, S[i]), S[i + 1]);
-  mx = fmaxf(mx, S[15]);
+  // a depth-3 tree of v_max3 (S holds no NaN, so no operand quieting)
+  const float a = max3f(S[0], S[1], S[2]), b = max3f(S[3], S[4], S[5]), c = max3f(S[6], S[7], S[8]);
+  const float d = max3f(S[9], S[10], S[11]), e2 = max3f(S[12], S[13], S[14]);
+  float mx = max2f(max3f(a, b, c), max3f(d, e2, S[15]));
   const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-  mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));   // max over lanes l and l ^ 32
+  mx = max2f(__uint_as_float(sw[0]), __uint_as_float(sw[1]));   // max over lanes l and l ^ 32
   mloc = mx * scale_log2 + bias;     // -inf stays -inf
   return bias;
 }
@@ -379,8 +392,12 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   auto step = [&](int i, f32x16& Sc, f32x16& Sn) {
     const int cur = i & 1, nxt = cur ^ 1;
     const int u3 = __builtin_amdgcn_readfirstlane(u3raw);
-    issue_rows<NB>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
-    issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
+    // the general call issues its loads first; the two-block call (8 waves,
+    // half the loads each) spreads them over the first products
+    if (NB == 1 || PRECISE) {
+      issue_rows<NB>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
+      issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
+    }
     const float nb = bias - (m == -INFINITY ? 0.0f : m);
     if (PRECISE) {
       Sn = s_tile(kslot(nxt), pair, lane, qop);
@@ -405,6 +422,8 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
         Sn = mfma32(ka[st], qop[st], Sn);
+        if (NB == 2 && st == 0) issue_rows<NB>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
+        if (NB == 2 && st == 3) issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
         if (st < 4)
           ka[st + 4] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + 8 + hh));
         else
