@@ -341,6 +341,14 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const int TB = p.T / NB;
   const int work = xcd_remap(blockIdx.x, p.H * TB);
   const int h = work / TB, t = (work % TB) * NB + grp;
+  // query operand: lane's query row, dims 16*st + 8*hh + [0,8); requested
+  // first so its latency overlaps the unit list
+  const int r = lane & 31, hh = lane >> 5;
+  const long long qrow = (long long)(t * 64 + qw * 32 + r);
+  u32x4 qop[8];
+  const uint16_t* qp = p.q + qrow * p.q_tok + (long long)h * p.q_head + 8 * hh;
+#pragma unroll
+  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st);
   if (NB == 1) {
     own_units(p, h, t, tid, kThreads, units, maskw, &nunits_s);
   } else {
@@ -348,13 +356,6 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     for (int i = tid; i < p.P; i += kThreads * NB) units[i] = i;
     if (tid == 0) nunits_s = p.P;
   }
-  // query operand: lane's query row, dims 16*st + 8*hh + [0,8)
-  const int r = lane & 31, hh = lane >> 5;
-  const long long qrow = (long long)(t * 64 + qw * 32 + r);
-  u32x4 qop[8];
-  const uint16_t* qp = p.q + qrow * p.q_tok + (long long)h * p.q_head + 8 * hh;
-#pragma unroll
-  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st);
   __syncthreads();
   const int nunits = nunits_s;
   lds_u8* const kbase = (lds_u8*)ring;
