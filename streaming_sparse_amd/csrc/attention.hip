@@ -95,31 +95,6 @@ __device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long lon
   return o;
 }
 
-// N consecutive 1 KB global->LDS loads of one wave: load jj reads base +
-// off[jj] + jj * 1024 (per lane) into lds + jj * 1024 + 16 * lane, with one
-// M0 write for all of them.
-template <int N>
-__device__ __forceinline__ void dma_rows(const void* base, const uint32_t (&off)[4], uint32_t lds) {
-  if constexpr (N == 4) {
-    asm volatile(
-        "s_mov_b32 m0, %4\n\ts_nop 0\n\t"
-        "global_load_lds_dwordx4 %0, %5\n\t"
-        "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
-        "global_load_lds_dwordx4 %2, %5 offset:2048\n\t"
-        "global_load_lds_dwordx4 %3, %5 offset:3072" ::"v"(off[0]),
-        "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(lds), "s"(base)
-        : "memory", "m0");
-  } else {
-    static_assert(N == 2, "2 or 4 loads");
-    asm volatile(
-        "s_mov_b32 m0, %2\n\ts_nop 0\n\t"
-        "global_load_lds_dwordx4 %0, %3\n\t"
-        "global_load_lds_dwordx4 %1, %3 offset:1024" ::"v"(off[0]),
-        "v"(off[1]), "s"(lds), "s"(base)
-        : "memory", "m0");
-  }
-}
-
 // Where a workgroup's units come from: head h's K, V, rep key and rep value
 // rows as byte pointers, and the byte stride of a page.
 struct UnitSources {
@@ -191,18 +166,11 @@ __device__ __forceinline__ f32x16 s_tile(const lds_u8* kbuf, int pair, int lane,
   return S;
 }
 
-// Maxima without the sNaN-quieting canonicalization the compiler adds
-// around fmaxf of values it cannot prove canonical.
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-__device__ __forceinline__ float max2f(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
+// Maxima as trees of v_max3 / v_max.  The sources build with NaN-free
+// float semantics, so the compiler adds no quieting of matrix-pipe results
+// (and keeps its own hazard waits before reading them).
+__device__ __forceinline__ float max3f(float a, float b, float c) { return __builtin_fmaxf(__builtin_fmaxf(a, b), c); }
+__device__ __forceinline__ float max2f(float a, float b) { return __builtin_fmaxf(a, b); }
 
 // Row max of S in log2 units (+ bias); rep tiles first drop the reps of
 // selected pages and of pages >= P.  Returns the bias of the unit.

@@ -69,4 +69,29 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
                : "memory", "m0");
 }
 
+// N consecutive 1 KB global->LDS loads of one wave: load jj reads base +
+// off[jj] + jj * 1024 (per lane) into lds + jj * 1024 + 16 * lane, with one
+// M0 write for all of them.
+template <int N>
+__device__ __forceinline__ void dma_rows(const void* base, const uint32_t (&off)[4], uint32_t lds) {
+  if constexpr (N == 4) {
+    asm volatile(
+        "s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %5\n\t"
+        "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
+        "global_load_lds_dwordx4 %2, %5 offset:2048\n\t"
+        "global_load_lds_dwordx4 %3, %5 offset:3072" ::"v"(off[0]),
+        "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(lds), "s"(base)
+        : "memory", "m0");
+  } else {
+    static_assert(N == 2, "2 or 4 loads");
+    asm volatile(
+        "s_mov_b32 m0, %2\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %3 offset:1024" ::"v"(off[0]),
+        "v"(off[1]), "s"(lds), "s"(base)
+        : "memory", "m0");
+  }
+}
+
 }  // namespace ssa

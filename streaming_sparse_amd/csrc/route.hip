@@ -79,6 +79,12 @@ __device__ __forceinline__ float row_sum16(float v) {
   return v;
 }
 
+// Maxima as trees of v_max3 / v_max.  The sources build with NaN-free
+// float semantics, so the compiler adds no quieting of matrix-pipe results
+// (and keeps its own hazard waits before reading them).
+__device__ __forceinline__ float max3f(float a, float b, float c) { return __builtin_fmaxf(__builtin_fmaxf(a, b), c); }
+__device__ __forceinline__ float max2f(float a, float b) { return __builtin_fmaxf(a, b); }
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -209,9 +215,11 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   auto mine = [&](int jj) { return wave + 4 * max(min(jj, nmine - 1), 0); };
   lds_u8* const ring = (lds_u8*)&s.ring[wave][0][0];
   const uint32_t ring_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring);
-  uint32_t koff[8];
+  // row offsets of a full tile in the instruction-offset form of dma_rows:
+  // loads 0-3 and 4-7 each share one M0 value (rows >= 4 jj keep them >= 0)
+  uint32_t koff[2][4];
 #pragma unroll
-  for (int jj = 0; jj < 8; ++jj) koff[jj] = tile_row_off(jj, lane, 31);
+  for (int jj = 0; jj < 8; ++jj) koff[jj >> 2][jj & 3] = tile_row_off(jj, lane, 31) - 1024u * (jj & 3);
   // the stats of the tile's 8 pages: 768 contiguous bytes; lanes 48..63 land
   // past them in the slot's 1 KB stats region (a clamped re-read)
   auto issue_tile = [&](int tile_in, int slot, bool stats) {
@@ -220,8 +228,8 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     const uint16_t* kb = rkh + (long long)tile * 32 * kHeadDim;
     const int last_row = P * 4 - 1 - tile * 32;
     if (last_row >= 31) {
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) dma16(kb, koff[jj], l + jj * 1024);
+      dma_rows<4>(kb, koff[0], l);
+      dma_rows<4>(kb, koff[1], l + 4096);
     } else {
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) dma16(kb, tile_row_off(jj, lane, last_row), l + jj * 1024);
@@ -273,26 +281,28 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
 
   // pass 1: max and sum of exp over all reps, per probe, and the per-head
-  // bound of the page value norm max_p stats[p,1,11] from the tiles' stats
+  // bound of the page value norm max_p stats[p,1,11] from the tiles' stats.
+  // Software-pipelined: the logits of tile j+1 are on the matrix pipe while
+  // the exponentials of tile j run.
   float mx = -INFINITY, den = 0.f, bmax = -INFINITY;
-  for (int j = 0; j < nmine; ++j) {
+  auto stats_bound = [&](int j) {
     const int tile = mine(j);
-    wait_tile(9);                                    // tile j landed (tile j+1 may be in flight)
-    u32x4 av[8];
-    read_reps(ring + (j & 1) * kSlotBytes, lane, av);
     if (lane < 8 && tile * 8 + lane < P)
       bmax = fmaxf(bmax, bf16_to_f32(((lds_u16*)(ring + (j & 1) * kSlotBytes + 8192))[lane * 48 + 23]));
-    wait_lds();
-    issue_tile(mine(j + 2), j & 1, true);
-    f32x16 S;
-    rep_logits(av, qop, S);
-    float tmax = -INFINITY;
+  };
+  auto soft1 = [&](f32x16 S, int tile) {
+    if (tile * 8 + 8 <= P) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int page = tile * 8 + 2 * (i >> 2) + hh;
-      S[i] = page < P ? S[i] * c2 : -INFINITY;
-      tmax = fmaxf(tmax, S[i]);
+      for (int i = 0; i < 16; ++i) S[i] *= c2;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int page = tile * 8 + 2 * (i >> 2) + hh;
+        S[i] = page < P ? S[i] * c2 : -INFINITY;
+      }
     }
+    const float tmax = max2f(max3f(max3f(S[0], S[1], S[2]), max3f(S[3], S[4], S[5]), max3f(S[6], S[7], S[8])),
+                             max3f(max3f(S[9], S[10], S[11]), max3f(S[12], S[13], S[14]), S[15]));
     const float mnew = fmaxf(mx, tmax);
     const float muse = mnew == -INFINITY ? 0.f : mnew;
     float acc = 0.f;
@@ -300,6 +310,27 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     for (int i = 0; i < 16; ++i) acc += __builtin_amdgcn_exp2f(S[i] - muse);
     den = den * __builtin_amdgcn_exp2f(mx - muse) + acc;
     mx = mnew;
+  };
+  // tile j's slot is read into registers, then refilled with tile j+2
+  auto next_logits = [&](int j, f32x16& S) {
+    wait_tile(9);                                    // tile j landed (tile j+1 may be in flight)
+    u32x4 av[8];
+    read_reps(ring + (j & 1) * kSlotBytes, lane, av);
+    stats_bound(j);
+    wait_lds();
+    issue_tile(mine(j + 2), j & 1, true);
+    rep_logits(av, qop, S);
+  };
+  if (nmine > 0) {
+    f32x16 S;
+    next_logits(0, S);
+    for (int j = 0; j + 1 < nmine; ++j) {
+      f32x16 Sn;
+      next_logits(j + 1, Sn);
+      soft1(S, mine(j));
+      S = Sn;
+    }
+    soft1(S, mine(nmine - 1));
   }
   wait_loads();                                      // surplus loads of the clamped tail
   issue_tile(mine(0), 0, true);                      // pass 2's first two tiles
@@ -324,11 +355,17 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   float DEN = 0.f;
 #pragma unroll
   for (int w = 0; w < 4; ++w) DEN += s.part[w][pi][1] * __builtin_amdgcn_exp2f(s.part[w][pi][0] - MX);
-  const float inv_den = 1.0f / DEN;
+  // probabilities 2^(z2 - MX) / DEN as one power of two, 2^(z2 - (MX + log2 DEN))
+  const float nlse = -(MX + __log2f(DEN));
   if (p.lse && wave == 0 && hh == 0 && t0 + blk < p.T)
     p.lse[((long long)h * p.T + t0 + blk) * 16 + m] = (MX + __log2f(DEN)) * 0.69314718055994531f;
   bmax = fmaxf(fmaxf(s.bmax_w[0], s.bmax_w[1]), fmaxf(s.bmax_w[2], s.bmax_w[3]));
-  const float th0 = p.theta[h * 4 + 0], th1 = p.theta[h * 4 + 1], th2 = p.theta[h * 4 + 2], th3 = p.theta[h * 4 + 3];
+  // theta is wave-uniform; taking it into scalar registers here also keeps
+  // the wait for its load out of the tile loop (a wait there would cover
+  // the in-flight tile loads too)
+  auto uniform = [](float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v))); };
+  const float th0 = uniform(p.theta[h * 4 + 0]), th1 = uniform(p.theta[h * 4 + 1]);
+  const float th2 = uniform(p.theta[h * 4 + 2]), th3 = uniform(p.theta[h * 4 + 3]);
 
   // pass 2: probabilities -> four features -> theta-weighted value -> probe mean.
   // The per-rep stats reach the lane layout of S through the matrix pipe:
@@ -347,30 +384,40 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     bqn = u32x4{hh == 0 ? pack_bf16(qh, qn - qh) : 0u, 0u, 0u, 0u};
     bone = u32x4{hh == 0 ? 0x3F80u : 0u, 0u, 0u, 0u};
   }
-  for (int j = 0; j < nmine; ++j) {
-    const int tile = mine(j);
-    wait_tile(9);
-    const lds_u8* slot = ring + (j & 1) * kSlotBytes;
-    u32x4 av[8];
-    read_reps(slot, lane, av);
-    // stats of rep row lane%32: words (st0,st1)..(st6,st7), (st8,st9), (st10,st11)
-    const lds_u8* sr = slot + 8192 + pi * 24;
-    const u32x2 w01 = *(lds_u32x2*)sr, w23 = *(lds_u32x2*)(sr + 8), w45 = *(lds_u32x2*)(sr + 16);
-    // stats[p,0,11] and stats[p,1,11] of this lane's 4 pages (2 jj + hh of the tile)
+  // per-tile stats in registers: rep row lane%32's words (st0,st1)..(st6,st7),
+  // (st8,st9), (st10,st11), and stats[p,0,11], stats[p,1,11] of this lane's
+  // 4 pages (2 jj + hh of the tile)
+  struct TileStats {
+    u32x2 w01, w23, w45;
     float s011[4], s111[4];
+  };
+  auto read_stats = [&](int j, TileStats& ts) {
+    const lds_u8* slot = ring + (j & 1) * kSlotBytes;
+    const lds_u8* sr = slot + 8192 + pi * 24;
+    ts.w01 = *(lds_u32x2*)sr;
+    ts.w23 = *(lds_u32x2*)(sr + 8);
+    ts.w45 = *(lds_u32x2*)(sr + 16);
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const lds_u16* sp = (lds_u16*)(slot + 8192) + (2 * jj + hh) * 48;
-      s011[jj] = bf16_to_f32(sp[11]);
-      s111[jj] = bf16_to_f32(sp[23]);
+      ts.s011[jj] = bf16_to_f32(sp[11]);
+      ts.s111[jj] = bf16_to_f32(sp[23]);
     }
+  };
+  auto next_tile = [&](int j, f32x16& S, TileStats& ts) {
+    wait_tile(9);
+    u32x4 av[8];
+    read_reps(ring + (j & 1) * kSlotBytes, lane, av);
+    read_stats(j, ts);
     wait_lds();
     issue_tile(mine(j + 2), j & 1, true);
-    f32x16 S;
     rep_logits(av, qop, S);
-    const u32x4 ag = {w01[0], w01[1], w23[0], w23[1]};
-    const uint32_t st8 = w45[0] & 0xffffu, st9 = w45[0] >> 16, st10 = w45[1] & 0xffffu;
-    const uint32_t lo_only = hh == 0 ? 0xffffffffu : 0u;
+  };
+  const uint32_t lo_only = hh == 0 ? 0xffffffffu : 0u;
+  // features of one tile from its logits and stats, down to the block mean
+  auto soft2 = [&](const f32x16& S, const TileStats& ts, int tile) {
+    const u32x4 ag = {ts.w01[0], ts.w01[1], ts.w23[0], ts.w23[1]};
+    const uint32_t st8 = ts.w45[0] & 0xffffu, st9 = ts.w45[0] >> 16, st10 = ts.w45[1] & 0xffffu;
     const f32x16 U = mfma32(ag, bq, f32x16{});
     const f32x16 Bt = mfma32(u32x4{(st8 | (st8 << 16)) & lo_only, 0u, 0u, 0u}, bqn, f32x16{});
     const f32x16 F9 = mfma32(u32x4{st9 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
@@ -380,13 +427,13 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       const int page = tile * 8 + 2 * jj + hh;
       float prob[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) prob[i] = __builtin_amdgcn_exp2f(fmaf(S[4 * jj + i], c2, -MX)) * inv_den;
+      for (int i = 0; i < 4; ++i) prob[i] = __builtin_amdgcn_exp2f(fmaf(S[4 * jj + i], c2, nlse));
       const float alpha = ((prob[0] + prob[1]) + prob[2]) + prob[3];
-      const float c = s111[jj] + bmax;                    // stats[p,1,11] + max_p stats[p,1,11]
-      float x0 = alpha * s011[jj], x1 = 0.f, x2 = 0.f, x3 = 0.f;
+      const float c = ts.s111[jj] + bmax;                 // stats[p,1,11] + max_p stats[p,1,11]
+      float x0 = alpha * ts.s011[jj], x1 = 0.f, x2 = 0.f, x3 = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float u = fmaxf(U[4 * jj + i], 0.f);
+        const float u = max2f(U[4 * jj + i], 0.f);
         const float beta = Bt[4 * jj + i];
         x0 += fabsf(prob[i] - alpha * 0.25f) * F9[4 * jj + i];
         x1 += prob[i] * __builtin_amdgcn_sqrtf(u) * F10[4 * jj + i];
@@ -400,6 +447,21 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       val = row_sum16(val);
       if (m == 15 && page < P) s.risk[blk][page] = val * 0.0625f;
     }
+  };
+  // software-pipelined like pass 1: logits of tile j+1 beside the features of tile j
+  if (nmine > 0) {
+    f32x16 S;
+    TileStats ts;
+    next_tile(0, S, ts);
+    for (int j = 0; j + 1 < nmine; ++j) {
+      f32x16 Sn;
+      TileStats tn;
+      next_tile(j + 1, Sn, tn);
+      soft2(S, ts, mine(j));
+      S = Sn;
+      ts = tn;
+    }
+    soft2(S, ts, mine(nmine - 1));
   }
   wait_loads();                                      // the ring is reused for selection below
   __syncthreads();
