@@ -109,10 +109,15 @@ def main():
     stream = torch.cuda.current_stream(dev)
     basis = g.basis.to(torch.bfloat16).contiguous()   # the caller keeps the basis bf16-rounded
 
+    vrep_call = ws.tensor('call_rep_values', (H, P, 4, D), dev, torch.bfloat16)
+
     def step():
-        # own page of block t is P-72+t (the kernel's default when own is None)
-        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
-        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, precise_av=args.precise_av)
+        # own page of block t is P-72+t (the kernel's default when own is None); the router also writes the
+        # call's rep value rows, which the attention kernel reads
+        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_basis=basis,
+                             rep_out=vrep_call)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, precise_av=args.precise_av,
+                         rep_values=vrep_call)
 
     for _ in range(args.warmup):
         step()
@@ -143,9 +148,8 @@ def main():
 
     iters = max(10, args.steps)
     attn_ms = time_loop(attn_only, iters, stream)
-    route_ms = time_loop(lambda: route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False),
-                         iters, stream)
-    rep_ms = time_loop(lambda: rep_values(g.summary, basis, P, vrep), iters, stream)
+    route_ms = time_loop(lambda: route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False,
+                                       rep_basis=basis, rep_out=vrep_call), iters, stream)
 
     dense_ms = None
     if not args.no_dense:
@@ -193,8 +197,7 @@ def main():
                                f"per 64-query block, 12 heads x 4608 queries x d128, route + attention",
                    "pages": P, "exact_pages": C, "heads": H, "queries": N, "head_dim": D,
                    "precise_av": bool(args.precise_av)},
-        "breakdown_ms": {"route": round(route_ms, 4), "rep_values": round(rep_ms, 4),
-                         "attention_kernel": round(attn_ms, 4)},
+        "breakdown_ms": {"route_and_rep_values": round(route_ms, 4), "attention_kernel": round(attn_ms, 4)},
         "dense_sdpa_ms": None if dense_ms is None else round(dense_ms, 4),
         "ratio_vs_dense": None if dense_ms is None else round(ms_call / dense_ms, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved_tflops, 2), "peak": PEAK_BF16_TFLOPS,
@@ -240,17 +243,19 @@ def intersection_lines(args, dense_ms, iters):
         device=dev, dtype=torch.int32)
     recompute = lambda: summary.build(g.k, g.v, basis, init, g.summary, P - 72, 72)
 
+    vrep = ws.tensor('call_rep_values', (12, P, 4, 128), dev, torch.bfloat16)
+
     def plain():
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
-                             want_mask=False)
-        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws)
+                             want_mask=False, rep_basis=basis, rep_out=vrep)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep)
 
     def corrected():
         recompute()
         pset.encode(g.summary, basis, reader, out=enc, first=P - 72, pages=72)
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
-                             full_pset=PSET_HEADS, encoding=enc, reader=reader)
-        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws)
+                             full_pset=PSET_HEADS, encoding=enc, reader=reader, rep_basis=basis, rep_out=vrep)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep)
 
     out = {}
     for name, fn in (("intersection", plain), ("intersection_full_pset", corrected)):

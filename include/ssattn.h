@@ -73,11 +73,16 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
  * mode 2: fixed top-count with own forced first.  Ties -> lower page.
  * ids [H,blocks,count] int32 and mask [H,blocks,pages] uint8 may be NULL; lse
  * [H,blocks,16] fp32 (NULL to skip) receives each probe's log-sum-exp over
- * all reps of the window (natural log), the input ssa_pset needs. */
+ * all reps of the window (natural log), the input ssa_pset needs.
+ * rep_values [H,rep_head_pages,4,128] bf16 (NULL to skip) receives, on the
+ * side, exactly what ssa_rep_values writes for pages [0,pages) from mean,
+ * detail and basis (as in ssa_rep_values), so a call that routes needs no
+ * separate rep-value launch. */
 int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
-              int pages, int head_pages, int count, int mode, int total, hipStream_t stream);
+              int pages, int head_pages, int count, int mode, int total, const void* mean, const void* detail,
+              const void* basis, void* rep_values, int rep_head_pages, hipStream_t stream);
 
 /* Page summaries of pages [first_page, first_page + pages) of the resident
  * cache (k, v addressed as in ssa_attention): a 4-way k-means of each page's

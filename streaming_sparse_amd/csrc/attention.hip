@@ -488,20 +488,14 @@ __global__ __launch_bounds__(128) void rep_values_kernel(const uint16_t* mean, c
   if (d < 24) det[d] = bf16_to_f32(detail[((long long)h * HP + pg) * 24 + d]);
   __syncthreads();
   const float mu = bf16_to_f32(mean[((long long)h * HP + pg) * kHeadDim + d]);
-  float b[8];
+  float b[8], dv[24], o[4];
 #pragma unroll
   for (int k = 0; k < 8; ++k) b[k] = bf16_to_f32(basis[((long long)h * kHeadDim + d) * 8 + k]);
-  const float haar[3][4] = {{1, 1, -1, -1}, {1, -1, 1, -1}, {1, -1, -1, 1}};
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    float acc = mu;
+  for (int k = 0; k < 24; ++k) dv[k] = det[k];
+  rep_value_rows(mu, dv, b, o);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float code = haar[0][rr] * det[k] + haar[1][rr] * det[8 + k] + haar[2][rr] * det[16 + k];
-      acc += code * b[k];
-    }
-    vrep[(((long long)h * HPV + pg) * 4 + rr) * kHeadDim + d] = to_bf16(acc);
-  }
+  for (int rr = 0; rr < 4; ++rr) vrep[(((long long)h * HPV + pg) * 4 + rr) * kHeadDim + d] = to_bf16(o[rr]);
 }
 
 }  // namespace

@@ -94,4 +94,22 @@ __device__ __forceinline__ void dma_rows(const void* base, const uint32_t (&off)
   }
 }
 
+// The 4 rep value rows of one page at dimension d: row r = mean[d] +
+// sum_k (sum_a HAAR[a,r] detail[a,k]) basis[d,k] in fp32 (rounded to bf16 by
+// the caller); the compensation's value rows.  Shared by every kernel that
+// writes them, so they agree bit for bit.
+__device__ __forceinline__ void rep_value_rows(float mu, const float (&det)[24], const float (&b)[8], float (&out)[4]) {
+  const float haar[3][4] = {{1, 1, -1, -1}, {1, -1, 1, -1}, {1, -1, -1, 1}};
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    float acc = mu;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float code = haar[0][rr] * det[k] + haar[1][rr] * det[8 + k] + haar[2][rr] * det[16 + k];
+      acc += code * b[k];
+    }
+    out[rr] = acc;
+  }
+}
+
 }  // namespace ssa

@@ -51,6 +51,12 @@ struct RouteParams {
   uint8_t* mask;               // [H, T, P] or null
   float* lse;                  // [H, T, 16] LSE of each probe over all reps (natural log), or null
   int H, T, P, HP, C, mode, total;
+  // rep value rows of the window's pages, written on the side (rvals null:
+  // not asked for): mean [H,HP,128], detail [H,HP,3,8], basis [H,128,8] bf16
+  // -> rvals [H,HPV,4,128] bf16
+  const uint16_t *rmean, *rdetail, *rbasis;
+  uint16_t* rvals;
+  int HPV;
 };
 
 constexpr int kSlotBytes = 9 * 1024;   // a rep tile: 32 rows x 256 B (swizzled) + its pages' stats (768 B)
@@ -279,6 +285,33 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
 #pragma unroll
   for (int g = 0; g < 8; ++g) qsum += q2[g];
   const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
+
+  // rep value rows of this workgroup's share of the head's pages (the
+  // workgroups of a head split its pages evenly); the tile loads issued
+  // above are in flight meanwhile
+  if (p.rvals) {
+    const int share = (P + NP - 1) / NP, pbeg = (work % NP) * share, npg = min(P - pbeg, share);
+    const int d = tid & 127;
+    float b[8];
+    {
+      const u32x4 bw = ldg16(p.rbasis + ((long long)h * kHeadDim + d) * 8);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        b[2 * w] = bf16_lo(bw[w]);
+        b[2 * w + 1] = bf16_hi(bw[w]);
+      }
+    }
+    for (int pl = tid >> 7; pl < npg; pl += 2) {
+      const long long pg = (long long)h * p.HP + pbeg + pl;
+      float dv[24], o[4];
+#pragma unroll
+      for (int k = 0; k < 24; ++k) dv[k] = bf16_to_f32(p.rdetail[pg * 24 + k]);
+      rep_value_rows(bf16_to_f32(p.rmean[pg * kHeadDim + d]), dv, b, o);
+      uint16_t* dst = p.rvals + (((long long)h * p.HPV + pbeg + pl) * 4) * kHeadDim + d;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) dst[rr * kHeadDim] = to_bf16(o[rr]);
+    }
+  }
 
   // pass 1: max and sum of exp over all reps, per probe, and the per-head
   // bound of the page value norm max_p stats[p,1,11] from the tiles' stats.
@@ -576,10 +609,12 @@ extern "C" {
 int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
-              int pages, int head_pages, int count, int mode, int total, hipStream_t stream) {
+              int pages, int head_pages, int count, int mode, int total, const void* mean, const void* detail,
+              const void* basis, void* rep_values, int rep_head_pages, hipStream_t stream) {
   if (heads <= 0 || blocks <= 0 || pages <= 0 || pages > kMaxPages || head_pages < pages || mode < -1 ||
       mode > 2)
     return (int)hipErrorInvalidValue;
+  if (rep_values && (!mean || !detail || !basis || rep_head_pages < pages)) return (int)hipErrorInvalidValue;
   if (mode == 0 && (count < 1 + kAnchors || pages < kAnchors + kCurrent)) return (int)hipErrorInvalidValue;
   if (mode == 1 && (count != kAnchors + total || pages <= kAnchors + kCurrent || current == nullptr))
     return (int)hipErrorInvalidValue;
@@ -606,6 +641,11 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
   p.C = count;
   p.mode = mode;
   p.total = total;
+  p.rmean = (const uint16_t*)mean;
+  p.rdetail = (const uint16_t*)detail;
+  p.rbasis = (const uint16_t*)basis;
+  p.rvals = (uint16_t*)rep_values;
+  p.HPV = rep_head_pages;
   const int np = (blocks + 1) / 2;
   hipLaunchKernelGGL(route_kernel, dim3(heads * np), dim3(kThreads), 0, stream, p);
   return (int)hipGetLastError();

@@ -55,8 +55,11 @@ def rep_values(s: Summary, basis: torch.Tensor, pages: int, out: torch.Tensor):
     return out
 
 
+rep_values_fn = rep_values   # attention() takes a `rep_values` keyword
+
+
 @torch.no_grad()
-def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=False):
+def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=False, rep_values=None):
     """Exact attention over the LUT pages + summary compensation + merge.
 
     q [1,N,H,128] bf16 contiguous; k, v [1,64P,H,128] bf16 (resident cache);
@@ -64,7 +67,10 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=Fal
     own page first.  Returns ``out`` [1,N,H,128] bf16, owned by `workspace`
     and overwritten by the next call.  ``bf16_av`` is accepted for signature
     compatibility; ``precise_av`` selects two-term (hi+lo) bf16 P.V in every
-    unit, the reference's exact-stage arithmetic."""
+    unit, the reference's exact-stage arithmetic.  ``rep_values``: the
+    [H,P,4,128] rep value rows of `s` and `basis` when the caller already has
+    them (route(..., rep_out=...) writes them on the side); otherwise they
+    are computed here."""
     _, n, h, d = q.shape
     p = k.shape[1] // 64
     count = ids.shape[-1]
@@ -81,12 +87,22 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=Fal
     def buf(name, shape, dtype):
         return workspace.tensor('ssa_' + name, shape, q.device, dtype)
 
-    vrep = rep_values(s, basis, p, buf('rep_values', (h, p, 4, d), torch.bfloat16))
+    if count >= p:
+        # every page exact: the kernel reads no rep rows (the rep keys stand
+        # in for the unused pointer)
+        vrep = s.keys
+    elif rep_values is not None:
+        if rep_values.dtype != torch.bfloat16 or not rep_values.is_contiguous() or rep_values.shape[0] != h or \
+                rep_values.shape[1] < p or tuple(rep_values.shape[2:]) != (4, d):
+            raise ValueError("rep_values must be a contiguous bf16 [H,>=P,4,128] tensor")
+        vrep = rep_values
+    else:
+        vrep = rep_values_fn(s, basis, p, buf('rep_values', (h, p, 4, d), torch.bfloat16))
     out = buf('out', q.shape, q.dtype)
     flags = 1 if precise_av else 0
     _lib.check(_lib.lib().ssa_attention(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(s.keys), _lib.ptr(vrep),
-                                        _lib.ptr(ids), _lib.ptr(out), n, h, p, hp, p, count, tok, head, flags,
-                                        _lib.stream_handle(q.device)), "ssa_attention")
+                                        _lib.ptr(ids), _lib.ptr(out), n, h, p, hp, vrep.shape[1], count, tok, head,
+                                        flags, _lib.stream_handle(q.device)), "ssa_attention")
     return out
 
 
@@ -107,5 +123,6 @@ def risk(probes, z, summary, theta):
     out = torch.empty(h, t, p, device=probes.device, dtype=torch.float32)
     _lib.check(_lib.lib().ssa_route(_lib.ptr(pr), t * m * d, m * d, d, 1, _lib.ptr(summary.keys),
                                     _lib.ptr(summary.stats), _lib.ptr(th), None, None, _lib.ptr(out), None, None,
-                                    None, h, t, p, hp, 0, -1, 0, _lib.stream_handle(probes.device)), "ssa_route")
+                                    None, h, t, p, hp, 0, -1, 0, None, None, None, None, 0,
+                                    _lib.stream_handle(probes.device)), "ssa_route")
     return out

@@ -144,11 +144,12 @@ class ChunkRuntime:
             pset.encode(L.summary, L.basis, self.reader, out=L.encoding, first=P - CURRENT, pages=CURRENT)
         a = self.quota_a[step, layer - 1]
         n = int(self.quota_n[step][layer - 1])
+        vrep = self.ws.tensor('rt_rep_values', (L.summary.mean.shape[0], P, 4, 128), q.device, torch.bfloat16)
         ids, _, _, stats = route(q, L.summary, self.theta, tier='intersection', current_slots=a, n=n,
                                  workspace=self.ws, want_mask=correct, lse_out=self.lse if correct else None,
                                  full_pset=cfg.pset_heads if correct else None, encoding=L.encoding,
-                                 reader=self.reader)
-        return attention(q, L.k, L.v, L.summary, L.basis, ids, self.ws)
+                                 reader=self.reader, rep_basis=L.basis, rep_out=vrep)
+        return attention(q, L.k, L.v, L.summary, L.basis, ids, self.ws, rep_values=vrep)
 
     def commit(self, layer: int, q):
         """Clean step: dense attention, then the new pages' summaries (and

@@ -123,6 +123,27 @@ def test_route_intersection_matches_oracle(device):
     assert (mask.cpu()[..., :24]).all() and (got_mask[..., P - 72:].sum(-1) == a[:, None]).all()
 
 
+@pytest.mark.parametrize("cfg,frames", [(0, 9), (1, 18)])
+def test_route_writes_rep_values(device, cfg, frames):
+    """The router's side output of rep value rows equals the standalone
+    rep-value kernel bit for bit (into a slab wider than the window), and the
+    attention call that reads them equals the one that computes its own."""
+    from streaming_sparse_amd.legacy_components import rep_values
+    x = call_inputs(cfg, frames)
+    g = x.to(device)
+    P = x.pages
+    basis = g.basis.to(torch.bfloat16).contiguous()
+    want = rep_values(g.summary, basis, P, torch.empty(12, P, 4, 128, device=device, dtype=torch.bfloat16))
+    slab = torch.full((12, P + 5, 4, 128), float("nan"), device=device, dtype=torch.bfloat16)
+    ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, rep_basis=basis, rep_out=slab)
+    assert torch.equal(slab[:, :P].view(torch.int16), want.view(torch.int16))
+    assert bool(slab[:, P:].isnan().all())           # rows past the window untouched
+    ws = Workspace()
+    a = attention(g.q, g.k, g.v, g.summary, basis, ids, ws).clone()
+    b = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=slab)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 @pytest.mark.parametrize("precise", [False, True])
 def test_attention_config0(device, precise):
     """216-page window, base tier LUT (32 pages), all 72 query blocks x 12 heads."""
