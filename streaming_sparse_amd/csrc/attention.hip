@@ -409,6 +409,11 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       }
       __builtin_amdgcn_sched_barrier(0);
       const u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
+      // the P.V products, the next max and the running-max update run at
+      // raised wave priority: this wave then wins the SIMD's issue slots over
+      // the other workgroup's wave in its exponentials or load issue, and the
+      // step reaches its barrier sooner (general call only; measured ~6%)
+      if (NB == 1) __builtin_amdgcn_s_setprio(1);
       L = mfma32(ones, pb[0], L);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
@@ -422,6 +427,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       for (int dt = 0; dt < 4; ++dt) O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
     }
     update_max(mloc, m, L, O);
+    if (NB == 1 && !PRECISE) __builtin_amdgcn_s_setprio(0);
     u1 = u2;
     u2 = u3;
     u3raw = units[min(i + 4, nunits - 1)];
