@@ -77,7 +77,8 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
  * rep_values [H,rep_head_pages,4,128] bf16 (NULL to skip) receives, on the
  * side, exactly what ssa_rep_values writes for pages [0,pages) from mean,
  * detail and basis (as in ssa_rep_values), so a call that routes needs no
- * separate rep-value launch. */
+ * separate rep-value launch; mean, detail, basis and rep_values must then be
+ * 16-byte aligned. */
 int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,

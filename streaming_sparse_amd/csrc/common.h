@@ -41,6 +41,10 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
                                                  c, 0, 0, 0);
 }
 
+// Row of probe m (0..15) in its 64-query block: round(63 m / 15), the 16
+// evenly spaced rows of VR/runtime.py:84 (linspace(0, 63, 16).round()).
+__device__ __forceinline__ int probe_row(int m) { return (42 * m + 5) / 10; }
+
 // Monotone map of a float to an unsigned key (larger float -> larger key);
 // -0.0 and +0.0 share a key so equal floats compare equal.
 __device__ __forceinline__ uint32_t orderable(float f) {

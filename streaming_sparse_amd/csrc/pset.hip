@@ -202,8 +202,6 @@ struct PsetParams {
   int H, T, P, C;
 };
 
-__constant__ int kProbeOffsets[16] = {0, 4, 8, 13, 17, 21, 25, 29, 34, 38, 42, 46, 50, 55, 59, 63};
-
 __device__ __forceinline__ int own_page(const PsetParams& p, int h, int t) {
   return p.own ? p.own[(long long)h * p.T + t] : p.P - p.T + t;
 }
@@ -381,7 +379,7 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
   {
     const int pr = tid >> 3, i = tid & 7;
     const int tb = min(t0 + (pr >> 4), p.T - 1);
-    const long long rr = p.gathered ? (pr & 15) : kProbeOffsets[pr & 15];
+    const long long rr = p.gathered ? (pr & 15) : probe_row(pr & 15);
     const uint16_t* qq = p.q + (long long)h * p.q_head + (long long)tb * p.q_block + rr * p.q_row;
     const f32x4* wr = reinterpret_cast<const f32x4*>(p.wq + i * 128);
     u32x4 qv[16];
@@ -405,7 +403,7 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
   const int pi = lane & 31, hh = lane >> 5;
   const int blk = pi >> 4, m = pi & 15;
   const int tq = min(t0 + blk, p.T - 1);
-  const long long row = p.gathered ? m : kProbeOffsets[m];
+  const long long row = p.gathered ? m : probe_row(m);
   const uint16_t* qbase = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
   u32x4 qop[8];
 #pragma unroll

@@ -13,12 +13,15 @@
 // Workgroup: 256 threads (4 waves) = 32 probes (2 query blocks) of one head.
 // Each wave takes every 4th tile of 32 reps (8 pages).  S^T = R . Probe^T runs
 // on v_mfma_f32_32x32x16_bf16, so a lane holds one probe and the 4 reps of
-// each of its pages: the page's features are lane-local.  Two passes over the
-// reps: the first finds each probe's max and sum of exp, the second turns the
-// recomputed logits into probabilities and features; per-page values are
-// summed over the 16 probe lanes of a block with cross-lane shuffles.  The
-// risk rows then stay in LDS for selection, which ranks 64-bit keys
-// (orderable risk, ~page) by counting: no sort network, ties -> lower page.
+// each of its pages: the page's features are lane-local.  One pass over the
+// reps: each lane keeps a running max and sum of exponentials of its probe,
+// and since a page's features are linear in the probabilities of its reps,
+// each page value is formed with 2^(z - running max) and rescaled once the
+// probe's totals are known.  The rescaled values go through LDS to be summed
+// over the 16 probes of a block; the risk rows then stay in LDS for the
+// selection, a bitonic sort of 64-bit keys (group, orderable risk, ~page):
+// ties -> lower page.  Workgroups appended to the grid write the call's rep
+// value rows on the side.
 #include "common.h"
 
 using namespace ssa;
@@ -29,13 +32,12 @@ constexpr int kThreads = 256;
 constexpr int kMaxPages = 512;
 constexpr int kAnchors = 24;
 constexpr int kCurrent = 72;
+constexpr int kTilesPerWave = kMaxPages / 32;   // tiles of 8 pages, every 4th to a wave
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
 typedef __attribute__((address_space(3))) const uint16_t lds_u16;
-
-__constant__ int kProbeOffsets[16] = {0, 4, 8, 13, 17, 21, 25, 29, 34, 38, 42, 46, 50, 55, 59, 63};
 
 struct RouteParams {
   const uint16_t* q;           // probe source
@@ -61,7 +63,7 @@ struct RouteParams {
 
 constexpr int kSlotBytes = 9 * 1024;   // a rep tile: 32 rows x 256 B (swizzled) + its pages' stats (768 B)
 
-struct Sel {                   // selection state, aliasing the tile ring once both passes are done
+struct Sel {                   // selection state, aliasing the tile ring once the tiles are done
   unsigned long long key[2][kMaxPages];
   uint8_t sel[2][kMaxPages];
   int list[2][kMaxPages];
@@ -71,19 +73,8 @@ struct Smem {
   alignas(16) uint8_t ring[4][2][kSlotBytes];   // per-wave double buffer of rep tiles
   float part[4][32][2];        // per-wave (max, sum) of each probe
   float risk[2][kMaxPages];
-  float bmax_w[4];
 };
 static_assert(sizeof(Sel) <= sizeof(Smem::ring), "selection state must fit in the tile ring");
-
-// Sum over each 16-lane row, left in the row's lane 15 (DPP row shifts,
-// out-of-row sources read as 0).
-__device__ __forceinline__ float row_sum16(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, true));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xf, 0xf, true));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xf, 0xf, true));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xf, 0xf, true));
-  return v;
-}
 
 // Maxima as trees of v_max3 / v_max.  The sources build with NaN-free
 // float semantics, so the compiler adds no quieting of matrix-pipe results
@@ -121,11 +112,13 @@ __device__ __forceinline__ void rep_logits(const u32x4 (&av)[8], const u32x4 (&q
 }
 
 // Value of lane (lane ^ LX) for a 64-bit key: DPP quad permutes for 1 and 2,
-// ds_swizzle bit-mask mode for 4, 8 and 16, the 32-lane swap for 32.
+// the DPP row rotate by 8 for 8, ds_swizzle bit-mask mode for 4 and 16, the
+// 32-lane swap for 32.
 template <int LX>
 __device__ __forceinline__ uint32_t xlane32(uint32_t v, int lane) {
   if constexpr (LX == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);   // [1,0,3,2]
   else if constexpr (LX == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);   // [2,3,0,1]
+  else if constexpr (LX == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
   else if constexpr (LX == 32) {
     const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
     return lane < 32 ? r[1] : r[0];
@@ -191,10 +184,75 @@ __device__ __forceinline__ void sort512_desc(unsigned long long (&key)[4], int b
           const bool desc = (e & k) == 0;
           const bool keep_max = ((e & j) == 0) == desc;
           const unsigned long long x = key[i], y = other[i];
-          key[i] = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+          key[i] = (y > x) == keep_max ? y : x;
         }
       }
     }
+  }
+}
+
+// Rep value rows written on the side by workgroups of their own, appended
+// to the router's grid: they take the slots of the CUs that hold one router
+// workgroup.  Block r writes pages [r*kRvPages, (r+1)*kRvPages) of the flat
+// (head, page) range; item = (page, 8 dims), two per thread at a time.
+constexpr int kRvPages = 64;
+
+struct RvIn {
+  u32x4 mean, det[3], basis[8];
+};
+
+__device__ __forceinline__ void rv_load(const RouteParams& p, int h, int pg, int c, RvIn& in) {
+  const long long row = (long long)h * p.HP + pg;
+  in.mean = ldg16(p.rmean + row * kHeadDim + 8 * c);
+#pragma unroll
+  for (int a = 0; a < 3; ++a) in.det[a] = ldg16(p.rdetail + row * 24 + 8 * a);
+#pragma unroll
+  for (int dd = 0; dd < 8; ++dd) in.basis[dd] = ldg16(p.rbasis + ((long long)h * kHeadDim + 8 * c + dd) * 8);
+}
+
+__device__ __forceinline__ void rv_store(const RouteParams& p, int h, int pg, int c, const RvIn& in) {
+  float dv[24];
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      dv[8 * a + 2 * w] = bf16_lo(in.det[a][w]);
+      dv[8 * a + 2 * w + 1] = bf16_hi(in.det[a][w]);
+    }
+  u32x4 outw[4];
+#pragma unroll
+  for (int dd = 0; dd < 8; ++dd) {
+    float b[8], o[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      b[2 * w] = bf16_lo(in.basis[dd][w]);
+      b[2 * w + 1] = bf16_hi(in.basis[dd][w]);
+    }
+    const float mu = (dd & 1) ? bf16_hi(in.mean[dd >> 1]) : bf16_lo(in.mean[dd >> 1]);
+    rep_value_rows(mu, dv, b, o);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const uint32_t v = to_bf16(o[rr]);
+      if (dd & 1) outw[rr][dd >> 1] |= v << 16;
+      else outw[rr][dd >> 1] = v;
+    }
+  }
+  uint16_t* dst = p.rvals + ((long long)h * p.HPV + pg) * 4 * kHeadDim + 8 * c;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) *reinterpret_cast<u32x4*>(dst + rr * kHeadDim) = outw[rr];
+}
+
+__device__ void rep_value_block(const RouteParams& p, int r) {
+  const int beg = r * kRvPages, n = min(p.H * p.P - beg, kRvPages) * 16;
+  for (int it = threadIdx.x; it < n; it += 2 * kThreads) {
+    const int it2 = it + kThreads;
+    const int f0 = beg + (it >> 4), f1 = beg + (it2 >> 4);
+    const int h0 = f0 / p.P, h1 = f1 / p.P;
+    RvIn a, b;
+    rv_load(p, h0, f0 - h0 * p.P, it & 15, a);
+    if (it2 < n) rv_load(p, h1, f1 - h1 * p.P, it2 & 15, b);
+    rv_store(p, h0, f0 - h0 * p.P, it & 15, a);
+    if (it2 < n) rv_store(p, h1, f1 - h1 * p.P, it2 & 15, b);
   }
 }
 
@@ -202,6 +260,10 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   __shared__ Smem s;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int NP = (p.T + 1) >> 1;
+  if ((int)blockIdx.x >= p.H * NP) {
+    rep_value_block(p, blockIdx.x - p.H * NP);
+    return;
+  }
   const int work = xcd_remap(blockIdx.x, p.H * NP);
   const int h = work / NP, t0 = 2 * (work % NP);
   const int P = p.P;
@@ -216,9 +278,9 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   const float c2 = kLog2e / sqrtf((float)kHeadDim);
   // Each wave owns tiles wave + 4 j (j < nmine) and a double buffer of them
   // in LDS: no other wave reads its slots, so its own load counter orders
-  // them.  A wave without tiles (P < 32) re-reads tile `wave` and skips it.
+  // them.  A wave without tiles (P <= 24) re-reads the last tile and skips it.
   const int nmine = __builtin_amdgcn_readfirstlane(max((ntiles - wave + 3) >> 2, 0));
-  auto mine = [&](int jj) { return wave + 4 * max(min(jj, nmine - 1), 0); };
+  auto mine = [&](int jj) { return min(wave + 4 * max(min(jj, nmine - 1), 0), ntiles - 1); };
   lds_u8* const ring = (lds_u8*)&s.ring[wave][0][0];
   const uint32_t ring_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring);
   // row offsets of a full tile in the instruction-offset form of dma_rows:
@@ -250,161 +312,62 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   };
   auto wait_lds = [&]() { __builtin_amdgcn_s_waitcnt(0xC07F); };   // lgkmcnt(0)
 
-  // pass 1's first two tiles are in flight while the probe rows load
+  // Setup.  Every global read it needs is issued first and consumed before
+  // the first rep tiles go out: the compiler's wait for one of these loads
+  // would otherwise also wait for tile loads issued after it.
+  //
+  // probe operand (B): dims 16*st + 8*hh + [0,8) (the k order of read_reps)
+  const long long row = p.gathered ? m : probe_row(m);
+  const uint16_t* qp = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
+  u32x4 qop[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st + 8 * hh);
+  // max_p stats[p,1,11] over the head's pages, in every wave (pages <= 512:
+  // up to 8 per lane), so the tiles need no barrier first
+  uint32_t bw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) bw[i] = lane + 64 * i < P ? sth[(long long)(lane + 64 * i) * 48 + 23] : 0xff80u;
+  auto uniform = [](float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v))); };
+  const float th0 = uniform(p.theta[h * 4 + 0]), th1 = uniform(p.theta[h * 4 + 1]);
+  const float th2 = uniform(p.theta[h * 4 + 2]), th3 = uniform(p.theta[h * 4 + 3]);
+  // the loads above are complete past this point
+#pragma unroll
+  for (int st = 0; st < 8; ++st) asm volatile("" ::"v"(qop[st]));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("" ::"v"(bw[i]));
+  // the first two rep tiles are in flight during the rest of the setup
   issue_tile(mine(0), 0, true);
   issue_tile(mine(1), 1, true);
 
-  // probe operand (B): dims 16*st + 8*hh + [0,8) (the k order of read_reps).
-  // q2[g] = sum of q^2 over dims 16g..16g+15 / D, summed in one lane per
-  // group from the dims 64*hh + [0,64) of this lane half
-  const long long row = p.gathered ? m : kProbeOffsets[m];
-  const uint16_t* qp = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
-  u32x4 qop[8];
+  // q2[g] = sum of q^2 over dims 16g..16g+15 / D: this lane's 8 of them plus
+  // the other lane half's
   float q2[8];
 #pragma unroll
-  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st + 8 * hh);
-  {
-    float g4[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int st = 0; st < 8; ++st) {
+    float part = 0.f;
 #pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const u32x4 v = ldg16(qp + 64 * hh + 8 * st);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float a = bf16_lo(v[w]), b = bf16_hi(v[w]);
-        g4[st >> 1] += a * a + b * b;
-      }
+    for (int w = 0; w < 4; ++w) {
+      const float a = bf16_lo(qop[st][w]), b = bf16_hi(qop[st][w]);
+      part += a * a + b * b;
     }
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float other = __shfl_xor(g4[g], 32);
-      q2[4 * hh + g] = g4[g] / kHeadDim;
-      q2[4 * (1 - hh) + g] = other / kHeadDim;
-    }
+    const float other = __shfl_xor(part, 32);
+    q2[st] = (part + other) / kHeadDim;
   }
   float qsum = 0.f;
 #pragma unroll
   for (int g = 0; g < 8; ++g) qsum += q2[g];
   const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
 
-  // rep value rows of this workgroup's share of the head's pages (the
-  // workgroups of a head split its pages evenly); the tile loads issued
-  // above are in flight meanwhile
-  if (p.rvals) {
-    const int share = (P + NP - 1) / NP, pbeg = (work % NP) * share, npg = min(P - pbeg, share);
-    const int d = tid & 127;
-    float b[8];
-    {
-      const u32x4 bw = ldg16(p.rbasis + ((long long)h * kHeadDim + d) * 8);
+  float bmax = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        b[2 * w] = bf16_lo(bw[w]);
-        b[2 * w + 1] = bf16_hi(bw[w]);
-      }
-    }
-    for (int pl = tid >> 7; pl < npg; pl += 2) {
-      const long long pg = (long long)h * p.HP + pbeg + pl;
-      float dv[24], o[4];
-#pragma unroll
-      for (int k = 0; k < 24; ++k) dv[k] = bf16_to_f32(p.rdetail[pg * 24 + k]);
-      rep_value_rows(bf16_to_f32(p.rmean[pg * kHeadDim + d]), dv, b, o);
-      uint16_t* dst = p.rvals + (((long long)h * p.HPV + pbeg + pl) * 4) * kHeadDim + d;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) dst[rr * kHeadDim] = to_bf16(o[rr]);
-    }
-  }
+  for (int i = 0; i < 8; ++i) bmax = fmaxf(bmax, bf16_to_f32(bw[i]));
+  bmax = wave_max(bmax);
 
-  // pass 1: max and sum of exp over all reps, per probe, and the per-head
-  // bound of the page value norm max_p stats[p,1,11] from the tiles' stats.
-  // Software-pipelined: the logits of tile j+1 are on the matrix pipe while
-  // the exponentials of tile j run.
-  float mx = -INFINITY, den = 0.f, bmax = -INFINITY;
-  auto stats_bound = [&](int j) {
-    const int tile = mine(j);
-    if (lane < 8 && tile * 8 + lane < P)
-      bmax = fmaxf(bmax, bf16_to_f32(((lds_u16*)(ring + (j & 1) * kSlotBytes + 8192))[lane * 48 + 23]));
-  };
-  auto soft1 = [&](f32x16 S, int tile) {
-    if (tile * 8 + 8 <= P) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) S[i] *= c2;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int page = tile * 8 + 2 * (i >> 2) + hh;
-        S[i] = page < P ? S[i] * c2 : -INFINITY;
-      }
-    }
-    const float tmax = max2f(max3f(max3f(S[0], S[1], S[2]), max3f(S[3], S[4], S[5]), max3f(S[6], S[7], S[8])),
-                             max3f(max3f(S[9], S[10], S[11]), max3f(S[12], S[13], S[14]), S[15]));
-    const float mnew = fmaxf(mx, tmax);
-    const float muse = mnew == -INFINITY ? 0.f : mnew;
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc += __builtin_amdgcn_exp2f(S[i] - muse);
-    den = den * __builtin_amdgcn_exp2f(mx - muse) + acc;
-    mx = mnew;
-  };
-  // tile j's slot is read into registers, then refilled with tile j+2
-  auto next_logits = [&](int j, f32x16& S) {
-    wait_tile(9);                                    // tile j landed (tile j+1 may be in flight)
-    u32x4 av[8];
-    read_reps(ring + (j & 1) * kSlotBytes, lane, av);
-    stats_bound(j);
-    wait_lds();
-    issue_tile(mine(j + 2), j & 1, true);
-    rep_logits(av, qop, S);
-  };
-  if (nmine > 0) {
-    f32x16 S;
-    next_logits(0, S);
-    for (int j = 0; j + 1 < nmine; ++j) {
-      f32x16 Sn;
-      next_logits(j + 1, Sn);
-      soft1(S, mine(j));
-      S = Sn;
-    }
-    soft1(S, mine(nmine - 1));
-  }
-  wait_loads();                                      // surplus loads of the clamped tail
-  issue_tile(mine(0), 0, true);                      // pass 2's first two tiles
-  issue_tile(mine(1), 1, true);
-  {
-    const float omx = __shfl_xor(mx, 32), oden = __shfl_xor(den, 32);
-    const float mm = fmaxf(mx, omx);
-    const float mu = mm == -INFINITY ? 0.f : mm;
-    den = den * __builtin_amdgcn_exp2f(mx - mu) + oden * __builtin_amdgcn_exp2f(omx - mu);
-    mx = mm;
-    if (hh == 0) {
-      s.part[wave][pi][0] = mx;
-      s.part[wave][pi][1] = den;
-    }
-    bmax = wave_max(bmax);
-    if (lane == 0) s.bmax_w[wave] = bmax;
-  }
-  __syncthreads();
-  float MX = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) MX = fmaxf(MX, s.part[w][pi][0]);
-  float DEN = 0.f;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) DEN += s.part[w][pi][1] * __builtin_amdgcn_exp2f(s.part[w][pi][0] - MX);
-  // probabilities 2^(z2 - MX) / DEN as one power of two, 2^(z2 - (MX + log2 DEN))
-  const float nlse = -(MX + __log2f(DEN));
-  if (p.lse && wave == 0 && hh == 0 && t0 + blk < p.T)
-    p.lse[((long long)h * p.T + t0 + blk) * 16 + m] = (MX + __log2f(DEN)) * 0.69314718055994531f;
-  bmax = fmaxf(fmaxf(s.bmax_w[0], s.bmax_w[1]), fmaxf(s.bmax_w[2], s.bmax_w[3]));
-  // theta is wave-uniform; taking it into scalar registers here also keeps
-  // the wait for its load out of the tile loop (a wait there would cover
-  // the in-flight tile loads too)
-  auto uniform = [](float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v))); };
-  const float th0 = uniform(p.theta[h * 4 + 0]), th1 = uniform(p.theta[h * 4 + 1]);
-  const float th2 = uniform(p.theta[h * 4 + 2]), th3 = uniform(p.theta[h * 4 + 3]);
-
-  // pass 2: probabilities -> four features -> theta-weighted value -> probe mean.
-  // The per-rep stats reach the lane layout of S through the matrix pipe:
-  // U^T = ST . (q2_hi | q2_lo)^T gives u_r = sum_g q2_g st[r,g] (stats in both
-  // k halves, q2 split into two bf16 terms); B^T = st[r,8] (qn_hi + qn_lo)
-  // gives beta_r; unit-vector products give st[r,9] and st[r,10].
+  // One pass over the reps.  Each lane keeps a running max m and sum of
+  // exponentials den of its probe over its reps; the features of a page are
+  // linear in the probabilities of its reps, so each page value is formed
+  // with 2^(z2 - m) and rescaled by 2^(m - MX) / DEN once the totals are
+  // known.  Page values and the max they were formed with stay in registers.
   u32x4 bq, bqn, bone;
   {
 #pragma unroll
@@ -417,9 +380,6 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     bqn = u32x4{hh == 0 ? pack_bf16(qh, qn - qh) : 0u, 0u, 0u, 0u};
     bone = u32x4{hh == 0 ? 0x3F80u : 0u, 0u, 0u, 0u};
   }
-  // per-tile stats in registers: rep row lane%32's words (st0,st1)..(st6,st7),
-  // (st8,st9), (st10,st11), and stats[p,0,11], stats[p,1,11] of this lane's
-  // 4 pages (2 jj + hh of the tile)
   struct TileStats {
     u32x2 w01, w23, w45;
     float s011[4], s111[4];
@@ -447,22 +407,34 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     rep_logits(av, qop, S);
   };
   const uint32_t lo_only = hh == 0 ? 0xffffffffu : 0u;
-  // features of one tile from its logits and stats, down to the block mean
-  auto soft2 = [&](const f32x16& S, const TileStats& ts, int tile) {
+  float mx = -INFINITY, den = 0.f;
+  float vals[kTilesPerWave][4], mj[kTilesPerWave];
+  auto soft = [&](f32x16 S, const TileStats& ts, int tile, float (&v4)[4], float& mt) {
     const u32x4 ag = {ts.w01[0], ts.w01[1], ts.w23[0], ts.w23[1]};
     const uint32_t st8 = ts.w45[0] & 0xffffu, st9 = ts.w45[0] >> 16, st10 = ts.w45[1] & 0xffffu;
     const f32x16 U = mfma32(ag, bq, f32x16{});
     const f32x16 Bt = mfma32(u32x4{(st8 | (st8 << 16)) & lo_only, 0u, 0u, 0u}, bqn, f32x16{});
     const f32x16 F9 = mfma32(u32x4{st9 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
     const f32x16 F10 = mfma32(u32x4{st10 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
+    if (tile * 8 + 8 > P) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int page = tile * 8 + 2 * (i >> 2) + hh;
+        if (page >= P) S[i] = -INFINITY;
+      }
+    }
+    const float tmax = max2f(max3f(max3f(S[0], S[1], S[2]), max3f(S[3], S[4], S[5]), max3f(S[6], S[7], S[8])),
+                             max3f(max3f(S[9], S[10], S[11]), max3f(S[12], S[13], S[14]), S[15]));
+    const float mnew = fmaxf(mx, tmax * c2);
+    float asum = 0.f;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      const int page = tile * 8 + 2 * jj + hh;
       float prob[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) prob[i] = __builtin_amdgcn_exp2f(fmaf(S[4 * jj + i], c2, nlse));
+      for (int i = 0; i < 4; ++i) prob[i] = __builtin_amdgcn_exp2f(fmaf(S[4 * jj + i], c2, -mnew));
       const float alpha = ((prob[0] + prob[1]) + prob[2]) + prob[3];
-      const float c = ts.s111[jj] + bmax;                 // stats[p,1,11] + max_p stats[p,1,11]
+      asum += alpha;
+      const float c = ts.s111[jj] + bmax;
       float x0 = alpha * ts.s011[jj], x1 = 0.f, x2 = 0.f, x3 = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -475,35 +447,74 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       }
       x2 *= c;
       x3 *= c;
-      float val = ((x0 * th0 + x1 * th1) + x2 * th2) + x3 * th3;
-      // mean over the 16 probes of this lane's block: one DPP row
-      val = row_sum16(val);
-      if (m == 15 && page < P) s.risk[blk][page] = val * 0.0625f;
+      v4[jj] = ((x0 * th0 + x1 * th1) + x2 * th2) + x3 * th3;
     }
+    den = den * __builtin_amdgcn_exp2f(mx - mnew) + asum;
+    mx = mnew;
+    mt = mnew;
   };
-  // software-pipelined like pass 1: logits of tile j+1 beside the features of tile j
-  if (nmine > 0) {
-    f32x16 S;
-    TileStats ts;
-    next_tile(0, S, ts);
-    for (int j = 0; j + 1 < nmine; ++j) {
-      f32x16 Sn;
-      TileStats tn;
-      next_tile(j + 1, Sn, tn);
-      soft2(S, ts, mine(j));
-      S = Sn;
-      ts = tn;
+#pragma unroll
+  for (int j = 0; j < kTilesPerWave; ++j) {
+    if (j < nmine) {
+      f32x16 S;
+      TileStats ts;
+      next_tile(j, S, ts);
+      soft(S, ts, mine(j), vals[j], mj[j]);
     }
-    soft2(S, ts, mine(nmine - 1));
   }
   wait_loads();                                      // the ring is reused for selection below
-  __syncthreads();
-
-  const int nrow = min(2, p.T - t0);
-  for (int i = tid; i < 2 * P; i += kThreads) {
-    const int b = i / P, pg = i % P;
-    if (b < nrow) p.risk[((long long)h * p.T + t0 + b) * P + pg] = s.risk[b][pg];
+  {
+    const float omx = __shfl_xor(mx, 32), oden = __shfl_xor(den, 32);
+    const float mm = fmaxf(mx, omx);
+    const float mu = mm == -INFINITY ? 0.f : mm;   // a wave without tiles (P <= 24) has none
+    den = den * __builtin_amdgcn_exp2f(mx - mu) + oden * __builtin_amdgcn_exp2f(omx - mu);
+    mx = mm;
+    if (hh == 0) {
+      s.part[wave][pi][0] = mx;
+      s.part[wave][pi][1] = den;
+    }
   }
+  __syncthreads();
+  float MX = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) MX = fmaxf(MX, s.part[w][pi][0]);
+  float DEN = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) DEN += s.part[w][pi][1] * __builtin_amdgcn_exp2f(s.part[w][pi][0] - MX);
+  const float nlse = -(MX + __log2f(DEN));
+  if (p.lse && wave == 0 && hh == 0 && t0 + blk < p.T)
+    p.lse[((long long)h * p.T + t0 + blk) * 16 + m] = (MX + __log2f(DEN)) * 0.69314718055994531f;
+  // page values: rescaled into LDS by probe ([block][page][probe], the tile
+  // ring is free now), then summed over the block's 16 probes
+  float* const tr = reinterpret_cast<float*>(&s.ring[0][0][0]);
+  constexpr int kTrBlock = kMaxPages * 16 + 32;    // +32 floats: the two blocks use disjoint banks
+#pragma unroll
+  for (int j = 0; j < kTilesPerWave; ++j) {
+    if (j < nmine) {
+      const float f = __builtin_amdgcn_exp2f(mj[j] + nlse);
+      const int tile = mine(j);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int page = tile * 8 + 2 * jj + hh;
+        if (page < P) tr[blk * kTrBlock + page * 16 + m] = vals[j][jj] * f;
+      }
+    }
+  }
+  __syncthreads();
+  const int nrow = min(2, p.T - t0);
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    for (int pg = tid; pg < P; pg += kThreads) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(tr + b * kTrBlock + pg * 16);
+      const f32x4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+      const float sum = (((v0[0] + v0[1]) + (v0[2] + v0[3])) + ((v1[0] + v1[1]) + (v1[2] + v1[3]))) +
+                        (((v2[0] + v2[1]) + (v2[2] + v2[3])) + ((v3[0] + v3[1]) + (v3[2] + v3[3])));
+      const float val = sum * 0.0625f;
+      s.risk[b][pg] = val;
+      if (b < nrow) p.risk[((long long)h * p.T + t0 + b) * P + pg] = val;
+    }
+  }
+  __syncthreads();
   if (p.mode < 0) return;
 
   // ---------------------------------------------------------------- select
@@ -574,21 +585,21 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     }
     __syncthreads();
     if (idsrow) {
+      // LUT slot = number of listed pages ahead: own first (largest key),
+      // then descending risk, ties -> lower page.  The sorted keys are no
+      // longer needed, so the listed pages' keys take their place.
       for (int i = bt; i < p.C; i += 128) {
         const int pg = sl.list[b][i];
-        int slot = 0;
-        if (pg != own[b]) {
-          const uint32_t kx = orderable(s.risk[b][pg]);
-          int rank = 0;
-          for (int j = 0; j < p.C; ++j) {
-            const int y = sl.list[b][j];
-            if (y == own[b]) continue;
-            const uint32_t ky = orderable(s.risk[b][y]);
-            rank += (ky > kx) || (ky == kx && y < pg);
-          }
-          slot = 1 + rank;
-        }
-        if (row_ok && slot < p.C) idsrow[slot] = pg;
+        sl.key[b][i] = pg == own[b] ? ~0ull
+                                    : ((unsigned long long)orderable(s.risk[b][pg]) << 32) | (uint32_t)(1023 - pg);
+      }
+      __syncthreads();
+      for (int i = bt; i < p.C; i += 128) {
+        const unsigned long long kx = sl.key[b][i];
+        int rank = 0;
+#pragma unroll 8
+        for (int j = 0; j < p.C; ++j) rank += sl.key[b][j] > kx;
+        if (row_ok) idsrow[rank] = sl.list[b][i];
       }
     }
   }
@@ -615,6 +626,9 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
       mode > 2)
     return (int)hipErrorInvalidValue;
   if (rep_values && (!mean || !detail || !basis || rep_head_pages < pages)) return (int)hipErrorInvalidValue;
+  // the rep value rows move in 16-byte loads and stores
+  if (rep_values && (((uintptr_t)mean | (uintptr_t)detail | (uintptr_t)basis | (uintptr_t)rep_values) & 15))
+    return (int)hipErrorInvalidValue;
   if (mode == 0 && (count < 1 + kAnchors || pages < kAnchors + kCurrent)) return (int)hipErrorInvalidValue;
   if (mode == 1 && (count != kAnchors + total || pages <= kAnchors + kCurrent || current == nullptr))
     return (int)hipErrorInvalidValue;
@@ -647,7 +661,8 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
   p.rvals = (uint16_t*)rep_values;
   p.HPV = rep_head_pages;
   const int np = (blocks + 1) / 2;
-  hipLaunchKernelGGL(route_kernel, dim3(heads * np), dim3(kThreads), 0, stream, p);
+  const int nrv = rep_values ? (heads * pages + kRvPages - 1) / kRvPages : 0;
+  hipLaunchKernelGGL(route_kernel, dim3(heads * np + nrv), dim3(kThreads), 0, stream, p);
   return (int)hipGetLastError();
 }
 

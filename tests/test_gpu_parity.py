@@ -53,6 +53,25 @@ def test_risk_matches_oracle(device):
     assert rel < 1e-4
 
 
+@pytest.mark.parametrize("pages", [8, 20, 72])
+def test_risk_small_windows(device, pages):
+    """Windows of fewer than 32 pages leave some of the router's waves with
+    no tile of their own, and 20 pages end in a partial tile; 72 is the first
+    chunk's window (VB/graph.py:143-148)."""
+    x = call_inputs(0, 9)
+    sub = x.summary.slice(0, pages)
+    pr = ref.probes(x.q)
+    got = risk_fn(ref.probes(x.q.to(device)), None, Summary(*(t.to(device) for t in
+                                                               (x.summary.keys, x.summary.mean, x.summary.detail,
+                                                                x.summary.stats))).slice(0, pages),
+                  x.theta.to(device)).cpu()
+    want = ref.risk(pr, ref.route_logits(pr, sub.keys, torch.float64), sub.stats, x.theta, dtype=torch.float64)
+    assert got.shape == (12, 72, pages)
+    rel = ((got.double() - want).abs() / want.abs().clamp_min(1e-30)).max()
+    print(f"P={pages} risk max rel err {float(rel):.3e}", flush=True)
+    assert rel < 1e-4
+
+
 @pytest.mark.parametrize("cfg,frames", [(0, 9), (1, 18)])
 def test_route_base_matches_oracle(device, cfg, frames):
     x = call_inputs(cfg, frames)
