@@ -32,7 +32,9 @@ constexpr int kAnchors = 24;
 constexpr int kCurrent = 72;
 constexpr int kFeatures = 712;
 constexpr int kMaxHidden = 256;
-constexpr int kEncPages = 8;        // pages per encode workgroup
+constexpr int kEncPages = 4;        // pages per encode workgroup (the first-layer weights stream
+                                    // through each workgroup once: 4 pages balance that against the FMAs)
+static_assert(kEncPages % 4 == 0, "pages go to the four waves in turn");
 constexpr int kCoefStride = 128;    // bf16 per page: co[85] | 0 x 11 | A[32]
 constexpr int kCoefA = 96;
 constexpr int kCand = 48;           // 16 removes + 32 adds
@@ -66,9 +68,9 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
   const int g0 = blockIdx.x * kEncPages;
   const int npg = min(kEncPages, p.pages - g0);
 
-  // features: each wave normalises two pages
-  for (int j = 0; j < 2; ++j) {
-    const int pl = 2 * wave + j;
+  // features: wave w normalises pages w, w + 4, ...
+  for (int j = 0; j < kEncPages / 4; ++j) {
+    const int pl = 4 * j + wave;
     if (pl >= npg) break;
     const long long pg = (long long)h * p.HP + p.first + g0 + pl;
     float kv[8];
@@ -117,14 +119,14 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
 #pragma unroll 8
     for (int k = 0; k < kFeatures; ++k) {
       const float a = wr[(long long)k * 2 * H], b = wp[(long long)k * 2 * H];
-      const f32x4 x0 = *reinterpret_cast<const f32x4*>(&f[k][0]);
-      const f32x4 x1 = *reinterpret_cast<const f32x4*>(&f[k][4]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ar[i] = fmaf(x0[i], a, ar[i]);
-        ar[4 + i] = fmaf(x1[i], a, ar[4 + i]);
-        ap[i] = fmaf(x0[i], b, ap[i]);
-        ap[4 + i] = fmaf(x1[i], b, ap[4 + i]);
+      for (int c = 0; c < kEncPages / 4; ++c) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(&f[k][4 * c]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ar[4 * c + i] = fmaf(x[i], a, ar[4 * c + i]);
+          ap[4 * c + i] = fmaf(x[i], b, ap[4 * c + i]);
+        }
       }
     }
     const float br = p.b1[tid], bp = p.b1[H + tid];
