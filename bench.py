@@ -30,8 +30,8 @@ sys.path.insert(0, ROOT)
 
 # HBM bytes per attn_kernel launch of the base-tier call, keyed by (pages, exact pages), measured with
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this bench (profiles/attn_kernel_base432_traffic.md):
-# 117.4 MB read + 14.2 MB written
-MEASURED_TRAFFIC = {(432, 64): 131.6e6}
+# 116.4 MB read + 14.2 MB written
+MEASURED_TRAFFIC = {(432, 64): 130.6e6}
 METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
@@ -41,8 +41,10 @@ PSET_HEADS = (3, 4, 9)
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # one call is ~0.25 ms: 100 warmup calls (~25 ms) bring the clocks to
+    # their steady state under this load, 200 timed calls take ~50 ms
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--frames", type=int, default=18, help="window frames (18 -> 432 pages)")
     ap.add_argument("--precise-av", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -148,8 +150,20 @@ def main():
 
     iters = max(10, args.steps)
     attn_ms = time_loop(attn_only, iters, stream)
-    route_ms = time_loop(lambda: route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False,
-                                       rep_basis=basis, rep_out=vrep_call), iters, stream)
+    # the router kernel alone (straight through the C ABI: back-to-back calls of the Python wrapper would
+    # time the host, not the kernel)
+    rids, _, rrisk, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False,
+                              rep_basis=basis, rep_out=vrep_call)
+    theta32 = g.theta.float().contiguous()
+
+    def route_only():
+        _lib.check(L.ssa_route(_lib.ptr(g.q), D, 64 * H * D, H * D, 0, _lib.ptr(g.summary.keys),
+                               _lib.ptr(g.summary.stats), _lib.ptr(theta32), None, None, _lib.ptr(rrisk),
+                               _lib.ptr(rids), None, None, H, N // 64, P, g.summary.head_pages, C, 0, 0,
+                               _lib.ptr(g.summary.mean), _lib.ptr(g.summary.detail), _lib.ptr(basis),
+                               _lib.ptr(vrep_call), P, _lib.stream_handle(dev)), "ssa_route")
+
+    route_ms = time_loop(route_only, iters, stream)
 
     dense_ms = None
     if not args.no_dense:
