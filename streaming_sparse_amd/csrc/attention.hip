@@ -29,6 +29,8 @@
 // The two key halves are merged through LDS at the end.
 #include "common.h"
 
+#include <type_traits>
+
 using namespace ssa;
 
 namespace {
@@ -116,13 +118,13 @@ __device__ __forceinline__ UnitSources unit_sources(const AttnParams& p, int h) 
 // of unit e (a page, or a rep tile) into `buf`: wave w of the 4*NB waves
 // loads rows (16/NB) w .. (16/NB) w + 16/NB - 1.  page_off / rep_off are the
 // instruction-offset forms of unit_offsets.
-template <int NB>
+template <int NB, int KIND = 2>
 __device__ __forceinline__ void issue_rows(const AttnParams& p, const UnitSources& src, int e, int kv, int wave,
                                            int lane, const UnitOffsets& page_off, const UnitOffsets& rep_off,
                                            lds_u8* buf) {
   constexpr int kLoads = 4 / NB;    // 1 KB loads per wave
   const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)buf + wave * 1024 * kLoads);
-  if (e >= 0) {
+  if (KIND == 0 || (KIND == 2 && e >= 0)) {
     dma_rows<kLoads>((kv ? src.v : src.k) + (uint32_t)e * src.page_bytes, kv ? page_off.v : page_off.k, l);
   } else {
     const int rt = rep_tile(e);
@@ -174,9 +176,10 @@ __device__ __forceinline__ float max2f(float a, float b) { return __builtin_fmax
 
 // Row max of S in log2 units (+ bias); rep tiles first drop the reps of
 // selected pages and of pages >= P.  Returns the bias of the unit.
+template <int KIND = 2>
 __device__ __forceinline__ float unit_max(f32x16& S, int e, int pair, int lane, float scale_log2, float& mloc) {
   float bias = 0.0f;
-  if (e < 0) {
+  if (KIND == 1 || (KIND == 2 && e < 0)) {
     bias = 4.0f;
     const uint32_t drop = rep_drop(e) >> (8 * pair + (lane >> 5));
 #pragma unroll
@@ -358,21 +361,22 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   // i+3 is read from LDS in step i-1, so the read completes at its barrier.
   int u1 = unit(min(1, nunits - 1)), u2 = unit(min(2, nunits - 1));
   int u3raw = units[min(3, nunits - 1)];
-  auto step = [&](int i, f32x16& Sc, f32x16& Sn) {
+  auto step = [&](auto kind, int i, f32x16& Sc, f32x16& Sn) {
+    constexpr int K = decltype(kind)::value;
     const int cur = i & 1, nxt = cur ^ 1;
     const int u3 = __builtin_amdgcn_readfirstlane(u3raw);
     // the general call issues its loads first; the two-block call (8 waves,
     // half the loads each) spreads them over the first products
     if (NB == 1 || PRECISE) {
-      issue_rows<NB>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
-      issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
+      issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
+      issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
     }
     const float nb = bias - (m == -INFINITY ? 0.0f : m);
     if (PRECISE) {
       Sn = s_tile(kslot(nxt), pair, lane, qop);
       u32x4 pb[2], pl[2];
       probabilities<PRECISE>(Sc, nb, p.scale_log2, pb, pl);
-      bias = unit_max(Sn, u1, pair, lane, p.scale_log2, mloc);
+      bias = unit_max<K>(Sn, u1, pair, lane, p.scale_log2, mloc);
       pv<PRECISE>(pb, pl, vslot(cur), pair, lane, L, O);
     } else {
       // One instruction stream that keeps the matrix pipe fed: the 8
@@ -391,8 +395,8 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
         Sn = mfma32(ka[st], qop[st], Sn);
-        if (NB == 2 && st == 0) issue_rows<NB>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
-        if (NB == 2 && st == 3) issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
+        if (NB == 2 && st == 0) issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
+        if (NB == 2 && st == 3) issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
         if (st < 4)
           ka[st + 4] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + 8 + hh));
         else
@@ -422,7 +426,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
         __builtin_amdgcn_sched_barrier(0);
       }
       L = mfma32(ones, pb[1], L);
-      bias = unit_max(Sn, u1, pair, lane, p.scale_log2, mloc);
+      bias = unit_max<K>(Sn, u1, pair, lane, p.scale_log2, mloc);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
     }
@@ -434,13 +438,28 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     wait_loads();
     __syncthreads();
   };
+  // Units are the exact pages, then the rep tiles: steps whose two units in
+  // flight are both pages or both rep tiles take their loads and maxima
+  // without testing the kind of unit
+  using PageUnits = std::integral_constant<int, 0>;
+  using RepUnits = std::integral_constant<int, 1>;
+  using AnyUnits = std::integral_constant<int, 2>;
+  const int npages = NB == 1 ? min(p.C, nunits) : nunits;
   int i = 0;
+  for (; i + 2 < nunits && i + 3 < npages; i += 2) {
+    step(PageUnits{}, i, S0, S1);
+    step(PageUnits{}, i + 1, S1, S0);
+  }
+  for (; i + 2 < nunits && i + 1 < npages; i += 2) {
+    step(AnyUnits{}, i, S0, S1);
+    step(AnyUnits{}, i + 1, S1, S0);
+  }
   for (; i + 2 < nunits; i += 2) {
-    step(i, S0, S1);
-    step(i + 1, S1, S0);
+    step(RepUnits{}, i, S0, S1);
+    step(RepUnits{}, i + 1, S1, S0);
   }
   if (i + 1 < nunits) {
-    step(i, S0, S1);
+    step(AnyUnits{}, i, S0, S1);
     ++i;
     S0 = S1;
   }
