@@ -118,7 +118,7 @@ int ssa_encode(const void* keys, const void* mean, const void* detail, const voi
  * (0/1 bytes) iff its gain > 0 and every legal score is finite, and the row
  * of ids [H,blocks,count] is rebuilt (own first, then descending risk).
  * Caller-owned scratch: cand n_heads*blocks*16*48*34 fp64, rows
- * n_heads*blocks*16*4*52 fp64, pool n_heads*blocks*64 int32.  Per-row outputs:
+ * n_heads*blocks*16*2*52 fp64, pool n_heads*blocks*64 int32.  Per-row outputs:
  * gain [n_heads,blocks] fp64, info [n_heads,blocks,3] int32 = (executed, best
  * pair index remove*32+add, non-finite legal scores); scores
  * [n_heads,blocks,16,32] fp64 (illegal pairs -1e30) or NULL; stats [3]

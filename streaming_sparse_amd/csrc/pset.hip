@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void pset_pool_kernel(PsetParams p) {
 
 // ----------------------------------------------------------------- rows ----
 
-constexpr int kSplit = 4;          // page ranges per (head, pair of blocks)
+constexpr int kSplit = 2;          // page ranges per (head, pair of blocks)
 constexpr int kRowPart = 52;       // accH[16], accT[16], accB[16], sH, sT, sB, max logs
 
 struct RowsSmem {
@@ -621,12 +621,16 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
       }
     }
     {
-      // kSplit x 52 doubles = 104 16-byte chunks
+      // kSplit x 52 doubles in 16-byte chunks
+      constexpr int kChunks = kSplit * kRowPart / 2;
       const u32x4* rs = reinterpret_cast<const u32x4*>(p.rows + (rowbase * 16 + m) * kSplit * kRowPart);
-      const u32x4 r0 = rs[lane], r1 = rs[min(64 + lane, 103)];
+      u32x4 r[(kChunks + 63) / 64];
+#pragma unroll
+      for (int k = 0; k < (kChunks + 63) / 64; ++k) r[k] = rs[min(64 * k + lane, kChunks - 1)];
       u32x4* dst = reinterpret_cast<u32x4*>(s.part[w]);
-      dst[lane] = r0;
-      if (lane < 40) dst[64 + lane] = r1;
+#pragma unroll
+      for (int k = 0; k < (kChunks + 63) / 64; ++k)
+        if (64 * k + lane < kChunks) dst[64 * k + lane] = r[k];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();

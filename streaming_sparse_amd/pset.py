@@ -22,7 +22,7 @@ COEF_A = 96
 CAND = 48
 CAND_VALS = 34
 ROW_VALS = 52
-ROW_SPLIT = 4          # page ranges per pair of query blocks in the rows kernel
+ROW_SPLIT = 2          # page ranges per pair of query blocks in the rows kernel
 POOL_INTS = 64
 
 
