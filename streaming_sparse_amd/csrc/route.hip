@@ -546,7 +546,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
         else if (pg >= P - kCurrent) key = (2ull << 62) | ord | low;
         else if (pg >= kAnchors) key = (1ull << 62) | ord | low;
       } else {
-        key = pg == own[b] ? ~0ull : ((1ull << 62) | ord | low);
+        key = pg == own[b] ? ~0ull - (unsigned long long)pg : ((1ull << 62) | ord | low);   // own first
       }
     }
     keys[i] = key;

@@ -105,6 +105,58 @@ def test_route_base_matches_oracle(device, cfg, frames):
     assert torch.equal(mask.cpu(), ref.mask_from_ids(got, P))
 
 
+def test_route_topk_matches_oracle(device):
+    """Fixed top-floor(0.1 P) with own forced (mode 2)."""
+    x = call_inputs(0, 9)
+    g = x.to(device)
+    ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='topk', own=g.own)
+    P = x.pages
+    r64 = ref.risk(ref.probes(x.q), ref.route_logits(ref.probes(x.q), x.summary.keys, torch.float64),
+                   x.summary.stats, x.theta, dtype=torch.float64)
+    count = max(1, int(P * 0.1))
+    want, want_mask = ref.select_topk(r64, x.own, count)
+    cand = r64.scatter(-1, x.own[..., None], -math.inf)
+    ties = ref.near_tie_rows(cand, torch.full(x.own.shape, count - 1))
+    got = ids.cpu()
+    same = (got == want).all(-1)
+    order_ties = ref.near_tie_order_rows(r64, want, 1)
+    same_set = (got.sort(-1).values == want.sort(-1).values).all(-1)
+    print(f"topk: {int(same.sum())}/{same.numel()} rows identical, {int(ties.sum())} near-tie rows", flush=True)
+    assert bool((same | ties | (order_ties & same_set)).all())
+    assert (got[..., 0] == x.own).all()
+    assert torch.equal(mask.cpu(), ref.mask_from_ids(got, P))
+    assert bool((mask.cpu() == want_mask)[~ties].all())
+
+
+@pytest.mark.parametrize("blocks", [3, 5])
+def test_route_odd_blocks(device, blocks):
+    """An odd number of query blocks leaves the router's last workgroup one
+    block; base tier on the first `blocks` blocks of the 216-page call."""
+    x = call_inputs(0, 9)
+    q = x.q[:, :64 * blocks].contiguous()
+    own = x.own[:, :blocks].contiguous()
+    g = x.to(device)
+    ids, mask, risk, _ = route(q.to(device), g.summary, g.theta, tier='base', own=own.to(device))
+    P = x.pages
+    count = P * 15 // 100
+    r64 = ref.risk(ref.probes(q), ref.route_logits(ref.probes(q), x.summary.keys, torch.float64),
+                   x.summary.stats, x.theta, dtype=torch.float64)
+    assert risk.shape == (12, blocks, P)
+    rel = float(((risk.cpu().double() - r64).abs() / r64.abs().clamp_min(1e-30)).max())
+    assert rel < 1e-4, rel
+    want = ref.select_base(r64, own, count)
+    cand = r64.clone()
+    cand[..., :24] = -math.inf
+    cand.scatter_(-1, own[..., None], -math.inf)
+    ties = ref.near_tie_rows(cand, torch.full(own.shape, count - 25)) | ref.near_tie_order_rows(r64, want, 25)
+    got = ids.cpu()
+    same = (got == want).all(-1)
+    print(f"blocks={blocks}: {int(same.sum())}/{same.numel()} rows identical, {int(ties.sum())} near-tie rows",
+          flush=True)
+    assert bool((same | ties).all())
+    assert torch.equal(mask.cpu(), ref.mask_from_ids(got, P))
+
+
 def test_route_intersection_matches_oracle(device):
     x = call_inputs(2, 18)
     g = x.to(device)
@@ -207,7 +259,7 @@ def test_attention_all_pages_equals_dense(device):
 def test_attention_odd_window_and_slab(device, n):
     """Window of 100 pages (last rep tile partly beyond P) inside a 128-page
     summary slab, head-major strided K/V, single-page LUT; random page tables
-    per block, for an even and an odd number of query blocks."""
+    per block, for an even and an odd number of query blocks, up to every page."""
     h, p, cap = 3, 100, 128
     gen = torch.Generator().manual_seed(77)
     q = torch.randn(1, n, h, 128, generator=gen).bfloat16()
@@ -221,7 +273,7 @@ def test_attention_odd_window_and_slab(device, n):
         getattr(slab, f)[:, :p] = getattr(s, f)
     k4 = kk.transpose(0, 1)[None]          # [1, L, H, D] view of head-major storage
     v4 = vv.transpose(0, 1)[None]
-    for count in (1, 7):
+    for count in (1, 7, p):     # p: every page exact (an odd block count takes the one-block kernel)
         t = n // 64
         ids = torch.stack([torch.randperm(p, generator=gen)[:count] for _ in range(h * t)]).reshape(h, t, count).int()
         sd = slab.slice(0, p)
