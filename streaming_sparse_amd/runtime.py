@@ -104,7 +104,8 @@ class ChunkRuntime:
             v = torch.randn(64 * P, H, D, generator=g, device=dev)
             k = k.to(torch.bfloat16)[None].contiguous()
             v = v.to(torch.bfloat16)[None].contiguous()
-            basis = workload.pca_basis(v[0].transpose(0, 1).reshape(H, P, 64, D).float()).to(torch.bfloat16)
+            # contiguous bf16 once here, so no call of the chunk copies it
+            basis = workload.pca_basis(v[0].transpose(0, 1).reshape(H, P, 64, D).float()).to(torch.bfloat16).contiguous()
             slab = Summary(torch.empty(H, P, 4, D, device=dev, dtype=torch.bfloat16),
                            torch.empty(H, P, D, device=dev, dtype=torch.bfloat16),
                            torch.empty(H, P, 3, 8, device=dev, dtype=torch.bfloat16),
