@@ -462,7 +462,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       soft(S, ts, mine(j), vals[j], mj[j]);
     }
   }
-  wait_loads();                                      // the ring is reused for selection below
+  wait_loads();                                      // the ring takes the probe sums, then the selection
   {
     const float omx = __shfl_xor(mx, 32), oden = __shfl_xor(den, 32);
     const float mm = fmaxf(mx, omx);
