@@ -70,8 +70,9 @@ def _near_tie(scores, legal, rel=1e-3):
     return ((top[..., 0] - top[..., 1]).abs() <= rel * scale) | (top[..., 0].abs() <= rel * scale)
 
 
-def test_pset_matches_oracle(device):
-    x, w, a, n = inputs()
+@pytest.mark.parametrize("frames", [18, 12])
+def test_pset_matches_oracle(device, frames):
+    x, w, a, n = inputs(frames)
     g, reader, enc = gpu_encoding(x, w, device)
     ws = Workspace()
     lse = torch.empty(12, 72, 16, device=device)
