@@ -16,7 +16,9 @@ Also measured in the same run:
 
 Prints ONE JSON line; `value` is ms per call (lower is better).  The
 roofline object covers the dominant kernel (fused exact + compensation +
-merge), timed with HIP events on the stream it runs on.  cpu_baseline times
+merge): its average duration inside a call, from HIP events recorded around
+each launch on the stream it runs on, over a second pass of the same calls
+right after the timed region.  cpu_baseline times
 the CPU oracle on a bounded sample of the headline call.
 """
 import argparse
@@ -113,13 +115,20 @@ def main():
 
     vrep_call = ws.tensor('call_rep_values', (H, P, 4, D), dev, torch.bfloat16)
 
-    def step():
+    def step(marks=None):
         # own page of block t is P-72+t (the kernel's default when own is None); the router also writes the
-        # call's rep value rows, which the attention kernel reads
+        # call's rep value rows, which the attention kernel reads.  `marks`: three events recorded on the
+        # stream before the router, between the two kernels and after the attention kernel
+        if marks:
+            marks[0].record(stream)
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_basis=basis,
                              rep_out=vrep_call)
-        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, precise_av=args.precise_av,
-                         rep_values=vrep_call)
+        if marks:
+            marks[1].record(stream)
+        o = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, precise_av=args.precise_av, rep_values=vrep_call)
+        if marks:
+            marks[2].record(stream)
+        return o
 
     for _ in range(args.warmup):
         step()
@@ -133,6 +142,14 @@ def main():
     end.record(stream)
     torch.cuda.synchronize()
     ms_call = start.elapsed_time(end) / args.steps
+    # the same calls again with HIP events around each kernel (kept out of the timed region, whose calls
+    # they would space out by a few microseconds): the kernels' average durations inside a call
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(marks[i])
+    torch.cuda.synchronize()
+    route_in_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
+    attn_in_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
 
     # per-kernel timings (same stream, same inputs)
     ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
@@ -183,8 +200,8 @@ def main():
     exact_flop = 4.0 * N * H * D * 64 * C
     comp_flop = 2.0 * N * H * D * 4 * P + 2.0 * N * H * P * D + 6.0 * N * H * P * 8 + 2.0 * N * H * 8 * D
     gather_bytes = H * (N // 64) * C * 64 * D * 2 * 2
-    achieved_tflops = (exact_flop + comp_flop) / (attn_ms * 1e-3) / 1e12
-    gather_gbs = gather_bytes / (attn_ms * 1e-3) / 1e9
+    achieved_tflops = (exact_flop + comp_flop) / (attn_in_ms * 1e-3) / 1e12
+    gather_gbs = gather_bytes / (attn_in_ms * 1e-3) / 1e9
 
     # HBM bytes per attn_kernel launch (rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors from a copy
     # kernel), known for the default workload only
@@ -211,16 +228,17 @@ def main():
                                f"per 64-query block, 12 heads x 4608 queries x d128, route + attention",
                    "pages": P, "exact_pages": C, "heads": H, "queries": N, "head_dim": D,
                    "precise_av": bool(args.precise_av)},
-        "breakdown_ms": {"route_and_rep_values": round(route_ms, 4), "attention_kernel": round(attn_ms, 4)},
+        "breakdown_ms": {"route_and_rep_values": round(route_in_ms, 4), "attention_kernel": round(attn_in_ms, 4),
+                         "route_back_to_back": round(route_ms, 4), "attention_back_to_back": round(attn_ms, 4)},
         "dense_sdpa_ms": None if dense_ms is None else round(dense_ms, 4),
         "ratio_vs_dense": None if dense_ms is None else round(ms_call / dense_ms, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "kernel": "attn_kernel (exact + compensation + merge)",
                      "algorithmic_gflop": round((exact_flop + comp_flop) / 1e9, 2),
-                     "hbm_GBps": None if traffic is None else round(traffic / (attn_ms * 1e-3) / 1e9, 1),
+                     "hbm_GBps": None if traffic is None else round(traffic / (attn_in_ms * 1e-3) / 1e9, 1),
                      "hbm_frac_of_peak": None if traffic is None else
-                     round(traffic / (attn_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     round(traffic / (attn_in_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                      "page_gather_gb": round(gather_bytes / 1e9, 3),
                      "page_gather_GBps_from_l2": round(gather_gbs, 1)},
         "extra": extra,
