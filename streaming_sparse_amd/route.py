@@ -62,14 +62,16 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
     t = nq // 64
     p = summary.mean.shape[1]
     hp = _check_summary(summary, h, p)
+    if tier not in MODES:
+        raise ValueError(f"unknown tier {tier!r}")
+    if tier == 'intersection' and (current_slots is None or n is None):
+        raise ValueError("intersection tier needs current_slots and n")
     mode = MODES[tier]
     count = tier_count(tier, p, n)
     dev = q.device
     cur = None
     total = 0
     if tier == 'intersection':
-        if current_slots is None or n is None:
-            raise ValueError("intersection tier needs current_slots and n")
         cur = torch.as_tensor(current_slots, device=dev).to(torch.int32).contiguous()
         if cur.shape != (h,):
             raise ValueError("current_slots must be [H]")

@@ -1,0 +1,143 @@
+"""Host-side logic on the CPU: tier page counts, the Python wrappers' argument
+checks, K/V stride detection, summary slab slicing, and the C ABI's own
+argument checks (every rejected call returns hipErrorInvalidValue before any
+HIP call, so these run without a GPU)."""
+import os
+
+import pytest
+import torch
+
+from streaming_sparse_amd import _lib, workload
+from streaming_sparse_amd.attention import Workspace
+from streaming_sparse_amd.legacy_components import attention, kv_strides
+from streaming_sparse_amd.ops import Summary
+from streaming_sparse_amd.route import route, tier_count
+
+INVALID = 1   # hipErrorInvalidValue
+H, D = 2, 128
+
+
+def summary_slab(pages, cap=None):
+    cap = cap or pages
+    s = Summary(torch.zeros(H, cap, 4, D, dtype=torch.bfloat16), torch.zeros(H, cap, D, dtype=torch.bfloat16),
+                torch.zeros(H, cap, 3, 8, dtype=torch.bfloat16), torch.zeros(H, cap, 4, 12, dtype=torch.bfloat16))
+    return s.slice(0, pages)
+
+
+def test_tier_counts():
+    """Page counts of the reference tiers: floor(0.15 P) (VR/runtime.py:279-288),
+    24 + n (VB/graph.py:210), max(1, floor(0.1 P)) (RV/ops.py:113-138)."""
+    assert [tier_count('base', p) for p in (216, 288, 432, 504)] == [32, 43, 64, 75]
+    assert tier_count('intersection', 432, 40) == 64
+    assert [tier_count('topk', p) for p in (5, 216, 432)] == [1, 21, 43]
+    with pytest.raises(ValueError):
+        tier_count('dense', 432)
+
+
+def test_summary_slice_keeps_slab_head_stride():
+    s = summary_slab(100, cap=128)
+    assert s.pages == 100 and s.head_pages == 128
+
+
+def test_kv_strides_token_and_head_major():
+    L = 64 * 3
+    k = torch.zeros(1, L, H, D, dtype=torch.bfloat16)
+    assert kv_strides(k, k.clone()) == (H * D, D)
+    hm = torch.zeros(H, L, D, dtype=torch.bfloat16)
+    kh = hm.transpose(0, 1)[None]
+    assert kv_strides(kh, hm.clone().transpose(0, 1)[None]) == (D, L * D)
+    with pytest.raises(ValueError):
+        kv_strides(k[:, ::2], k[:, ::2])
+
+
+def test_route_rejects_bad_arguments():
+    s = summary_slab(216)
+    q = torch.zeros(1, 128, H, D, dtype=torch.bfloat16)
+    theta = torch.ones(H, 4)
+    with pytest.raises(ValueError):
+        route(q.float(), s, theta)                                   # q must be bf16
+    with pytest.raises(ValueError):
+        route(q[:, :, :, :64], s, theta)                              # head dim 128
+    with pytest.raises(ValueError):
+        route(q, s, theta, tier='intersection')                       # needs current_slots and n
+    with pytest.raises(ValueError):
+        route(q, summary_slab(72), theta, tier='base')                # base tier needs a history window
+    with pytest.raises(ValueError):
+        route(q, s, theta, rep_out=torch.zeros(H, 216, 4, D, dtype=torch.bfloat16))   # rep_out needs rep_basis
+    with pytest.raises(ValueError):
+        route(q, s, theta, full_pset=[0])                             # Full_Pset only on the intersection tier
+    with pytest.raises(ValueError):
+        route(q, s, theta, lse_out=torch.zeros(H, 2, 8))              # lse_out shape
+
+
+def test_attention_rejects_bad_arguments():
+    p = 20
+    s = summary_slab(p)
+    q = torch.zeros(1, 128, H, D, dtype=torch.bfloat16)
+    k = torch.zeros(1, 64 * p, H, D, dtype=torch.bfloat16)
+    ids = torch.zeros(H, 2, 3, dtype=torch.int32)
+    basis = torch.zeros(H, D, 8)
+    ws = Workspace()
+    with pytest.raises(ValueError):
+        attention(q.transpose(1, 2).contiguous().transpose(1, 2), k, k, s, basis, ids, ws)   # q not contiguous
+    with pytest.raises(ValueError):
+        attention(q, k, k.float(), s, basis, ids, ws)                 # v must be bf16 like k
+    with pytest.raises(ValueError):
+        attention(q, k, k, s, basis, ids.long(), ws)                  # ids int32
+    with pytest.raises(ValueError):
+        attention(q, k, k, s, basis, ids[:, :1], ws)                  # ids [H, N/64, C]
+    with pytest.raises((TypeError, ValueError)):
+        bad = Summary(s.keys.float(), s.mean, s.detail, s.stats)
+        attention(q, k, k, bad, basis, ids, ws)                       # summaries are bf16
+
+
+def test_quota_tables_keep_totals():
+    """Seeded A/B tables: A + B constant over heads at every (step, layer)
+    (VB/quota_counts.py:1-13)."""
+    tab = workload.quota_table(2)
+    tot = tab.sum(-1)
+    assert bool((tot == tot[..., :1]).all()) and bool((tab[..., 0] >= 1).all())
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libssattn.so not built")
+def test_c_abi_rejects_bad_shapes():
+    L = _lib.lib()
+    N = None
+    # ssa_attention: queries a multiple of 64, pages <= 512, count <= pages, K/V rows of 128 elements
+    att = lambda n, pages, count, tok: L.ssa_attention(N, N, N, N, N, N, N, n, 12, pages, pages, pages, count, tok,
+                                                       128, 0, N)
+    assert att(65, 432, 64, 1536) == INVALID
+    assert att(4608, 513, 64, 1536) == INVALID
+    assert att(4608, 432, 433, 1536) == INVALID
+    assert att(4608, 432, 64, 64) == INVALID
+    # ssa_route: pages in (0, 512], modes -1..2, base count >= 25, quota count = 24 + total,
+    # rep-value pointers 16-byte aligned
+    rt = lambda pages, count, mode, total, cur=None, rv=None, mean=None: L.ssa_route(
+        N, 128, 64 * 12 * 128, 12 * 128, 0, N, N, N, cur, N, N, N, N, N, 12, 72, pages, pages, count, mode, total,
+        mean, mean, mean, rv, pages, N)
+    assert rt(0, 64, 0, 0) == INVALID
+    assert rt(513, 64, 0, 0) == INVALID
+    assert rt(432, 64, 3, 0) == INVALID
+    assert rt(432, 24, 0, 0) == INVALID
+    assert rt(72, 64, 0, 0) == INVALID
+    assert rt(432, 60, 1, 40, cur=8) == INVALID
+    assert rt(432, 64, 1, 40) == INVALID                              # no current quotas
+    assert rt(432, 64, 0, 0, rv=16, mean=None) == INVALID            # rep values without mean/detail/basis
+    assert rt(432, 64, 0, 0, rv=16, mean=8) == INVALID               # misaligned
+    # ssa_summary: page range inside the slab, iters >= 1
+    sm = lambda first, pages, iters, init: L.ssa_summary(N, N, 1536, 128, init, N, N, N, N, N, 432, 12, first, pages,
+                                                         iters, N)
+    assert sm(400, 72, 4, 16) == INVALID
+    assert sm(360, 72, 0, 16) == INVALID
+    assert sm(360, 72, 4, None) == INVALID
+    # ssa_encode: hidden width <= 256, page range inside both slabs
+    en = lambda pages, hidden: L.ssa_encode(N, N, N, N, 432, N, N, N, N, N, N, N, N, N, N, N, 432, 12, 360, pages,
+                                            hidden, N)
+    assert en(73, 256) == INVALID
+    assert en(72, 257) == INVALID
+    # ssa_pset: 96 < pages <= 512 and at least 64 unselected pages
+    ps = lambda pages, count: L.ssa_pset(N, 128, 64 * 12 * 128, 12 * 128, 0, N, pages, N, N, N, pages, N, N, N, N,
+                                         N, N, N, 3, N, N, N, N, N, N, N, 12, 72, pages, count, N)
+    assert ps(96, 40) == INVALID
+    assert ps(432, 400) == INVALID
+    assert L.ssa_rep_values(N, N, N, N, 0, 432, 432, 432, N) == INVALID
