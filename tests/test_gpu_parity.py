@@ -242,6 +242,46 @@ def test_attention_config1_tiles(device):
     check_out(out[:, rows], want[:, rows], "config1 tiles")
 
 
+def test_full_call_properties(device):
+    """Size-independent properties of the whole base call at its full size
+    (432 pages, 12 heads, 4608 queries), where the oracle would take minutes:
+    - two calls on the same inputs give bit-identical risk, page tables, rep
+      value rows and outputs (no atomics or order-dependent reductions);
+    - scaling V, the page V means and the V details by 2 scales every rep
+      value and every output by exactly 2 (the compensated and exact parts are
+      linear in V, and a power of two commutes with every rounding);
+    - reversing the order of each row's pages after its own page changes the
+      output only by the online softmax's rounding, well inside the parity bar."""
+    x = call_inputs(1, 18)
+    g = x.to(device)
+    basis = g.basis.to(torch.bfloat16).contiguous()
+    ws = Workspace()
+
+    def call(v, s):
+        vrep = torch.empty(12, x.pages, 4, 128, device=device, dtype=torch.bfloat16)
+        ids, _, risk, _ = route(g.q, s, g.theta, tier='base', own=g.own, workspace=ws, rep_basis=basis, rep_out=vrep)
+        out = attention(g.q, g.k, v, s, basis, ids, ws, rep_values=vrep).clone()
+        return ids.clone(), risk.clone(), vrep, out
+
+    ids, risk, vrep, out = call(g.v, g.summary)
+    ids2, risk2, vrep2, out2 = call(g.v, g.summary)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids2) and torch.equal(risk, risk2)
+    assert torch.equal(vrep, vrep2) and torch.equal(out, out2)
+    assert ids.shape == (12, 72, 64) and bool(torch.isfinite(out.float()).all())
+
+    s2 = Summary(g.summary.keys, g.summary.mean * 2, g.summary.detail * 2, g.summary.stats)
+    ids3, risk3, vrep3, out3 = call(g.v * 2, s2)
+    torch.cuda.synchronize()
+    assert torch.equal(ids3, ids) and torch.equal(risk3, risk)
+    assert torch.equal(vrep3, vrep * 2) and torch.equal(out3, out * 2)
+
+    rev = torch.cat([ids[..., :1], ids[..., 1:].flip(-1)], -1).contiguous()
+    out4 = attention(g.q, g.k, g.v, g.summary, basis, rev, ws, rep_values=vrep).clone()
+    torch.cuda.synchronize()
+    check_out(out4, out.cpu(), "reversed page order")
+
+
 def test_route_and_attention_largest_window(device):
     """504 pages (21 frames), the largest window of whole frames under the
     512-page limit: the router's waves hold 15 or 16 tiles, the attention
