@@ -333,19 +333,6 @@ struct RowsSmem {
   double part[4][32][kRowPart];
 };
 
-__device__ __forceinline__ void rep_tile(const uint16_t* rkh, int tile, int P, int lane, const u32x4 (&qop)[8],
-                                         f32x16& S) {
-  const int hh = lane >> 5;
-  const int row = min(tile * 32 + (lane & 31), P * 4 - 1);
-  const uint16_t* a = rkh + (long long)row * kHeadDim + 64 * hh;
-  u32x4 av[8];
-#pragma unroll
-  for (int st = 0; st < 8; ++st) av[st] = ldg16(a + 8 * st);
-  S = f32x16{};
-#pragma unroll
-  for (int st = 0; st < 8; ++st) S = mfma32(av[st], qop[st], S);
-}
-
 // One workgroup per (scoped head, pair of blocks, page range): per probe
 // and page, the log mass lm = LSE_r z - LSE z, the readout (rp, beta), the
 // summary approximation, then partial mixture sums; candidate pages write
@@ -426,36 +413,50 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
   const long long row_id = ((long long)hs * p.T + tq) * 16 + m;
   float* cw = &s.coef[wave][0][0];
   double* mw = &s.md[wave][0][0];
+  // A tile's inputs (the 8 pages' coefficients and meanB | detailB, and its
+  // 32 rep keys) are loaded into registers one tile ahead: the loads of the
+  // wave's next tile are in flight while this tile's pages are computed.
+  u32x4 fa, fb, fm[4], fk[8];
+  auto fetch = [&](int tile) {
+    const int pl = lane >> 3, c = lane & 7;
+    const int page = min(tile * 8 + pl, P - 1);
+    const uint16_t* cf = p.coef + ((long long)h * p.EP + page) * kCoefStride + 16 * c;
+    const double* src = c < 2 ? p.mean_b + ((long long)h * p.EP + page) * 16 + 8 * c
+                               : p.detail_b + ((long long)h * p.EP + page) * 48 + 8 * (c - 2);
+    fa = ldg16(cf);
+    fb = ldg16(cf + 8);
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) fm[k] = s4[k];
+    const int row = min(tile * 32 + (lane & 31), P * 4 - 1);
+    const uint16_t* a = rkh + (long long)row * kHeadDim + 64 * hh;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) fk[st] = ldg16(a + 8 * st);
+  };
+  if (tile0 + wave < tile1) fetch(tile0 + wave);
   for (int tile = tile0 + wave; tile < tile1; tile += 4) {
     // stage this tile's 8 pages: coefficients (bf16 -> fp32) and meanB | detailB
     {
       const int pl = lane >> 3, c = lane & 7;
-      const int page = min(tile * 8 + pl, P - 1);
-      const uint16_t* cf = p.coef + ((long long)h * p.EP + page) * kCoefStride + 16 * c;
-      const double* src = c < 2 ? p.mean_b + ((long long)h * p.EP + page) * 16 + 8 * c
-                                 : p.detail_b + ((long long)h * p.EP + page) * 48 + 8 * (c - 2);
-      const u32x4 a = ldg16(cf), b = ldg16(cf + 8);
-      const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
-      const u32x4 m0 = s4[0], m1 = s4[1], m2 = s4[2], m3 = s4[3];
       float* d = cw + pl * 128 + 16 * c;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        d[2 * k] = bf16_lo(a[k]);
-        d[2 * k + 1] = bf16_hi(a[k]);
-        d[8 + 2 * k] = bf16_lo(b[k]);
-        d[8 + 2 * k + 1] = bf16_hi(b[k]);
+        d[2 * k] = bf16_lo(fa[k]);
+        d[2 * k + 1] = bf16_hi(fa[k]);
+        d[8 + 2 * k] = bf16_lo(fb[k]);
+        d[8 + 2 * k + 1] = bf16_hi(fb[k]);
       }
       u32x4* md = reinterpret_cast<u32x4*>(mw + pl * 64 + 8 * c);
-      md[0] = m0;
-      md[1] = m1;
-      md[2] = m2;
-      md[3] = m3;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) md[k] = fm[k];
     }
+    f32x16 S = {};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) S = mfma32(fk[st], qop[st], S);
+    if (tile + 4 < tile1) fetch(tile + 4);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    f32x16 S;
-    rep_tile(rkh, tile, P, lane, qop, S);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int pl = 2 * j + hh;
@@ -577,6 +578,7 @@ struct ScoreSmem {
   alignas(16) double part[4][kSplit * kRowPart];   // the probe's split row partials
   uint32_t legal[16];
   int page[kMaxPages];                   // pool pages, then the compacted selection
+  unsigned long long key[kMaxPages];     // LUT keys of the compacted selection
   float risk[kMaxPages];
   uint8_t sel[kMaxPages];
   double best[4];
@@ -605,33 +607,36 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
     s.sel[i] = p.mask[r] ? 1 : 0;
   }
   for (int i = lane; i < 512; i += 64) s.acc[w][i] = 0.0;
-  for (int m = w; m < 16; m += 4) {
-    // stage the probe's candidates and row state
-    {
-      // 48 x 34 doubles = 816 16-byte chunks: all loads in flight, then stores
-      const u32x4* cd = reinterpret_cast<const u32x4*>(p.cand + (rowbase * 16 + m) * kCand * kCandVals);
-      u32x4 v[13];
+  // A probe's candidates (48 x 34 doubles = 816 16-byte chunks) and split row
+  // partials (kSplit x 52 doubles) are loaded one probe ahead: the loads of
+  // probe m + 4 are in flight while probe m is scored.
+  constexpr int kChunks = kSplit * kRowPart / 2;
+  constexpr int kRowLoads = (kChunks + 63) / 64;
+  u32x4 v[13], r[kRowLoads];
+  auto load_probe = [&](int m) {
+    const u32x4* cd = reinterpret_cast<const u32x4*>(p.cand + (rowbase * 16 + m) * kCand * kCandVals);
 #pragma unroll
-      for (int k = 0; k < 13; ++k) v[k] = cd[min(lane + 64 * k, 815)];
+    for (int k = 0; k < 13; ++k) v[k] = cd[min(lane + 64 * k, 815)];
+    const u32x4* rs = reinterpret_cast<const u32x4*>(p.rows + (rowbase * 16 + m) * kSplit * kRowPart);
+#pragma unroll
+    for (int k = 0; k < kRowLoads; ++k) r[k] = rs[min(64 * k + lane, kChunks - 1)];
+  };
+  load_probe(w);
+  for (int m = w; m < 16; m += 4) {
+    // stage the probe's candidates and row state, then request the next probe's
+    {
       u32x4* dst = reinterpret_cast<u32x4*>(&s.cand[w][0][0]);
 #pragma unroll
       for (int k = 0; k < 13; ++k) {
         const int c = lane + 64 * k;
         if (c < 816) dst[c] = v[k];
       }
-    }
-    {
-      // kSplit x 52 doubles in 16-byte chunks
-      constexpr int kChunks = kSplit * kRowPart / 2;
-      const u32x4* rs = reinterpret_cast<const u32x4*>(p.rows + (rowbase * 16 + m) * kSplit * kRowPart);
-      u32x4 r[(kChunks + 63) / 64];
+      u32x4* pd = reinterpret_cast<u32x4*>(s.part[w]);
 #pragma unroll
-      for (int k = 0; k < (kChunks + 63) / 64; ++k) r[k] = rs[min(64 * k + lane, kChunks - 1)];
-      u32x4* dst = reinterpret_cast<u32x4*>(s.part[w]);
-#pragma unroll
-      for (int k = 0; k < (kChunks + 63) / 64; ++k)
-        if (64 * k + lane < kChunks) dst[64 * k + lane] = r[k];
+      for (int k = 0; k < kRowLoads; ++k)
+        if (64 * k + lane < kChunks) pd[64 * k + lane] = r[k];
     }
+    if (m + 4 < 16) load_probe(m + 4);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -818,17 +823,19 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
   }
   __syncthreads();
   const int nsel = s.besti[0];
-  if (tid == 0) ids[0] = own;
+  // key (orderable risk, 1023 - page): a higher key ranks first, ties go to
+  // the lower page; a page's slot is the count of listed keys above its own
   for (int i = tid; i < nsel; i += 256) {
     const int x = s.page[i];
-    const uint32_t kx = orderable(s.risk[x]);
+    s.key[i] = ((unsigned long long)orderable(s.risk[x]) << 32) | (uint32_t)(1023 - x);
+  }
+  __syncthreads();
+  if (tid == 0) ids[0] = own;
+  for (int i = tid; i < nsel; i += 256) {
+    const unsigned long long kx = s.key[i];
     int rank = 0;
-    for (int k = 0; k < nsel; ++k) {
-      const int y = s.page[k];
-      const uint32_t ky = orderable(s.risk[y]);
-      rank += (ky > kx) || (ky == kx && y < x);
-    }
-    if (1 + rank < p.C) ids[1 + rank] = x;
+    for (int k = 0; k < nsel; ++k) rank += s.key[k] > kx;
+    if (1 + rank < p.C) ids[1 + rank] = s.page[i];
   }
 }
 
