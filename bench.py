@@ -4,22 +4,28 @@ Headline workload: the full-window base tier, 12 heads x 4608 queries x d128
 bf16 against a 432-page (27648-token) window with 64 exact pages per 64-query
 block (24 anchors + own + 39 by risk) and every other page compensated from
 its summary.  One step = route + rep values + fused attention over one call's
-inputs, all resident in HBM.
+inputs, all resident in HBM, in the arithmetic a drop-in caller gets by
+default: the reference's two-term bf16 P.V (--single-av: one bf16 product).
 
 Also measured in the same run:
+* the same call in the other P.V arithmetic, and the 216-page window (base
+  tier, 32 exact pages) in both;
 * the intersection tier: 24 anchors + A current + B history pages per head,
   (A, B) from a seeded per-(step, layer, head) quota table;
 * the same with the Full_Pset swap correction on heads {3, 4, 9}, plus what a
   denoise step refreshes first: the summaries (4-iteration k-means) and the
   encodings of the 72 current pages x 12 heads;
-* torch's dense scaled_dot_product_attention over the whole window.
+* dense attention over the whole window: torch's scaled_dot_product_attention
+  and this library's kernel with every page exact;
+* a chunk of the 30-layer streaming workload (rolling window runtime).
 
 Prints ONE JSON line; `value` is ms per call (lower is better).  The
 roofline object covers the dominant kernel (fused exact + compensation +
 merge): its average duration inside a call, from HIP events recorded around
 each launch on the stream it runs on, over a second pass of the same calls
-right after the timed region.  cpu_baseline times
-the CPU oracle on a bounded sample of the headline call.
+right after the timed region.  cpu_baseline times the CPU oracle on a
+bounded sample of the headline call; extra.cpu_baseline_other_configs the
+same for the 216-page call, the intersection call and the Full_Pset call.
 """
 import argparse
 import json
@@ -30,10 +36,10 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-# HBM bytes per attn_kernel launch of the base-tier call, keyed by (pages, exact pages), measured with
-# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this bench (profiles/attn_kernel_base432_traffic.md):
-# 116.4 MB read + 14.2 MB written
-MEASURED_TRAFFIC = {(432, 64): 130.6e6}
+# HBM bytes per attn_kernel launch of the base-tier call, keyed by (pages, exact pages, single-term P.V),
+# measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this bench (profiles/attn_kernel_base432_traffic.md):
+# two-term 129.6 MB read + 14.2 MB written, single-term 116.5 MB read + 14.2 MB written
+MEASURED_TRAFFIC = {(432, 64, False): 143.8e6, (432, 64, True): 130.6e6}
 METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
@@ -48,12 +54,15 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--frames", type=int, default=18, help="window frames (18 -> 432 pages)")
-    ap.add_argument("--precise-av", action="store_true")
+    ap.add_argument("--single-av", action="store_true",
+                    help="headline in single-term bf16 P.V (default: the reference's two-term product)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the intersection / Full_Pset lines")
     ap.add_argument("--no-chunk", action="store_true", help="skip the per-chunk 30-layer line")
     ap.add_argument("--cpu-sample-blocks", type=int, default=4)
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the headline call (for a profiler run whose kernel averages are the headline's)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (scales rocprof FETCH/WRITE_SIZE)")
     return ap.parse_args()
@@ -71,6 +80,11 @@ def calibrate_copy(mib):
     print(json.dumps({"calibration_copy_bytes": src.numel(), "copies": 3}), flush=True)
 
 
+def log(msg):
+    """Progress line on stderr (the JSON line is the only stdout output)."""
+    print(f"# {time.strftime('%H:%M:%S')} {msg}", file=sys.stderr, flush=True)
+
+
 def time_loop(fn, iters, stream):
     """Average ms of `fn` over `iters` back-to-back launches, HIP events on
     the stream the work is enqueued on."""
@@ -85,6 +99,63 @@ def time_loop(fn, iters, stream):
     return a.elapsed_time(b) / iters
 
 
+def call_timings(g, P, C, single, steps, warmup, stream):
+    """One base-tier call (route + attention) timed over `steps` calls after
+    `warmup`, then the kernels' average durations inside a call from HIP events
+    recorded around each launch on its stream (a second pass of the same
+    calls, kept out of the timed region whose calls they would space out)."""
+    import torch
+    from streaming_sparse_amd.attention import Workspace
+    from streaming_sparse_amd.legacy_components import attention
+    from streaming_sparse_amd.route import route
+    dev = g.q.device
+    H, D = 12, 128
+    ws = Workspace()
+    basis = g.basis.to(torch.bfloat16).contiguous()   # the caller keeps the basis bf16-rounded
+    vrep = ws.tensor('call_rep_values', (H, P, 4, D), dev, torch.bfloat16)
+
+    def step(marks=None):
+        # own page of block t is P-72+t (the router's default when own is None); the router also writes
+        # the call's rep value rows, which the attention kernel reads
+        if marks:
+            marks[0].record(stream)
+        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_basis=basis,
+                             rep_out=vrep)
+        if marks:
+            marks[1].record(stream)
+        o = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, single_av=single, rep_values=vrep)
+        if marks:
+            marks[2].record(stream)
+        return o
+
+    for _ in range(warmup):
+        step()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_call = start.elapsed_time(end) / steps
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for i in range(steps):
+        step(marks[i])
+    torch.cuda.synchronize()
+    route_in = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
+    attn_in = sum(m[1].elapsed_time(m[2]) for m in marks) / steps
+    return ms_call, route_in, attn_in
+
+
+def attn_flop(N, H, D, C, P):
+    """Algorithmic FLOP of the fused kernel: exact QK + PV over C pages, and the
+    compensation (rep QK, mean PV, detail PV, rank-8 projection)."""
+    exact = 4.0 * N * H * D * 64 * C
+    comp = 2.0 * N * H * D * 4 * P + 2.0 * N * H * P * D + 6.0 * N * H * P * 8 + 2.0 * N * H * 8 * D
+    return exact, comp
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -95,7 +166,7 @@ def main():
         calibrate_copy(args.calibrate_copy)
         return
     import torch
-    from streaming_sparse_amd import _lib, pset, workload
+    from streaming_sparse_amd import _lib, workload
     from streaming_sparse_amd.attention import Workspace
     from streaming_sparse_amd.legacy_components import attention, rep_values, kv_strides
     from streaming_sparse_amd.route import route
@@ -109,68 +180,38 @@ def main():
     P = x.pages
     H, N, D = 12, 4608, 128
     C = P * 15 // 100
-    ws = Workspace()
     stream = torch.cuda.current_stream(dev)
-    basis = g.basis.to(torch.bfloat16).contiguous()   # the caller keeps the basis bf16-rounded
+    single = bool(args.single_av)
+    print(f"# headline: base tier P={P} C={C} single_av={single}", file=sys.stderr, flush=True)
+    ms_call, route_in_ms, attn_in_ms = call_timings(g, P, C, single, args.steps, args.warmup, stream)
+    log(f"headline call {ms_call:.4f} ms (attention kernel {attn_in_ms:.4f} ms)")
+    if args.headline_only:
+        print(json.dumps({"metric": METRIC, "value": round(ms_call, 4), "unit": "ms", "headline_only": True,
+                          "attention_kernel_ms": round(attn_in_ms, 4), "route_ms": round(route_in_ms, 4),
+                          "single_av": single}), flush=True)
+        return
 
-    vrep_call = ws.tensor('call_rep_values', (H, P, 4, D), dev, torch.bfloat16)
-
-    def step(marks=None):
-        # own page of block t is P-72+t (the kernel's default when own is None); the router also writes the
-        # call's rep value rows, which the attention kernel reads.  `marks`: three events recorded on the
-        # stream before the router, between the two kernels and after the attention kernel
-        if marks:
-            marks[0].record(stream)
-        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_basis=basis,
-                             rep_out=vrep_call)
-        if marks:
-            marks[1].record(stream)
-        o = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, precise_av=args.precise_av, rep_values=vrep_call)
-        if marks:
-            marks[2].record(stream)
-        return o
-
-    for _ in range(args.warmup):
-        step()
-    # timed region: exactly `steps` calls, synchronized on both sides
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(args.steps):
-        out = step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms_call = start.elapsed_time(end) / args.steps
-    # the same calls again with HIP events around each kernel (kept out of the timed region, whose calls
-    # they would space out by a few microseconds): the kernels' average durations inside a call
-    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        step(marks[i])
-    torch.cuda.synchronize()
-    route_in_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
-    attn_in_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
-
-    # per-kernel timings (same stream, same inputs)
+    # per-kernel timings back to back (same stream, same inputs), straight through the C ABI
+    ws = Workspace()
+    basis = g.basis.to(torch.bfloat16).contiguous()
     ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
     vrep = ws.tensor('ssa_rep_values', (H, P, 4, D), dev, torch.bfloat16)
     rep_values(g.summary, basis, P, vrep)
+    out = torch.empty_like(g.q)
     tok, head = kv_strides(g.k, g.v)
     L = _lib.lib()
-    flags = 1 if args.precise_av else 0
 
-    def attn_only():
+    def attn_only(flags):
         _lib.check(L.ssa_attention(_lib.ptr(g.q), _lib.ptr(g.k), _lib.ptr(g.v), _lib.ptr(g.summary.keys),
                                    _lib.ptr(vrep), _lib.ptr(ids), _lib.ptr(out), N, H, P,
                                    g.summary.head_pages, P, C, tok, head, flags, _lib.stream_handle(dev)),
                    "ssa_attention")
 
     iters = max(10, args.steps)
-    attn_ms = time_loop(attn_only, iters, stream)
-    # the router kernel alone (straight through the C ABI: back-to-back calls of the Python wrapper would
-    # time the host, not the kernel)
-    rids, _, rrisk, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False,
-                              rep_basis=basis, rep_out=vrep_call)
+    attn_ms = {name: time_loop(lambda f=f: attn_only(f), iters, stream) for name, f in (("two_term", 1),
+                                                                                       ("single_term", 0))}
+    rids, _, rrisk, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
+    vrep_call = torch.empty(H, P, 4, D, device=dev, dtype=torch.bfloat16)
     theta32 = g.theta.float().contiguous()
 
     def route_only():
@@ -181,8 +222,10 @@ def main():
                                _lib.ptr(vrep_call), P, _lib.stream_handle(dev)), "ssa_route")
 
     route_ms = time_loop(route_only, iters, stream)
+    log(f"kernels back to back: attention {attn_ms}, route {route_ms:.4f} ms")
 
     dense_ms = None
+    dense_own = {}
     if not args.no_dense:
         qd = g.q[0].transpose(0, 1)[None]
         kd = g.k[0].transpose(0, 1)[None]
@@ -191,25 +234,62 @@ def main():
         for _ in range(3):
             dense()
         dense_ms = time_loop(dense, max(5, iters // 5), stream)
+        # this library's kernel with every page exact (the dense layers' call)
+        own = torch.arange(N // 64, device=dev) + P - N // 64
+        allp = torch.arange(P, device=dev)
+        dids = torch.cat([own[:, None], allp[None].expand(N // 64, -1)], 1)
+        keep = dids != own[:, None]
+        keep[:, 0] = True
+        dids = dids[keep].reshape(N // 64, P)[None].expand(H, -1, -1).to(torch.int32).contiguous()
+        for name, sgl in (("two_term", False), ("single_term", True)):
+            fn = lambda s=sgl: attention(g.q, g.k, g.v, g.summary, basis, dids, ws, single_av=s, all_pages=True)
+            for _ in range(3):
+                fn()
+            dense_own[name] = time_loop(fn, max(5, iters // 5), stream)
 
-    extra = None if args.no_extra else intersection_lines(args, dense_ms, iters)
-    if extra is not None and not args.no_chunk:
-        extra["chunk"] = chunk_line(args)
+    # the same call in the other arithmetic, and the 216-page window (config 0)
+    other = not single
+    log(f"dense: sdpa {dense_ms} ms, this kernel {dense_own}")
+    o_call, o_route_in, o_attn_in = call_timings(g, P, C, other, args.steps, args.warmup // 2, stream)
+    log(f"other arithmetic call {o_call:.4f} ms")
+    x0 = workload.make_call(cfg=0, frames=9)
+    g0 = x0.to(dev)
+    P0, C0 = x0.pages, x0.pages * 15 // 100
+    cfg0 = {}
+    for name, sgl in (("two_term", False), ("single_term", True)):
+        c_ms, c_route, c_attn = call_timings(g0, P0, C0, sgl, args.steps, args.warmup // 2, stream)
+        e0, m0 = attn_flop(N, H, D, C0, P0)
+        cfg0[name] = {"call_ms": round(c_ms, 4), "attention_kernel_ms": round(c_attn, 4),
+                      "route_ms": round(c_route, 4),
+                      "attention_frac_of_bf16_peak": round((e0 + m0) / (c_attn * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    del g0
 
-    # algorithmic work of the fused kernel (exact + compensation), per call
-    exact_flop = 4.0 * N * H * D * 64 * C
-    comp_flop = 2.0 * N * H * D * 4 * P + 2.0 * N * H * P * D + 6.0 * N * H * P * 8 + 2.0 * N * H * 8 * D
+    extra = {"other_arithmetic": {"single_av": other, "call_ms": round(o_call, 4),
+                                  "attention_kernel_ms": round(o_attn_in, 4), "route_ms": round(o_route_in, 4)},
+             "config0_p216_c32": cfg0}
+    if not args.no_extra:
+        extra.update(intersection_lines(args, dense_ms, iters))
+        log("intersection lines done")
+        if not args.no_chunk:
+            extra["chunk"] = chunk_line(args)
+            log(f"chunk line {extra['chunk']}")
+
+    exact_flop, comp_flop = attn_flop(N, H, D, C, P)
     gather_bytes = H * (N // 64) * C * 64 * D * 2 * 2
     achieved_tflops = (exact_flop + comp_flop) / (attn_in_ms * 1e-3) / 1e12
     gather_gbs = gather_bytes / (attn_in_ms * 1e-3) / 1e9
+    o_tflops = (exact_flop + comp_flop) / (o_attn_in * 1e-3) / 1e12
+    extra["other_arithmetic"]["roofline_frac"] = round(o_tflops / PEAK_BF16_TFLOPS, 4)
 
     # HBM bytes per attn_kernel launch (rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, factors from a copy
     # kernel), known for the default workload only
-    traffic = MEASURED_TRAFFIC.get((P, C)) if not args.precise_av else None
+    traffic = MEASURED_TRAFFIC.get((P, C, single))
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(x, C, args.cpu_sample_blocks)
+        cpu = cpu_baseline(x, C, args.cpu_sample_blocks, cfg=1)
+        log(f"cpu baseline config 1: {cpu['value']} ms")
+        extra["cpu_baseline_other_configs"] = cpu_other_configs(args.cpu_sample_blocks)
 
     line = {
         "metric": METRIC,
@@ -225,13 +305,19 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) Q/K/V with RoPE, k-means page summaries)",
         "config": {"workload": f"full-window base tier: P={P} pages ({64 * P} KV tokens), {C} exact pages "
-                               f"per 64-query block, 12 heads x 4608 queries x d128, route + attention",
-                   "pages": P, "exact_pages": C, "heads": H, "queries": N, "head_dim": D,
-                   "precise_av": bool(args.precise_av)},
+                               f"per 64-query block, 12 heads x 4608 queries x d128, route + attention, "
+                               f"{'single-term' if single else 'two-term (reference)'} bf16 P.V",
+                   "tier": "base", "pages": P, "exact_pages": C, "heads": H, "queries": N, "head_dim": D,
+                   "single_av": single},
         "breakdown_ms": {"route_and_rep_values": round(route_in_ms, 4), "attention_kernel": round(attn_in_ms, 4),
-                         "route_back_to_back": round(route_ms, 4), "attention_back_to_back": round(attn_ms, 4)},
+                         "route_back_to_back": round(route_ms, 4),
+                         "attention_back_to_back_two_term": round(attn_ms["two_term"], 4),
+                         "attention_back_to_back_single_term": round(attn_ms["single_term"], 4)},
         "dense_sdpa_ms": None if dense_ms is None else round(dense_ms, 4),
         "ratio_vs_dense": None if dense_ms is None else round(ms_call / dense_ms, 4),
+        "dense_this_kernel_ms": {k: round(v, 4) for k, v in dense_own.items()},
+        "ratio_vs_dense_this_kernel": None if not dense_own else
+        round(ms_call / dense_own["single_term" if single else "two_term"], 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "kernel": "attn_kernel (exact + compensation + merge)",
@@ -277,10 +363,10 @@ def intersection_lines(args, dense_ms, iters):
 
     vrep = ws.tensor('call_rep_values', (12, P, 4, 128), dev, torch.bfloat16)
 
-    def plain():
+    def plain(single=None):
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
                              want_mask=False, rep_basis=basis, rep_out=vrep)
-        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep, single_av=single)
 
     def corrected():
         recompute()
@@ -290,7 +376,8 @@ def intersection_lines(args, dense_ms, iters):
         return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep)
 
     out = {}
-    for name, fn in (("intersection", plain), ("intersection_full_pset", corrected)):
+    for name, fn in (("intersection", plain), ("intersection_single_term", lambda: plain(True)),
+                     ("intersection_full_pset", corrected)):
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
@@ -341,21 +428,56 @@ def chunk_line(args, chunks=2):
             "ratio_vs_dense_sdpa": round(chunk_ms / dense_sdpa_ms, 4), "setup_s": round(setup_s, 2)}
 
 
-def cpu_baseline(x, count, blocks):
-    """CPU oracle on a bounded sample: the router over the whole call (all
-    72 blocks x 12 heads, it is cheap) and the attention over `blocks` query
-    blocks, scaled to a full call (72 blocks)."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_baseline(x, count, blocks, cfg, tier='base', quota=None, pset_heads=None):
+    """CPU oracle on a bounded sample of one call: the router over the whole
+    call (all 72 blocks x 12 heads, it is cheap), the tier's selection, for
+    config 3 the current pages' summaries and encodings and the Full_Pset
+    correction of the scoped heads, and the attention over `blocks` query
+    blocks scaled to the full 72; median of 3 after 1 warm-up."""
     import torch
     from oracle import reference as ref
+    from oracle import pset as opset
+    from oracle import summary as osum
+    from streaming_sparse_amd import workload
     cores = os.cpu_count() or 1
     torch.set_num_threads(cores)
     tiles = list(range(0, 72, max(1, 72 // blocks)))[:blocks]
+    P = x.pages
+    if pset_heads:
+        w = workload.reader_weights()
+        s = x.summary
+        enc = opset.encode(s.keys, s.mean, s.detail, s.stats, x.basis, w)
+        kp = x.k[0].transpose(0, 1).reshape(12, P, 64, 128)[:, P - 72:]
+        vp = x.v[0].transpose(0, 1).reshape(12, P, 64, 128)[:, P - 72:]
+        init = workload.kmeans_init(12, 72, torch.Generator().manual_seed(workload.seed_for(cfg, 3, 0, 9)))
 
     def run():
         t0 = time.perf_counter()
+        if pset_heads:
+            cs = osum.summaries(kp, vp, x.basis, init)
+            opset.encode(cs['keys'], cs['mean'], cs['detail'], cs['stats'], x.basis, w)
         pr = ref.probes(x.q)
-        r = ref.risk(pr, ref.route_logits(pr, x.summary.keys), x.summary.stats, x.theta)
-        ids = ref.select_base(r, x.own, count)
+        z = ref.route_logits(pr, x.summary.keys)
+        r = ref.risk(pr, z, x.summary.stats, x.theta)
+        if tier == 'base':
+            ids = ref.select_base(r, x.own, count)
+        else:
+            a, n = quota
+            mask = ref.quota_mask(r, x.own, a, n)
+            if pset_heads:
+                mask, _, _ = opset.correct(pr, z, r, mask, x.own, enc, w['wq'], list(pset_heads))
+            ids = ref.lut(r, mask, x.own, 24 + n)
         t1 = time.perf_counter()
         ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, ids, tiles=tiles)
         t2 = time.perf_counter()
@@ -365,18 +487,31 @@ def cpu_baseline(x, count, blocks):
     times = sorted((run() for _ in range(3)), key=lambda a: a[0] + a[1])
     route_s, attn_s = times[1]
     total_ms = (route_s + attn_s * 72 / len(tiles)) * 1e3
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    what = {'base': "base-tier route", 'intersection': "intersection route"}[tier]
+    if pset_heads:
+        what = f"current summaries + encodings, intersection route + Full_Pset on heads {list(pset_heads)}"
     return {"value": round(total_ms, 1), "unit": "ms", "cores": cores, "kind": "port",
-            "sample": f"oracle route over the full call + attention over {len(tiles)} of 72 query blocks "
-                      f"(x12 heads), scaled to 72 blocks; median of 3 after 1 warm-up; cpu: {model}"}
+            "sample": f"config {cfg}: oracle {what} over the full call + attention over {len(tiles)} of 72 "
+                      f"query blocks (x12 heads), scaled to 72 blocks; median of 3 after 1 warm-up; "
+                      f"cpu: {_cpu_model()}"}
+
+
+def cpu_other_configs(blocks):
+    """cpu_baseline of configs 0 (216 pages, base), 2 (432 pages,
+    intersection) and 3 (config 2 plus Full_Pset on heads {3,4,9})."""
+    from streaming_sparse_amd import workload
+    out = {}
+    x0 = workload.make_call(cfg=0, frames=9)
+    out["config0"] = cpu_baseline(x0, x0.pages * 15 // 100, blocks, 0)
+    log(f"cpu baseline config 0: {out['config0']['value']} ms")
+    del x0
+    x2 = workload.make_call(cfg=2, frames=18)
+    tab = workload.quota_table(2)
+    quota = (tab[0, 3, :, 0], int(tab[0, 3, 0].sum()))
+    out["config2"] = cpu_baseline(x2, None, blocks, 2, tier='intersection', quota=quota)
+    log(f"cpu baseline config 2: {out['config2']['value']} ms")
+    out["config3"] = cpu_baseline(x2, None, blocks, 3, tier='intersection', quota=quota, pset_heads=PSET_HEADS)
+    return out
 
 
 if __name__ == "__main__":

@@ -53,8 +53,16 @@ int ssa_rep_values(const void* mean, const void* detail, const void* basis, void
  * q, out [1,n_tokens,H,128] bf16 contiguous; k, v: page p, token j, head h at
  * element (64p+j)*kv_token_stride + h*kv_head_stride (+ dim); keys
  * [H,head_pages,4,128] bf16 (rep keys); rep_values from ssa_rep_values;
- * ids [H,n_tokens/64,count] int32 (page ids in [0,pages)).
- * flags bit 0: two-term bf16 P.V (hi + lo parts of each probability). */
+ * ids [H,n_tokens/64,count] int32: page ids, own page first; entries
+ * outside [0,pages) (the -1 padding of a shorter table, RV/ops.py:115) are
+ * not read and select nothing; a page listed twice is attended twice.
+ * flags bit 0: two-term bf16 P.V (hi + lo parts of each probability, the
+ * reference's HIGH_PRECISION_AV / BF16_AV arithmetic,
+ * LE/gap_exact_round_kernel.py:98-125, RV/tuned_attention.py:16-18);
+ * clear: single-term bf16 P.V.
+ * flags bit 1: the caller guarantees every row of ids lists each page of the
+ * window exactly once (count == pages, a dense call); ids are then not read
+ * and two query blocks share each K/V page load. */
 int ssa_attention(const void* q, const void* k, const void* v, const void* keys, const void* rep_values,
                   const int32_t* ids, void* out, int n_tokens, int heads, int pages, int head_pages,
                   int rep_head_pages, int count, long long kv_token_stride, long long kv_head_stride, int flags,
@@ -68,9 +76,19 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
  * keys [H,head_pages,4,128] bf16, stats [H,head_pages,4,12] bf16, theta
  * [H,4] fp32, own [H,blocks] int32 or NULL (own = pages - blocks + t).
  * mode 0: base tier, ids = [own, 0..23, top count-25 by risk];
- * mode 1: anchor/current/history quota, current[h] = A >= 1, total = A+B,
- *         count = 24 + total, ids = own then selected by descending risk;
+ * mode 1: anchor/current/history quota (VB/quota_mask.py:7-39), total = A+B
+ *         <= pages - 24, count = 24 + total: anchors 0..23, the top A of the
+ *         current pages [pages-72, pages) with own forced, the top total-A
+ *         of the history pages [24, pages-72), A = current[h]; each quota is
+ *         clamped to [0, its partition's size] as the reference's _keep
+ *         does (the history one computed from the unclamped A).
+ *         pages == 72 (the anchor frame inside the chunk, VB/graph.py:
+ *         143-148): anchors + the top `total` of pages [24,72), own forced;
+ *         current may be NULL.  Otherwise pages >= 96.  ids = own first
+ *         (also when its quota left it out), then the selected pages by
+ *         descending risk, truncated to count, padded with -1;
  * mode 2: fixed top-count with own forced first.  Ties -> lower page.
+ * own pages outside [0,pages) are clamped into the window.
  * ids [H,blocks,count] int32 and mask [H,blocks,pages] uint8 may be NULL; lse
  * [H,blocks,16] fp32 (NULL to skip) receives each probe's log-sum-exp over
  * all reps of the window (natural log), the input ssa_pset needs.

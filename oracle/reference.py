@@ -54,8 +54,9 @@ def route_logits(pr, keys, dtype=torch.float32):
 
 def risk(pr, z, stats, theta, dtype=torch.float32):
     """Per-page risk [H,T,P]: the four features of RV/ops.py:80-111 in the
-    deployed form VR/risk_online.py:140-149 (row normaliser :151-159, fused
-    reduction :86-122): prob = exp(z-max)/sum exp(z-max) over the P*4 reps of
+    deployed form risk_from_logits (VR/runtime.py:27-40; the fused kernels
+    VR/risk_online.py:24-59 (_risk_tile), :77-86 (risk), row normaliser
+    :88-113): prob = exp(z-max)/sum exp(z-max) over the P*4 reps of
     each probe row, u = max(0, sum_g q2_g*st_g), beta = |q|/sqrt(D)*st_8,
     c = st[p,1,11] + max_p st[p,1,11], value = ((t0 x0 + t1 x1) + t2 x2) + t3 x3,
     mean over the 16 probes."""
@@ -125,34 +126,54 @@ def select_base(risk_, own, count):
     return torch.cat((own[..., None], frame, order), -1).int()
 
 
+def _keep(scores, slots):
+    """_keep (VB/quota_mask.py:7-15) over one partition's rows: the top
+    `slots` scores, ties -> lower index; slots <= 0 keeps nothing, slots >= the
+    partition size keeps all of it.  Returns the kept column indices."""
+    if slots <= 0:
+        return scores[..., :0].long()
+    return scores.sort(dim=-1, descending=True, stable=True).indices[..., :slots]
+
+
 def quota_mask(risk_, own, current, total):
-    """Anchor/history/current partition selection (VB/quota_mask.py:7-39):
+    """Anchor/history/current partition selection (VB/quota_mask.py:17-39):
     pages < 24 always; history [24, P-72) keeps its top (total - A); current
-    [P-72, P) keeps its top A with own forced (+inf); ties -> lower index."""
+    [P-72, P) keeps its top A with own forced (+inf, when own is a current
+    page); ties -> lower index.  A 72-page window, whose first frame is the
+    anchor frame (VB/graph.py:143-148), keeps the anchors and the top `total`
+    of pages [24, 72) with own forced; `current` is then not read."""
     h, t, p = risk_.shape
     mask = torch.zeros(h, t, p, dtype=torch.bool)
     mask[..., :ANCHORS] = True
+    if p == CURRENT:
+        page = torch.arange(p)
+        ranked = risk_.masked_fill(page < ANCHORS, -torch.inf).scatter(-1, own.long()[..., None], torch.inf)
+        mask.scatter_(-1, _keep(ranked[..., ANCHORS:], int(total)) + ANCHORS, True)
+        return mask
     for hh in range(h):
         a = int(current[hh])
-        slots_hist = total - a
         hist = risk_[hh, :, ANCHORS:p - CURRENT]
-        if slots_hist > 0:
-            order = hist.sort(dim=-1, descending=True, stable=True).indices[:, :slots_hist] + ANCHORS
-            mask[hh].scatter_(-1, order, True)
+        mask[hh].scatter_(-1, _keep(hist, int(total) - a) + ANCHORS, True)
         cur = risk_[hh, :, p - CURRENT:].clone()
-        cur.scatter_(-1, (own[hh] - (p - CURRENT))[:, None], torch.inf)
-        if a > 0:
-            order = cur.sort(dim=-1, descending=True, stable=True).indices[:, :a] + (p - CURRENT)
-            mask[hh].scatter_(-1, order, True)
+        rel = own[hh].long() - (p - CURRENT)
+        inside = (rel >= 0) & (rel < CURRENT)
+        cur[inside, rel[inside]] = torch.inf
+        mask[hh].scatter_(-1, _keep(cur, a) + (p - CURRENT), True)
     return mask
 
 
 def lut(risk_, mask, own, count):
     """Final page LUT (VB/graph.py:210): topk(count) of risk masked to the
     selection with own = +inf -> own first, then descending risk (ties -> lower
-    index; torch.topk leaves tie order unspecified)."""
-    ranked = risk_.masked_fill(~mask, -torch.inf).scatter(-1, own[..., None], torch.inf)
-    return ranked.sort(dim=-1, descending=True, stable=True).indices[..., :count].int()
+    index; torch.topk leaves tie order unspecified).  When the selection plus
+    own holds fewer than `count` pages (quotas clamped to their partitions)
+    torch.topk would return arbitrary unselected pages in the remaining slots;
+    they are -1 here (the padding of RV/ops.py:115-135), parity unpinned at
+    that edge."""
+    ranked = risk_.masked_fill(~mask, -torch.inf).scatter(-1, own.long()[..., None], torch.inf)
+    vals, idx = ranked.sort(dim=-1, descending=True, stable=True)
+    idx = idx[..., :count].int()
+    return idx.masked_fill(vals[..., :count] == -torch.inf, -1)
 
 
 def select_topk(risk_, own, count):
@@ -166,9 +187,12 @@ def select_topk(risk_, own, count):
 
 def mask_from_ids(ids, pages):
     """Selected-page set of each (head, block) from its LUT
-    (RV/tuned_attention.py:37-40; LE high_sparse_runtime.py:12-17)."""
+    (RV/tuned_attention.py:37-40; LE high_sparse_runtime.py:12-17); entries
+    outside [0, pages) (padding -1) select nothing."""
     h, t, _ = ids.shape
-    return torch.zeros(h, t, pages, dtype=torch.bool).scatter(-1, ids.long(), True)
+    ok = (ids >= 0) & (ids < pages)
+    col = torch.where(ok, ids.long(), torch.full_like(ids.long(), pages))   # invalid -> a spare column
+    return torch.zeros(h, t, pages + 1, dtype=torch.bool).scatter(-1, col, True)[..., :pages]
 
 
 # ------------------------------------------------------------- attention ----
@@ -198,13 +222,17 @@ def selected_attention(q, k, v, s, basis, ids, dtype=torch.float32, tiles=None):
     for tile in tiles:
         query = query_all[:, tile * 64:(tile + 1) * 64].to(dtype)
         sel = ids[:, tile, :count].long()
-        tokens = (sel[:, :, None] * 64 + offsets).flatten(1)
+        # LUT entries outside [0, P) (padding -1) are not read (RV/ops.py:115)
+        valid = ((sel >= 0) & (sel < p))[:, :, None].expand(-1, -1, 64).flatten(1)
+        tokens = (sel.clamp(0, p - 1)[:, :, None] * 64 + offsets).flatten(1)
         index = tokens[:, :, None].expand(-1, -1, d)
         kk = keys.gather(1, index).to(dtype)
         vv = values.gather(1, index).to(dtype)
         z = torch.bmm(query, kk.transpose(1, 2)) / math.sqrt(d)
+        z = z.masked_fill(~valid[:, None, :], -torch.inf)
         ze = z.logsumexp(-1)
         exact = torch.bmm(z.softmax(-1), vv)
+        exact = torch.where(torch.isfinite(ze)[..., None], exact, torch.zeros_like(exact))   # no valid entry
         zs = torch.bmm(query, reps.transpose(1, 2)).reshape(h, 64, p, 4) / math.sqrt(d)
         zs = zs.masked_fill(mask[:, tile, None, :, None], -torch.inf)
         zt = zs.flatten(2).logsumexp(-1) + math.log(16)

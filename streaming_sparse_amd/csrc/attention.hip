@@ -261,23 +261,37 @@ __device__ __forceinline__ void pv(const u32x4 (&pb)[2], const u32x4 (&pl)[2], c
   }
 }
 
-// Unit list of tile (t, h): its C pages, then the rep tiles holding at least
-// one page the table does not select (each carrying its drop mask); maskw
-// gets the 512-bit page mask.
-// Called by every thread of the workgroup (`nthreads` of them).
-__device__ void own_units(const AttnParams& p, int h, int t, int tid, int nthreads, int* units, uint32_t* maskw,
-                          int* nunits) {
+// Unit list of tile (t, h): its exact pages in LUT order, then the rep tiles
+// holding at least one page the table does not select (each carrying its
+// drop mask); maskw gets the 512-bit page mask.  LUT entries outside [0, P)
+// (the -1 padding of a shorter table) are not read: they add no exact unit
+// and select nothing.  A page listed twice is attended twice, as a LUT walk
+// does.  Called by every 4-wave workgroup's threads; wcount is 4 ints of LDS.
+__device__ void own_units(const AttnParams& p, int h, int t, int tid, int* units, uint32_t* maskw, int* wcount,
+                          int* nunits, int* nexact) {
+  const int lane = tid & 63, wave = tid >> 6;
   if (tid < 16) maskw[tid] = 0u;
   __syncthreads();
   const int32_t* ids = p.ids + ((long long)h * p.T + t) * p.C;
-  for (int i = tid; i < p.C; i += nthreads) {
-    const int pg = min(max(ids[i], 0), p.P - 1);
-    units[i] = pg;
-    atomicOr(&maskw[pg >> 5], 1u << (pg & 31));
+  int base = 0;
+  for (int i0 = 0; i0 < p.C; i0 += kThreads) {
+    const int i = i0 + tid;
+    const int pg = i < p.C ? ids[i] : -1;
+    const bool ok = pg >= 0 && pg < p.P;
+    const unsigned long long bal = __ballot(ok);
+    if (lane == 0) wcount[wave] = __popcll(bal);
+    __syncthreads();
+    int off = base;
+    for (int w = 0; w < wave; ++w) off += wcount[w];
+    if (ok) {
+      units[off + __popcll(bal & ((1ull << lane) - 1ull))] = pg;
+      atomicOr(&maskw[pg >> 5], 1u << (pg & 31));
+    }
+    base += wcount[0] + wcount[1] + wcount[2] + wcount[3];
+    __syncthreads();
   }
-  __syncthreads();
   if (tid < 64) {
-    const int lane = tid, R = (p.P + 15) >> 4;
+    const int R = (p.P + 15) >> 4;
     bool live = false;
     uint32_t drop = 0xffffu;
     if (lane < R) {
@@ -289,8 +303,11 @@ __device__ void own_units(const AttnParams& p, int h, int t, int tid, int nthrea
       live = drop != 0xffffu;
     }
     const unsigned long long bal = __ballot(live);
-    if (live) units[p.C + __popcll(bal & ((1ull << lane) - 1ull))] = rep_unit(lane, drop);
-    if (lane == 0) *nunits = p.C + __popcll(bal);
+    if (live) units[base + __popcll(bal & ((1ull << lane) - 1ull))] = rep_unit(lane, drop);
+    if (lane == 0) {
+      *nunits = base + __popcll(bal);
+      *nexact = base;
+    }
   }
 }
 
@@ -306,7 +323,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   __shared__ int units[kMaxCount + kMaxRepTiles];
   __shared__ uint32_t maskw[16];
   __shared__ float xm[NB][2][64], xl[NB][2][64];
-  __shared__ int nunits_s;
+  __shared__ int nunits_s, nexact_s, wcount[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave >> 2, pair = (wave >> 1) & 1, qw = wave & 1;
   const int TB = p.T / NB;
@@ -321,11 +338,11 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
   for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st);
   if (NB == 1) {
-    own_units(p, h, t, tid, kThreads, units, maskw, &nunits_s);
+    own_units(p, h, t, tid, units, maskw, wcount, &nunits_s, &nexact_s);
   } else {
     // every page exact, no rep tiles: units are the pages in order
     for (int i = tid; i < p.P; i += kThreads * NB) units[i] = i;
-    if (tid == 0) nunits_s = p.P;
+    if (tid == 0) nunits_s = nexact_s = p.P;
   }
   __syncthreads();
   const int nunits = nunits_s;
@@ -444,7 +461,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   using PageUnits = std::integral_constant<int, 0>;
   using RepUnits = std::integral_constant<int, 1>;
   using AnyUnits = std::integral_constant<int, 2>;
-  const int npages = NB == 1 ? min(p.C, nunits) : nunits;
+  const int npages = nexact_s;
   int i = 0;
   for (; i + 2 < nunits && i + 3 < npages; i += 2) {
     step(PageUnits{}, i, S0, S1);
@@ -565,9 +582,11 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   p.HPV = rep_head_pages;
   p.C = count;
   p.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
-  // a call that selects every page with an even number of blocks runs two
-  // blocks per workgroup on one shared K/V stream
-  if (count == pages && p.T % 2 == 0) {
+  // a call whose caller states that every LUT row lists each page once
+  // (flags bit 1: a dense call) runs, with an even number of blocks, two
+  // blocks per workgroup on one shared K/V stream of pages 0..P-1; ids are
+  // then not read.  Without the flag the LUT is walked as given.
+  if ((flags & 2) && count == pages && p.T % 2 == 0) {
     const dim3 grid(heads * p.T / 2);
     if (flags & 1)
       hipLaunchKernelGGL((attn_kernel<true, 2>), grid, dim3(2 * kThreads), 0, stream, p);

@@ -66,35 +66,37 @@ __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70
 
 // 16-byte global->LDS load of one wave: lane l's 16 bytes at base + off
 // (bytes; base wave-uniform in SGPRs, off per lane) land at lds + 16*l.
+// The LDS base goes in through the "{m0}" operand, so the compiler writes
+// M0 itself and knows its value (the asm reads M0 and clobbers nothing);
+// the s_nop keeps the one wait state an M0 write needs before an LDS DMA.
 // Issued from inline asm so the compiler does not fence later LDS reads on
 // it; wait_loads() (and a barrier, for other waves' loads) orders it.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // N consecutive 1 KB global->LDS loads of one wave: load jj reads base +
 // off[jj] + jj * 1024 (per lane) into lds + jj * 1024 + 16 * lane, with one
-// M0 write for all of them.
+// M0 value for all of them.
 template <int N>
 __device__ __forceinline__ void dma_rows(const void* base, const uint32_t (&off)[4], uint32_t lds) {
   if constexpr (N == 4) {
     asm volatile(
-        "s_mov_b32 m0, %4\n\ts_nop 0\n\t"
-        "global_load_lds_dwordx4 %0, %5\n\t"
-        "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
-        "global_load_lds_dwordx4 %2, %5 offset:2048\n\t"
-        "global_load_lds_dwordx4 %3, %5 offset:3072" ::"v"(off[0]),
-        "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(lds), "s"(base)
-        : "memory", "m0");
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %4\n\t"
+        "global_load_lds_dwordx4 %1, %4 offset:1024\n\t"
+        "global_load_lds_dwordx4 %2, %4 offset:2048\n\t"
+        "global_load_lds_dwordx4 %3, %4 offset:3072" ::"v"(off[0]),
+        "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(base), "{m0}"(lds)
+        : "memory");
   } else {
     static_assert(N == 2, "2 or 4 loads");
     asm volatile(
-        "s_mov_b32 m0, %2\n\ts_nop 0\n\t"
-        "global_load_lds_dwordx4 %0, %3\n\t"
-        "global_load_lds_dwordx4 %1, %3 offset:1024" ::"v"(off[0]),
-        "v"(off[1]), "s"(lds), "s"(base)
-        : "memory", "m0");
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %2\n\t"
+        "global_load_lds_dwordx4 %1, %2 offset:1024" ::"v"(off[0]),
+        "v"(off[1]), "s"(base), "{m0}"(lds)
+        : "memory");
   }
 }
 

@@ -205,7 +205,8 @@ struct PsetParams {
 };
 
 __device__ __forceinline__ int own_page(const PsetParams& p, int h, int t) {
-  return p.own ? p.own[(long long)h * p.T + t] : p.P - p.T + t;
+  // clamped into the window like the router's own page (memory safety)
+  return min(max(p.own ? p.own[(long long)h * p.T + t] : p.P - p.T + t, 0), p.P - 1);
 }
 
 struct PoolSmem {
@@ -837,6 +838,9 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
     for (int k = 0; k < nsel; ++k) rank += s.key[k] > kx;
     if (1 + rank < p.C) ids[1 + rank] = s.page[i];
   }
+  // a selection shorter than the table (quotas clamped to their partitions)
+  // leaves -1 padding, as the router writes it
+  for (int i = 1 + nsel + tid; i < p.C; i += 256) ids[i] = -1;
 }
 
 }  // namespace

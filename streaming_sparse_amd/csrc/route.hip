@@ -3,9 +3,9 @@
 //
 // Reference path (intersection tier, VB/graph.py:102-211):
 //   z    = bf16(probe) . bf16(repK)^T * D^-1/2           (VR/tensor_bmm.py:56-66)
-//   norm = max / sum exp over the P*4 reps of each probe  (VR/risk_online.py:151-159)
+//   norm = max / sum exp over the P*4 reps of each probe  (VR/risk_online.py:88-113)
 //   risk = mean over 16 probes of ((t0 x0 + t1 x1) + t2 x2) + t3 x3
-//                                                         (VR/risk_online.py:86-122)
+//          (VR/runtime.py:27-40; kernels VR/risk_online.py:24-59,77-86)
 //   mask = quota selection (VB/quota_mask.py:7-39) or the base LUT
 //          (VR/runtime.py:279-288) or fixed top-k (VR/fixed_page_select.py:8-47)
 //   ids  = own first, then descending risk                (VB/graph.py:210)
@@ -528,9 +528,25 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int tb = min(t0 + q, p.T - 1);
-    own[q] = p.own ? p.own[(long long)h * p.T + tb] : P - p.T + tb;
+    // own pages outside the window are clamped into it (memory safety of
+    // the per-page state; a valid own is in [0, P))
+    own[q] = min(max(p.own ? p.own[(long long)h * p.T + tb] : P - p.T + tb, 0), P - 1);
   }
-  const int A = p.mode == 1 ? p.current[h] : 0;
+  // Quota partitions (VB/quota_mask.py:18-31): anchors [0,24), history
+  // [24,cur_lo), current [cur_lo,P).  With P == 72 the anchor frame is the
+  // chunk's first frame (VB/graph.py:143-148): current = [24,72), no history,
+  // and the current quota is the whole total.  Each partition keeps its
+  // quota clamped to [0, its size], as _keep does: current min(A, 72),
+  // history total - A (with the unclamped A, as quota_mask passes it).  The
+  // listed pages can then number more or fewer than the table holds.
+  const int cur_lo = P == kCurrent ? kAnchors : P - kCurrent;
+  const int ncur = P - cur_lo, nhist = cur_lo - kAnchors;
+  int A = 0, nh = 0;
+  if (p.mode == 1) {
+    const int araw = P == kCurrent ? p.total : p.current[h];
+    A = min(max(araw, 0), ncur);
+    nh = min(max(p.total - araw, 0), nhist);
+  }
   unsigned long long keys[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -542,8 +558,8 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       if (p.mode == 0) {
         if (pg >= kAnchors && pg != own[b]) key = (1ull << 62) | ord | low;
       } else if (p.mode == 1) {
-        if (pg == own[b]) key = (3ull << 62) - 1ull - (unsigned long long)pg;     // own first in current
-        else if (pg >= P - kCurrent) key = (2ull << 62) | ord | low;
+        if (pg >= cur_lo) key = pg == own[b] ? (3ull << 62) - 1ull - (unsigned long long)pg   // own first in current
+                                             : (2ull << 62) | ord | low;
         else if (pg >= kAnchors) key = (1ull << 62) | ord | low;
       } else {
         key = pg == own[b] ? ~0ull - (unsigned long long)pg : ((1ull << 62) | ord | low);   // own first
@@ -575,32 +591,41 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       if (row_ok && idsrow) idsrow[i] = pg;
     }
   } else {
-    // quota: current top A at sorted [0, A) (own first), history top n-A at
-    // sorted [72, 72+n-A), anchors; list them, then order the LUT by risk
-    const int nh = p.total - A;
-    for (int i = bt; i < p.C; i += 128) {
-      const int pg = i < A ? page_at(i) : (i < A + nh ? page_at(kCurrent + i - A) : i - A - nh);
+    // quota: current top A at sorted [0, A) (own first), history top nh at
+    // sorted [ncur, ncur + nh), anchors; list them, then order the LUT by risk
+    const int nlist = kAnchors + A + nh;    // <= P
+    for (int i = bt; i < nlist; i += 128) {
+      const int pg = i < A ? page_at(i) : (i < A + nh ? page_at(ncur + i - A) : i - A - nh);
       sl.list[b][i] = pg;
       sl.sel[b][pg] = 1;
     }
     __syncthreads();
     if (idsrow) {
-      // LUT slot = number of listed pages ahead: own first (largest key),
-      // then descending risk, ties -> lower page.  The sorted keys are no
-      // longer needed, so the listed pages' keys take their place.
-      for (int i = bt; i < p.C; i += 128) {
-        const int pg = sl.list[b][i];
+      // The LUT is topk(C) of the risk masked to the listed pages with own at
+      // +inf (VB/graph.py:210): own first even when its quota left it out
+      // (then it is an extra entry and the lowest listed page falls off),
+      // then descending risk, ties -> lower page; slots past the entries
+      // are padding -1.  LUT slot = number of entries with a larger key.
+      // The sorted keys are no longer needed, so the entries' keys take
+      // their place.
+      const bool own_listed = sl.sel[b][own[b]] != 0;
+      const int nent = nlist + (own_listed ? 0 : 1);   // <= P
+      for (int i = bt; i < nent; i += 128) {
+        const int pg = i < nlist ? sl.list[b][i] : own[b];
+        if (i >= nlist) sl.list[b][i] = pg;
         sl.key[b][i] = pg == own[b] ? ~0ull
                                     : ((unsigned long long)orderable(s.risk[b][pg]) << 32) | (uint32_t)(1023 - pg);
       }
       __syncthreads();
-      for (int i = bt; i < p.C; i += 128) {
+      for (int i = bt; i < nent; i += 128) {
         const unsigned long long kx = sl.key[b][i];
         int rank = 0;
 #pragma unroll 8
-        for (int j = 0; j < p.C; ++j) rank += sl.key[b][j] > kx;
-        if (row_ok) idsrow[rank] = sl.list[b][i];
+        for (int j = 0; j < nent; ++j) rank += sl.key[b][j] > kx;
+        if (row_ok && rank < p.C) idsrow[rank] = sl.list[b][i];
       }
+      for (int i = nent + bt; i < p.C; i += 128)
+        if (row_ok) idsrow[i] = -1;
     }
   }
   __syncthreads();
@@ -629,10 +654,13 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
   // the rep value rows move in 16-byte loads and stores
   if (rep_values && (((uintptr_t)mean | (uintptr_t)detail | (uintptr_t)basis | (uintptr_t)rep_values) & 15))
     return (int)hipErrorInvalidValue;
+  if (mode >= 0 && (count < 1 || count > pages)) return (int)hipErrorInvalidValue;
   if (mode == 0 && (count < 1 + kAnchors || pages < kAnchors + kCurrent)) return (int)hipErrorInvalidValue;
-  if (mode == 1 && (count != kAnchors + total || pages <= kAnchors + kCurrent || current == nullptr))
+  // quota mode: windows of 72 pages (the anchor frame inside the chunk) or
+  // at least anchors + current; total <= P - 24 non-anchor pages
+  if (mode == 1 && (total < 0 || count != kAnchors + total || (pages != kCurrent && pages < kAnchors + kCurrent) ||
+                    (pages != kCurrent && current == nullptr)))
     return (int)hipErrorInvalidValue;
-  if (mode == 2 && (count < 1 || count > pages)) return (int)hipErrorInvalidValue;
   RouteParams p;
   p.q = (const uint16_t*)q;
   p.q_head = q_head_stride;

@@ -7,6 +7,8 @@ there is no CPU or eager-torch fallback.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib
@@ -58,19 +60,35 @@ def rep_values(s: Summary, basis: torch.Tensor, pages: int, out: torch.Tensor):
 rep_values_fn = rep_values   # attention() takes a `rep_values` keyword
 
 
+SINGLE_AV = False
+"""Module switch of the P.V arithmetic, as the reference's (legacy_components.py:4):
+False (default) runs the reference's two-term bf16 product (hi + lo parts of
+each probability, HIGH_PRECISION_AV=not SINGLE_AV at legacy_components.py:49;
+the tail's _av at tuned_attention.py:16-18); True runs one bf16 product."""
+
+
 @torch.no_grad()
-def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=False, rep_values=None):
+def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None, all_pages=False,
+              rep_values=None):
     """Exact attention over the LUT pages + summary compensation + merge.
 
     q [1,N,H,128] bf16 contiguous; k, v [1,64P,H,128] bf16 (resident cache);
     s a Summary covering the P pages; basis [H,128,8]; ids [H,N/64,C] int32 with
-    own page first.  Returns ``out`` [1,N,H,128] bf16, owned by `workspace`
-    and overwritten by the next call.  ``bf16_av`` is accepted for signature
-    compatibility; ``precise_av`` selects two-term (hi+lo) bf16 P.V in every
-    unit, the reference's exact-stage arithmetic.  ``rep_values``: the
-    [H,P,4,128] rep value rows of `s` and `basis` when the caller already has
-    them (route(..., rep_out=...) writes them on the side); otherwise they
-    are computed here."""
+    own page first (entries outside [0,P), the -1 padding of a shorter table,
+    are not read).  Returns ``out`` [1,N,H,128] bf16, owned by `workspace`
+    and overwritten by the next call.
+
+    Arithmetic: every probability multiplies V (and the rep value rows) as
+    the two-term bf16 product hi + lo, the reference's exact stage and its
+    ``bf16_av=True`` tail; ``bf16_av=False`` (the reference's tf32x3 tail) maps
+    to the same two-term product, the closest this kernel runs.
+    ``single_av=True`` (default: the module's SINGLE_AV) opts into one bf16
+    product instead.  ``all_pages=True`` states that every row of ids lists
+    each page exactly once (a dense call): two query blocks then share each
+    K/V page load and ids are not read.  ``rep_values``: the [H,P,4,128] rep
+    value rows of `s` and `basis` when the caller already has them
+    (route(..., rep_out=...) writes them on the side); otherwise they are
+    computed here."""
     _, n, h, d = q.shape
     p = k.shape[1] // 64
     count = ids.shape[-1]
@@ -87,7 +105,9 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=Fal
     def buf(name, shape, dtype):
         return workspace.tensor('ssa_' + name, shape, q.device, dtype)
 
-    if count >= p:
+    if all_pages and count != p:
+        raise ValueError("all_pages needs a table of exactly P pages per row")
+    if all_pages:
         # every page exact: the kernel reads no rep rows (the rep keys stand
         # in for the unused pointer)
         vrep = s.keys
@@ -99,7 +119,8 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=Fal
     else:
         vrep = rep_values_fn(s, basis, p, buf('rep_values', (h, p, 4, d), torch.bfloat16))
     out = buf('out', q.shape, q.dtype)
-    flags = 1 if precise_av else 0
+    single = SINGLE_AV if single_av is None else bool(single_av)
+    flags = (0 if single else 1) | (2 if all_pages else 0)
     _lib.check(_lib.lib().ssa_attention(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(s.keys), _lib.ptr(vrep),
                                         _lib.ptr(ids), _lib.ptr(out), n, h, p, hp, vrep.shape[1], count, tok, head,
                                         flags, _lib.stream_handle(q.device)), "ssa_attention")
@@ -107,17 +128,29 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, precise_av=Fal
 
 
 @torch.no_grad()
-def risk(probes, z, summary, theta):
-    """Per-page risk [H,T,P] fp32 from probe rows [H,T,16,128].  The probe
-    logits are recomputed on chip from `probes` and the rep keys (z is the
-    reference's precomputed q.repK/sqrt(D) and is only shape-checked)."""
+def risk(probes, z, summary, theta, *, z_tol=1e-4):
+    """Per-page risk [H,T,P] fp32 from probe rows [H,T,16,128].
+
+    The kernel forms the probe logits on chip from `probes` and the rep keys.
+    `z` is the reference's precomputed logits bf16(probe).bf16(repK)^T/sqrt(D)
+    [H,T,16,P,4] (legacy_components.py:14-22 consumes them); a z that is not
+    those of `probes` (beyond fp32 summation order: |dz| <= z_tol (1 + |z|))
+    is rejected with ValueError rather than silently ignored.  z=None skips
+    the check."""
     h, t, m, d = probes.shape
     p = summary.mean.shape[1]
     if m != 16 or d != HEAD_DIM:
         raise ValueError("probes must be [H,T,16,128]")
-    if z is not None and tuple(z.shape[:3]) != (h, t, m):
-        raise ValueError("z does not match probes")
     hp = _check_summary(summary, h, p)
+    if z is not None:
+        if tuple(z.shape) != (h, t, m, p, 4):
+            raise ValueError(f"z must be [H,T,16,P,4] = {(h, t, m, p, 4)}, got {tuple(z.shape)}")
+        pf = probes.to(torch.bfloat16).float().reshape(h, t * m, d)
+        kf = summary.keys.float().reshape(h, p * 4, d)
+        mine = torch.bmm(pf, kf.transpose(1, 2).contiguous()).reshape(h, t, m, p, 4) / math.sqrt(d)
+        zf = z.float()
+        if not bool(((mine - zf).abs() <= z_tol * (1 + zf.abs())).all()):
+            raise ValueError("z is not the probe logits of `probes` and the summary's rep keys")
     pr = probes.to(torch.bfloat16).contiguous()
     th = theta.float().contiguous()
     out = torch.empty(h, t, p, device=probes.device, dtype=torch.float32)

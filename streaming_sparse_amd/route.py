@@ -8,6 +8,9 @@
 * ``tier='intersection'``: anchors + top A current pages (own forced) + top
   (n - A) history pages; ids = own first then descending risk
   (reproduction/vbench_current/quota_mask.py:7-39, graph.py:150-151,210).
+  Quotas larger than their partition keep the whole partition and the table
+  is padded with -1.  A 72-page window (the anchor frame is the chunk's first
+  frame, graph.py:143-148) keeps the anchors and the top n of pages 24..71.
 * ``tier='topk'``: fixed top-floor(0.1 P) with own forced
   (local_experiments/review_v1/ops.py:113-138).
 
@@ -49,7 +52,8 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
           rep_out=None):
     """q [1,N,H,128] bf16 queries of the current chunk; summary over the P
     window pages; theta [H,4]; own [H,T] (default: page P-T+t).  For the
-    intersection tier pass current_slots [H] (A per head, >= 1) and n = A+B.
+    intersection tier pass n = A+B (<= P - 24) and, unless P == 72,
+    current_slots [H] (A per head).
     full_pset: head ids to correct with `encoding` (pset.Encoding over the
     window) and `reader` (pset.Reader).  lse_out: optional [H,T,16] fp32
     tensor that receives each probe's log-sum-exp over all reps.
@@ -64,17 +68,20 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
     hp = _check_summary(summary, h, p)
     if tier not in MODES:
         raise ValueError(f"unknown tier {tier!r}")
-    if tier == 'intersection' and (current_slots is None or n is None):
-        raise ValueError("intersection tier needs current_slots and n")
+    if tier == 'intersection' and (n is None or (current_slots is None and p != CURRENT)):
+        raise ValueError("intersection tier needs n and (unless P == 72) current_slots")
+    if tier == 'intersection' and not 0 <= int(n) <= p - ANCHORS:
+        raise ValueError(f"intersection quota n={n} outside [0, P-24]")
     mode = MODES[tier]
     count = tier_count(tier, p, n)
     dev = q.device
     cur = None
     total = 0
     if tier == 'intersection':
-        cur = torch.as_tensor(current_slots, device=dev).to(torch.int32).contiguous()
-        if cur.shape != (h,):
-            raise ValueError("current_slots must be [H]")
+        if current_slots is not None:
+            cur = torch.as_tensor(current_slots, device=dev).to(torch.int32).contiguous()
+            if cur.shape != (h,):
+                raise ValueError("current_slots must be [H]")
         total = int(n)
     if tier == 'base' and p < ANCHORS + CURRENT:
         raise ValueError("base tier needs a history window")

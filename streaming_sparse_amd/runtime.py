@@ -133,7 +133,7 @@ class ChunkRuntime:
 
     def dense_call(self, layer: int, q):
         L = self.layers[layer]
-        return attention(q, L.k, L.v, L.summary, L.basis, self.dense_ids, self.ws)
+        return attention(q, L.k, L.v, L.summary, L.basis, self.dense_ids, self.ws, all_pages=True)
 
     def sparse_call(self, layer: int, step: int, q):
         """One sparse attention call (layers >= 1): current summaries,

@@ -217,32 +217,70 @@ def test_route_writes_rep_values(device, cfg, frames):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-@pytest.mark.parametrize("precise", [False, True])
-def test_attention_config0(device, precise):
-    """216-page window, base tier LUT (32 pages), all 72 query blocks x 12 heads."""
+@pytest.mark.parametrize("single", [False, True])
+def test_attention_config0(device, single):
+    """216-page window, base tier LUT (32 pages), all 72 query blocks x 12
+    heads; the reference's two-term P.V (default) and the single-term opt-in."""
     x = call_inputs(0, 9)
     g = x.to(device)
     ids = ref.select_base(oracle_risk(x), x.own, 32)
-    out = attention(g.q, g.k, g.v, g.summary, g.basis, ids.to(device), Workspace(), precise_av=precise)
+    out = attention(g.q, g.k, g.v, g.summary, g.basis, ids.to(device), Workspace(), single_av=single)
     torch.cuda.synchronize()
     want = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, ids).bfloat16()
-    check_out(out, want, f"config0 precise={precise}")
+    check_out(out, want, f"config0 single={single}")
 
 
-def test_attention_config1_tiles(device):
+TILES8 = [0, 9, 23, 35, 36, 50, 64, 71]
+
+
+def tile_rows(tiles):
+    return torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in tiles])
+
+
+@pytest.mark.parametrize("single", [False, True])
+def test_attention_config1_tiles(device, single):
     """432-page window, 64 exact pages; oracle on 8 spread query blocks."""
     x = call_inputs(1, 18)
     g = x.to(device)
     ids = ref.select_base(oracle_risk(x), x.own, 64)
-    out = attention(g.q, g.k, g.v, g.summary, g.basis, ids.to(device), Workspace())
+    out = attention(g.q, g.k, g.v, g.summary, g.basis, ids.to(device), Workspace(), single_av=single)
     torch.cuda.synchronize()
-    tiles = [0, 9, 23, 35, 36, 50, 64, 71]
-    want = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, ids, tiles=tiles).bfloat16()
-    rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in tiles])
-    check_out(out[:, rows], want[:, rows], "config1 tiles")
+    want = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, ids, tiles=TILES8).bfloat16()
+    rows = tile_rows(TILES8)
+    check_out(out[:, rows], want[:, rows], f"config1 tiles single={single}")
 
 
-def test_full_call_properties(device):
+@pytest.mark.parametrize("single", [False, True])
+def test_attention_config2_intersection_tiles(device, single):
+    """432-page window under the intersection tier's per-head quotas (layer 3,
+    step 0 of the seeded table: 24 anchors + A current + B history pages per
+    head, A+B equal over the heads): the oracle's quota mask and LUT, then
+    attention against the oracle on 8 spread query blocks; and the GPU
+    router's own table through the same attention."""
+    x = call_inputs(2, 18)
+    g = x.to(device)
+    tab = workload.quota_table(2)
+    a = tab[0, 3, :, 0]
+    n = int(tab[0, 3, 0].sum())
+    r = oracle_risk(x)
+    ids = ref.lut(r, ref.quota_mask(r, x.own, a, n), x.own, 24 + n)
+    assert bool((ids >= 0).all())
+    out = attention(g.q, g.k, g.v, g.summary, g.basis, ids.to(device), Workspace(), single_av=single)
+    torch.cuda.synchronize()
+    want = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, ids, tiles=TILES8).bfloat16()
+    rows = tile_rows(TILES8)
+    check_out(out[:, rows], want[:, rows], f"config2 oracle table single={single}")
+    ws = Workspace()
+    gids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', own=g.own, current_slots=a, n=n,
+                          workspace=ws)
+    out2 = attention(g.q, g.k, g.v, g.summary, g.basis, gids, ws, single_av=single)
+    torch.cuda.synchronize()
+    want2 = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, gids.cpu(), tiles=TILES8).bfloat16()
+    check_out(out2[:, rows], want2[:, rows], f"config2 router table single={single}")
+
+
+@pytest.mark.parametrize("single", [False, True])
+def test_full_call_properties(device, single):
     """Size-independent properties of the whole base call at its full size
     (432 pages, 12 heads, 4608 queries), where the oracle would take minutes:
     - two calls on the same inputs give bit-identical risk, page tables, rep
@@ -260,7 +298,7 @@ def test_full_call_properties(device):
     def call(v, s):
         vrep = torch.empty(12, x.pages, 4, 128, device=device, dtype=torch.bfloat16)
         ids, _, risk, _ = route(g.q, s, g.theta, tier='base', own=g.own, workspace=ws, rep_basis=basis, rep_out=vrep)
-        out = attention(g.q, g.k, v, s, basis, ids, ws, rep_values=vrep).clone()
+        out = attention(g.q, g.k, v, s, basis, ids, ws, rep_values=vrep, single_av=single).clone()
         return ids.clone(), risk.clone(), vrep, out
 
     ids, risk, vrep, out = call(g.v, g.summary)
@@ -277,7 +315,7 @@ def test_full_call_properties(device):
     assert torch.equal(vrep3, vrep * 2) and torch.equal(out3, out * 2)
 
     rev = torch.cat([ids[..., :1], ids[..., 1:].flip(-1)], -1).contiguous()
-    out4 = attention(g.q, g.k, g.v, g.summary, basis, rev, ws, rep_values=vrep).clone()
+    out4 = attention(g.q, g.k, g.v, g.summary, basis, rev, ws, rep_values=vrep, single_av=single).clone()
     torch.cuda.synchronize()
     check_out(out4, out.cpu(), "reversed page order")
 
@@ -323,19 +361,157 @@ def test_route_and_attention_largest_window(device):
     check_out(out[:, rows], want[:, rows], "P=504 tiles")
 
 
-def test_attention_all_pages_equals_dense(device):
-    """Every page exact: no compensation, equals softmax attention."""
+def dense_ids(own, pages):
+    h, t = own.shape
+    rest = torch.arange(pages)
+    return torch.stack([torch.cat([own[a, b:b + 1], rest[rest != own[a, b]]]) for a in range(h)
+                        for b in range(t)]).reshape(h, t, pages).int()
+
+
+@pytest.mark.parametrize("single", [False, True])
+@pytest.mark.parametrize("all_pages", [False, True])
+def test_attention_all_pages_equals_dense(device, all_pages, single):
+    """Every page exact: no compensation, equals softmax attention; through
+    the two-block kernel (all_pages: the caller states the table lists every
+    page once) and through the table walk."""
     x = call_inputs(0, 9, heads=2)
     g = x.to(device)
-    P = x.pages
-    own = x.own
-    rest = torch.tensor([i for i in range(P)])
-    ids = torch.stack([torch.cat([own[h, t:t + 1], rest[rest != own[h, t]]]) for h in range(2)
-                       for t in range(72)]).reshape(2, 72, P).int()
-    out = attention(g.q, g.k, g.v, g.summary, g.basis, ids.to(device), Workspace())
+    ids = dense_ids(x.own, x.pages)
+    out = attention(g.q, g.k, g.v, g.summary, g.basis, ids.to(device), Workspace(), all_pages=all_pages,
+                    single_av=single)
     torch.cuda.synchronize()
     want = ref.dense_attention(x.q, x.k, x.v).bfloat16()
-    check_out(out, want, "all pages exact")
+    check_out(out, want, f"all pages exact all_pages={all_pages} single={single}")
+
+
+@pytest.mark.parametrize("single", [False, True])
+def test_attention_dense_432_tiles(device, single):
+    """The dense call at full size (432 pages, 12 heads, the two-block
+    kernel) against dense softmax attention on 8 spread query blocks."""
+    x = call_inputs(1, 18)
+    g = x.to(device)
+    ids = dense_ids(x.own, x.pages)
+    out = attention(g.q, g.k, g.v, g.summary, g.basis, ids.to(device), Workspace(), all_pages=True,
+                    single_av=single)
+    torch.cuda.synchronize()
+    rows = tile_rows(TILES8)
+    want = ref.dense_attention(x.q[:, rows], x.k, x.v).bfloat16()
+    check_out(out[:, rows], want, f"dense 432 tiles single={single}")
+
+
+def test_attention_padding_and_duplicates(device):
+    """LUT entries outside [0, P) are not read (RV/ops.py:115): a table with
+    -1 and out-of-window entries gives bit for bit the output of the table
+    without them (the kernel walks the same units).  A full-length table with
+    a page listed twice (so another page is missing) is walked as given
+    without the all-pages flag: the repeated page counts twice and the
+    missing one is compensated, as the oracle's table walk does."""
+    x = call_inputs(0, 9)
+    g = x.to(device)
+    P = x.pages
+    ids = ref.select_base(oracle_risk(x), x.own, 32)
+    short = ids[..., :27]
+    junk = torch.tensor([-1, P, -1000, 4096, -1], dtype=torch.int32).expand(12, 72, 5)
+    padded = torch.cat([short[..., :3], junk[..., :2], short[..., 3:], junk[..., 2:]], -1).contiguous()
+    ws = Workspace()
+    a = attention(g.q, g.k, g.v, g.summary, g.basis, short.to(device), ws).clone()
+    b = attention(g.q, g.k, g.v, g.summary, g.basis, padded.to(device), ws).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    want = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, padded).bfloat16()
+    check_out(b, want, "padded table")
+    x2 = call_inputs(0, 9, heads=2)
+    g2 = x2.to(device)
+    dup = dense_ids(x2.own, P)
+    dup[:, :, 5] = dup[:, :, 6]            # page at slot 5 missing, slot 6's page twice
+    out = attention(g2.q, g2.k, g2.v, g2.summary, g2.basis, dup.to(device), Workspace())
+    torch.cuda.synchronize()
+    want2 = ref.selected_attention(x2.q, x2.k, x2.v, x2.summary, x2.basis, dup).bfloat16()
+    check_out(out, want2, "duplicate page, full-length table")
+
+
+def test_risk_checks_z(device):
+    """risk() takes the reference's precomputed logits z: z of the same
+    probes passes and gives the same risk as z=None; z of other probes is
+    rejected."""
+    x = call_inputs(0, 9)
+    g = x.to(device)
+    pr = ref.probes(g.q)
+    z = ref.route_logits(pr.cpu(), x.summary.keys).to(device)
+    a = risk_fn(pr, None, g.summary, g.theta)
+    b = risk_fn(pr, z, g.summary, g.theta)
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        risk_fn(pr, z.flip(1), g.summary, g.theta)
+
+
+def route_intersection_check(x, g, a, n, tag):
+    """GPU intersection router vs. the oracle's quota mask and LUT; rows with
+    a near tie at a partition boundary are exempt from equality."""
+    P = x.pages
+    cur_a = a if P != 72 else None
+    ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='intersection', own=g.own, current_slots=cur_a, n=n)
+    r64 = ref.risk(ref.probes(x.q), ref.route_logits(ref.probes(x.q), x.summary.keys, torch.float64),
+                   x.summary.stats, x.theta, dtype=torch.float64)
+    rel = float(((risk.cpu().double() - r64).abs() / r64.abs().clamp_min(1e-30)).max())
+    assert rel < 1e-4, rel
+    want_mask = ref.quota_mask(r64, x.own, a, n)
+    want = ref.lut(r64, want_mask, x.own, 24 + n)
+    ties = torch.zeros(x.own.shape, dtype=torch.bool)
+    if P == 72:
+        cur = r64.clone()
+        cur[..., :24] = -math.inf
+        cur.scatter_(-1, x.own.long()[..., None], math.inf)
+        cur[..., :24] = -math.inf
+        ties |= ref.near_tie_rows(cur, torch.full(x.own.shape, n))
+    else:
+        hist = r64.clone()
+        hist[..., :24] = -math.inf
+        hist[..., P - 72:] = -math.inf
+        cur = r64.clone()
+        cur[..., :P - 72] = -math.inf
+        cur.scatter_(-1, x.own.long()[..., None], math.inf)
+        ties |= ref.near_tie_rows(hist, (n - a).clamp_min(0)[:, None].expand_as(x.own))
+        ties |= ref.near_tie_rows(cur, a.clamp(0, 72)[:, None].expand_as(x.own))
+    got_mask = mask.cpu()
+    got = ids.cpu()
+    same = (got_mask == want_mask).all(-1)
+    print(f"{tag}: {int(same.sum())}/{same.numel()} masks identical, {int(ties.sum())} near-tie rows", flush=True)
+    assert bool((same | ties).all())
+    rows = same & ~ties
+    # same entries (own first, then the selection by risk, -1 padding); the
+    # order among near-equal risks may differ
+    assert (got[..., 0] == x.own).all()
+    assert torch.equal(got[rows].sort(-1).values, want[rows].sort(-1).values)
+    return got, got_mask
+
+
+def test_route_intersection_first_chunk(device):
+    """72-page window: the anchor frame is the chunk's first frame
+    (VB/graph.py:143-148); anchors plus the top n of pages 24..71, own forced
+    (own pages 0..23 are anchors themselves)."""
+    x = call_inputs(2, 3)
+    assert x.pages == 72
+    g = x.to(device)
+    ids, mask = route_intersection_check(x, g, torch.zeros(12, dtype=torch.int64), 20, "P=72")
+    assert ids.shape == (12, 72, 44) and bool((mask[..., :24]).all())
+    assert (mask.sum(-1) == 44).all()
+
+
+def test_route_intersection_clamped_quotas(device):
+    """Quotas outside their partitions at P=216: A = 0 (own not selected,
+    still first in the table, the lowest selected page falls off), A = 72
+    and A > 72 (the whole current frame), A + B larger than the history
+    (the history is kept whole, the table padded with -1)."""
+    x = call_inputs(0, 9)
+    g = x.to(device)
+    a = torch.tensor([0, 1, 72, 80, 30, 5, 0, 72, 40, 3, 60, 10])
+    got, mask = route_intersection_check(x, g, a, 150, "clamped quotas")
+    assert (mask[:, :, 24:216 - 72].sum(-1) <= 120).all()
+    # heads whose quotas select fewer pages than the table holds end in -1
+    padded, full = [0, 1, 3, 5, 6, 9, 11], [2, 4, 7, 8, 10]
+    assert bool((got[padded] == -1).any(-1).all()) and not bool((got[full] == -1).any())
+    assert bool((~mask[[0, 6]].gather(-1, x.own[[0, 6]].long()[..., None])).all())   # A = 0: own not selected
 
 
 @pytest.mark.parametrize("n", [128, 192])

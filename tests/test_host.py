@@ -68,6 +68,10 @@ def test_route_rejects_bad_arguments():
         route(q, s, theta, full_pset=[0])                             # Full_Pset only on the intersection tier
     with pytest.raises(ValueError):
         route(q, s, theta, lse_out=torch.zeros(H, 2, 8))              # lse_out shape
+    with pytest.raises(ValueError):
+        route(q, s, theta, tier='intersection', current_slots=[4, 4], n=216 - 23)   # n > P - 24
+    with pytest.raises(ValueError):
+        route(q, s, theta, tier='intersection', n=20)                 # current_slots needed unless P == 72
 
 
 def test_attention_rejects_bad_arguments():
@@ -89,6 +93,24 @@ def test_attention_rejects_bad_arguments():
     with pytest.raises((TypeError, ValueError)):
         bad = Summary(s.keys.float(), s.mean, s.detail, s.stats)
         attention(q, k, k, bad, basis, ids, ws)                       # summaries are bf16
+    with pytest.raises(ValueError):
+        attention(q, k, k, s, basis, ids, ws, all_pages=True)         # all_pages needs P entries per row
+
+
+def test_risk_rejects_foreign_logits():
+    """risk() consumes the reference's z only if it is the probe logits of
+    its probes (checked on the host before any library call)."""
+    from streaming_sparse_amd.legacy_components import risk
+    p = 20
+    g = torch.Generator().manual_seed(1)
+    s = Summary(torch.randn(H, p, 4, D, generator=g).bfloat16(), torch.zeros(H, p, D, dtype=torch.bfloat16),
+                torch.zeros(H, p, 3, 8, dtype=torch.bfloat16), torch.zeros(H, p, 4, 12, dtype=torch.bfloat16))
+    probes = torch.randn(H, 2, 16, D, generator=g)
+    z = torch.randn(H, 2, 16, p, 4, generator=g)
+    with pytest.raises(ValueError):
+        risk(probes, z, s, torch.ones(H, 4))                          # not the logits of these probes
+    with pytest.raises(ValueError):
+        risk(probes, z[..., :2], s, torch.ones(H, 4))                 # wrong shape
 
 
 def test_quota_tables_keep_totals():
@@ -122,6 +144,10 @@ def test_c_abi_rejects_bad_shapes():
     assert rt(72, 64, 0, 0) == INVALID
     assert rt(432, 60, 1, 40, cur=8) == INVALID
     assert rt(432, 64, 1, 40) == INVALID                              # no current quotas
+    assert rt(216, 217, 2, 0) == INVALID                              # count > pages
+    assert rt(216, 24 + 193, 1, 193, cur=8) == INVALID                # total > P - 24
+    assert rt(432, 20, 1, -4, cur=8) == INVALID                       # negative total
+    assert rt(80, 44, 1, 20, cur=8) == INVALID                        # 72 < P < 96: no such window
     assert rt(432, 64, 0, 0, rv=16, mean=None) == INVALID            # rep values without mean/detail/basis
     assert rt(432, 64, 0, 0, rv=16, mean=8) == INVALID               # misaligned
     # ssa_summary: page range inside the slab, iters >= 1

@@ -221,6 +221,67 @@ def test_quota_mask_semantics(p):
             assert row[1:] == _brute_top(risk[hh, tt], rest, count - 1)
 
 
+@pytest.mark.parametrize("p", [72, 96, 216])
+def test_quota_mask_clamped_and_first_chunk(p):
+    """Quotas outside their partitions and the first-chunk window, against a
+    plain-Python restatement of _keep (VB/quota_mask.py:7-15: slots <= 0
+    keeps nothing, slots >= the partition keeps all of it; the history quota
+    is TOTAL - current with the unclamped current, :25), of the 72-page
+    branch (VB/graph.py:143-148) and of the final topk LUT (VB/graph.py:210)
+    with -1 where topk would run into unselected pages."""
+    h, t = 5, 6
+    risk = _adversarial_rows(p, h * t, 11).reshape(h, t, p)
+    if p == 72:
+        own = torch.tensor([3, 23, 24, 40, 60, 71])[None].expand(h, -1).contiguous()
+        total = 30
+    else:
+        own = (torch.arange(t) * 13 % 72 + p - 72)[None].expand(h, -1).contiguous()
+        total = {96: 50, 216: 150}[p]
+    current = torch.tensor([0, 1, 72, 80, 30])
+    count = 24 + total
+    mask = ref.quota_mask(risk, own, current, total)
+    ids = ref.lut(risk, mask, own, count)
+    for hh in range(h):
+        a = int(current[hh])
+        for tt in range(t):
+            o = int(own[hh, tt])
+            r = risk[hh, tt].clone()
+            if p == 72:
+                if o >= 24:
+                    r[o] = torch.inf
+                picked = _brute_top(r, range(24, 72), total)
+            else:
+                if p - 72 <= o:
+                    r[o] = torch.inf
+                picked = (_brute_top(r, range(p - 72, p), a) if a > 0 else []) + \
+                    (_brute_top(risk[hh, tt], range(24, p - 72), total - a) if total - a > 0 else [])
+            listed = set(range(24)) | set(picked)
+            assert [i for i in range(p) if mask[hh, tt, i]] == sorted(listed)
+            entries = [o] + _brute_top(risk[hh, tt], sorted(listed - {o}), len(listed))
+            want = (entries + [-1] * count)[:count]
+            assert ids[hh, tt].tolist() == want, (p, hh, tt)
+
+
+def test_selected_attention_skips_padding():
+    """LUT entries outside [0, P) are not read: a table with -1 and
+    out-of-window entries gives the output of the table without them."""
+    g = torch.Generator().manual_seed(21)
+    h, p, n = 2, 12, 128
+    q = torch.randn(1, n, h, 128, generator=g).bfloat16()
+    k = torch.randn(1, 64 * p, h, 128, generator=g).bfloat16()
+    v = torch.randn(1, 64 * p, h, 128, generator=g).bfloat16()
+    kp = k[0].transpose(0, 1).reshape(h, p, 64, 128)
+    vp = v[0].transpose(0, 1).reshape(h, p, 64, 128)
+    basis = workload.pca_basis(vp.float())
+    s = workload.kmeans_summaries(kp, vp, basis, torch.Generator().manual_seed(3))
+    ids = torch.tensor([[[11, 2, 5], [10, 0, 7]]] * h).int()
+    padded = torch.tensor([[[11, -1, 2, p, 5, -1], [10, 0, -1, 7, 99, -1]]] * h).int()
+    want = ref.selected_attention(q, k, v, s, basis, ids, dtype=torch.float64)
+    got = ref.selected_attention(q, k, v, s, basis, padded, dtype=torch.float64)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+    assert torch.equal(ref.mask_from_ids(padded, p), ref.mask_from_ids(ids, p))
+
+
 def test_select_topk_semantics():
     p = 216
     risk = _adversarial_rows(p, 6, 13).reshape(2, 3, p)
