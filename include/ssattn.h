@@ -150,6 +150,24 @@ int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, l
              double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
              int total_heads, int blocks, int pages, int count, hipStream_t stream);
 
+/* ssa_pset without the caller-owned scratch (cand, rows, pool): the library
+ * keeps that scratch in a file-scope device array of 48.05 MB per device
+ * (held until the process ends), sized for n_heads * blocks <= 216 scoped rows
+ * (3 heads x 72 query blocks); larger calls return hipErrorInvalidValue.
+ * Allocates nothing (no hipMalloc, no allocating library routine); the first
+ * call on a device looks the array's device address up.  Every call on one
+ * device shares that array: calls that overlap on one device race.
+ * No counterpart in the reference: this entry point is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  Other arguments and results as in
+ * ssa_pset. */
+int ssa_pset_noalloc(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
+                     int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
+                     const double* detail_b, int enc_pages, const float* wq, const float* risk,
+                     const float* probe_lse, uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads,
+                     int n_heads, double* gain, int32_t* info, double* scores, long long* stats, int total_heads,
+                     int blocks, int pages, int count, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

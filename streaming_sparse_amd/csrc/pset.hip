@@ -23,6 +23,8 @@
 // mass-weighted mean cancels in every delta, VR/reader_reduce.py:55-56).
 #include "common.h"
 
+#include <mutex>
+
 using namespace ssa;
 
 namespace {
@@ -880,12 +882,17 @@ int ssa_encode(const void* keys, const void* mean, const void* detail, const voi
   return (int)hipGetLastError();
 }
 
-int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
-             int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
-             const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,
-             uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand,
-             double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
-             int total_heads, int blocks, int pages, int count, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The three launches of one Full_Pset correction, after argument checks.
+int pset_launch(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
+                int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
+                const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,
+                uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand,
+                double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
+                int total_heads, int blocks, int pages, int count, hipStream_t stream) {
   if (n_heads <= 0 || n_heads > total_heads || blocks <= 0 || pages > kMaxPages || pages <= kAnchors + kCurrent ||
       head_pages < pages || enc_pages < pages || count < 1 || count > pages || pages - count < 64 ||
       heads == nullptr || probe_lse == nullptr || cand == nullptr || rows == nullptr || pool == nullptr ||
@@ -927,6 +934,81 @@ int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, l
   hipLaunchKernelGGL(pset_rows_kernel, dim3(n_heads * np * kSplit), dim3(256), 0, stream, p);
   hipLaunchKernelGGL(pset_scores_kernel, dim3(n_heads * blocks), dim3(256), 0, stream, p);
   return (int)hipGetLastError();
+}
+
+// Scratch of the allocation-free entry point: for at most kScratchRows
+// scoped (head, query block) rows, the candidate endpoint data
+// [rows,16,48,34] fp64, then the split row partials [rows,16,2,52] fp64, then
+// the pools [rows,64] int32, each region at a fixed offset (48.05 MB in all).
+// Every entry a call reads is written earlier in the same call (the pool
+// kernel writes all 48 slots of each row, the rows kernel the candidates'
+// endpoint data and every row partial), so nothing in it must start at zero.
+constexpr int kScratchRows = 216;   // 3 heads x 72 query blocks
+constexpr size_t kCandRowBytes = (size_t)16 * kCand * kCandVals * sizeof(double);
+constexpr size_t kRowsRowBytes = (size_t)16 * kSplit * kRowPart * sizeof(double);
+constexpr size_t kPoolRowBytes = (size_t)kPoolInts * sizeof(int32_t);
+constexpr size_t kScratchRowsOff = kScratchRows * kCandRowBytes;
+constexpr size_t kScratchPoolOff = kScratchRowsOff + kScratchRows * kRowsRowBytes;
+constexpr size_t kScratchBytes = kScratchPoolOff + kScratchRows * kPoolRowBytes;
+static_assert(kCandRowBytes % 256 == 0 && kRowsRowBytes % 256 == 0, "regions stay 256-byte aligned");
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+// Device address of `scratch` on each device, looked up once per device with
+// that device current (the array's name in host code is only a stand-in).
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+uint8_t* scratch_ptr[kMaxDevices] = {};
+
+int device_scratch(uint8_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    scratch_ptr[dev] = (uint8_t*)ptr;
+  }
+  *out = scratch_ptr[dev];
+  return (int)hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
+             int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
+             const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,
+             uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand,
+             double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
+             int total_heads, int blocks, int pages, int count, hipStream_t stream) {
+  return pset_launch(q, q_head_stride, q_block_stride, q_row_stride, gathered, keys, head_pages, coef, mean_b,
+                     detail_b, enc_pages, wq, risk, probe_lse, mask, ids, own, heads, n_heads, cand, rows, pool, gain,
+                     info, scores, stats, total_heads, blocks, pages, count, stream);
+}
+
+int ssa_pset_noalloc(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
+                     int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
+                     const double* detail_b, int enc_pages, const float* wq, const float* risk,
+                     const float* probe_lse, uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads,
+                     int n_heads, double* gain, int32_t* info, double* scores, long long* stats, int total_heads,
+                     int blocks, int pages, int count, hipStream_t stream) {
+  if (n_heads <= 0 || blocks <= 0 || (long long)n_heads * blocks > kScratchRows) return (int)hipErrorInvalidValue;
+  uint8_t* base = nullptr;
+  const int e = device_scratch(&base);
+  if (e != (int)hipSuccess) return e;
+  return pset_launch(q, q_head_stride, q_block_stride, q_row_stride, gathered, keys, head_pages, coef, mean_b,
+                     detail_b, enc_pages, wq, risk, probe_lse, mask, ids, own, heads, n_heads, (double*)base,
+                     (double*)(base + kScratchRowsOff), (int32_t*)(base + kScratchPoolOff), gain, info, scores,
+                     stats, total_heads, blocks, pages, count, stream);
 }
 
 }  // extern "C"

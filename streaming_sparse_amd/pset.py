@@ -105,11 +105,14 @@ def encode(summary: Summary, basis: torch.Tensor, reader: Reader, out: Encoding 
 
 @torch.no_grad()
 def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, lse, mask, ids, own, heads,
-            workspace=None, want_scores=False):
+            workspace=None, want_scores=False, no_alloc=False):
     """Full_Pset correction of the scoped `heads` in place on `mask` (uint8 or
     bool storage, [H,T,P]) and `ids` [H,T,C] from the intersection router,
     whose `risk` and per-probe `lse` ([H,T,16], route(..., lse_out=...)) it
     reads.  q [1,N,H,128] bf16 (probe rows at the reference offsets).
+    no_alloc: run ssa_pset_noalloc, whose scratch is the library's own
+    device array (at most 216 scoped (head, block) rows; concurrent calls on
+    one device race), instead of workspace scratch.
     Returns (stats int64 [3] = executed, rows, non-finite scores; per-row
     dict)."""
     _, nq, h, d = q.shape
@@ -138,20 +141,24 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, lse, 
             return torch.empty(shape, device=dev, dtype=dtype)
         return workspace.tensor('pset_' + name, shape, dev, dtype)
 
-    cand = buf('cand', (n, t, 16, CAND, CAND_VALS), torch.float64)
-    rows = buf('rows', (n, t, 16, ROW_SPLIT, ROW_VALS), torch.float64)
-    pool = buf('pool', (n, t, POOL_INTS), torch.int32)
     gain = buf('gain', (n, t), torch.float64)
     info = buf('info', (n, t, 3), torch.int32)
     scores = buf('scores', (n, t, 16, 32), torch.float64) if want_scores else None
     stats = buf('stats', (3,), torch.int64)
     mask_u8 = mask.view(torch.uint8) if mask.dtype == torch.bool else mask
     ow = None if own is None else own.to(device=dev, dtype=torch.int32).contiguous()
-    _lib.check(_lib.lib().ssa_pset(
-        _lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys), hp, _lib.ptr(encoding.coef),
-        _lib.ptr(encoding.mean), _lib.ptr(encoding.detail), encoding.coef.shape[1], _lib.ptr(reader.wq),
-        _lib.ptr(risk), _lib.ptr(lse), _lib.ptr(mask_u8), _lib.ptr(ids), _lib.ptr(ow), _lib.ptr(hs), n, _lib.ptr(cand),
-        _lib.ptr(rows), _lib.ptr(pool), _lib.ptr(gain), _lib.ptr(info), _lib.ptr(scores), _lib.ptr(stats), h, t, p,
-        ids.shape[-1], _lib.stream_handle(dev)), "ssa_pset")
+    head = (_lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys), hp, _lib.ptr(encoding.coef),
+            _lib.ptr(encoding.mean), _lib.ptr(encoding.detail), encoding.coef.shape[1], _lib.ptr(reader.wq),
+            _lib.ptr(risk), _lib.ptr(lse), _lib.ptr(mask_u8), _lib.ptr(ids), _lib.ptr(ow), _lib.ptr(hs), n)
+    tail = (_lib.ptr(gain), _lib.ptr(info), _lib.ptr(scores), _lib.ptr(stats), h, t, p, ids.shape[-1],
+            _lib.stream_handle(dev))
+    pool = None
+    if no_alloc:
+        _lib.check(_lib.lib().ssa_pset_noalloc(*head, *tail), "ssa_pset_noalloc")
+    else:
+        cand = buf('cand', (n, t, 16, CAND, CAND_VALS), torch.float64)
+        rows = buf('rows', (n, t, 16, ROW_SPLIT, ROW_VALS), torch.float64)
+        pool = buf('pool', (n, t, POOL_INTS), torch.int32)
+        _lib.check(_lib.lib().ssa_pset(*head, _lib.ptr(cand), _lib.ptr(rows), _lib.ptr(pool), *tail), "ssa_pset")
     return stats, dict(gain=gain, executed=info[..., 0], argmax=info[..., 1], nonfinite=info[..., 2],
                        scores=scores, pool=pool)

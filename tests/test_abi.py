@@ -21,7 +21,8 @@ def declared():
 
 
 def test_header_declares_entry_points():
-    assert set(declared()) == {"ssa_rep_values", "ssa_attention", "ssa_route", "ssa_encode", "ssa_pset", "ssa_summary"}
+    assert set(declared()) == {"ssa_rep_values", "ssa_attention", "ssa_route", "ssa_encode", "ssa_pset", "ssa_summary",
+                               "ssa_pset_noalloc"}
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libssattn.so not built")
