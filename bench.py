@@ -401,27 +401,35 @@ def intersection_lines(args, dense_ms, iters):
     return out
 
 
-def chunk_line(args, chunks=2):
-    """Total attention time of one 3-frame chunk of a 30-layer stack: 4
-    denoise steps (layer 0 dense, layers 1-29 intersection route, Full_Pset on
-    layers {3,4,5,8,14,17,27} x heads {3,4,9} at step 0, current-page
-    summaries each call) and the dense clean commit pass, against the same
-    chunk fully dense (this library's kernel with every page exact, and
-    torch scaled_dot_product_attention)."""
+def chunk_line(args):
+    """Total attention-path time of one 3-frame chunk of a 30-layer stack on
+    the rolling 432-page window: 4 denoise steps (layer 0 dense, layers 1-29
+    current-page summaries + intersection route + attention, Full_Pset on
+    layers {3,4,5,8,14,17,27} x heads {3,4,9} at step 0) and the clean step
+    (every layer dense, then the commit of the chunk's 72 pages, summaries
+    and encodings into the ring), plus the anchor rebase.  Chunks 0-5 fill
+    the window untimed; chunk 6 is the first with a full window after the
+    ring wrapped and the anchor was rebased, and is the one timed.  Beside it
+    the same chunk's calls fully dense (this library's kernel with every page
+    exact, and torch scaled_dot_product_attention)."""
     import torch
-    from streaming_sparse_amd.runtime import ChunkConfig, ChunkRuntime
+    from streaming_sparse_amd.runtime import StreamConfig, StreamRuntime
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
     t0 = time.time()
-    rt = ChunkRuntime(ChunkConfig(frames=args.frames), dev)
+    rt = StreamRuntime(StreamConfig(history_pages=24 * args.frames - 72), dev)
+    for c in range(6):
+        rt.run_chunk(rt.chunk_inputs())
+        torch.cuda.synchronize()
     setup_s = time.time() - t0
-    rt.run_chunk()
-    torch.cuda.synchronize()
-    chunk_ms = time_loop(rt.run_chunk, chunks, stream)
-    dense_kernel_ms = time_loop(lambda: rt.run_dense_chunk(False), 1, stream)
-    dense_sdpa_ms = time_loop(lambda: rt.run_dense_chunk(True), 1, stream)
+    inputs = rt.chunk_inputs()
+    dense_kernel_ms = time_loop(lambda: rt.run_dense_chunk(inputs, False), 1, stream)
+    dense_sdpa_ms = time_loop(lambda: rt.run_dense_chunk(inputs, True), 1, stream)
     calls = rt.calls_per_chunk()
-    return {"workload": "30 layers x (4 denoise steps + clean commit), 432-page window, 12 heads",
+    torch.cuda.synchronize()
+    chunk_ms = time_loop(lambda: rt.run_chunk(inputs), 1, stream)
+    return {"workload": f"30 layers x (4 denoise steps + clean commit), rolling {rt.cap}-page window, 12 heads; "
+                        f"chunk 6 (window full, ring wrapped, anchor rebased)",
             "calls": calls, "chunk_ms": round(chunk_ms, 3),
             "dense_chunk_ms_this_kernel": round(dense_kernel_ms, 3),
             "dense_chunk_ms_sdpa": round(dense_sdpa_ms, 3),

@@ -150,6 +150,29 @@ int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, l
              double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
              int total_heads, int blocks, int pages, int count, hipStream_t stream);
 
+/* Anchor rebase (LE/anchor_rebase.py:8-18 shift_temporal_, as VB/phase.py:4-25
+ * applies it to the cache's first frame): for `tokens` rows x `heads` of
+ * 128-dim bf16 keys (src, dst addressed token*stride + head*stride + dim,
+ * 4-byte aligned, even strides; dst may equal src), complex pair j < pairs
+ * (dims 2j, 2j+1: the temporal RoPE pairs) is multiplied in fp64 by phase[j]
+ * = (cos, sin) [pairs][2] (the rope table row of the offset) and rounded to
+ * bf16 through fp32; the other dims are copied. */
+int ssa_anchor_rebase(const void* src, long long src_token_stride, long long src_head_stride, void* dst,
+                      long long dst_token_stride, long long dst_head_stride, const double* phase, int pairs,
+                      int tokens, int heads, hipStream_t stream);
+
+/* Commit of a chunk's pages into the ring slots of the resident K/V cache
+ * (RV/runtime.py:22-55 PageStore.commit / commit_indexed): row r of
+ * destination page slots[p] (p < chunk_pages, slots[p] < dst_pages) takes
+ * chunk token order[h, 64p + r] (order [H, 64 chunk_pages] int32, NULL: token
+ * 64p + r) of head h, for K and V (token-major [tokens, H, 128] sources,
+ * destinations addressed like ssa_attention's k/v; 16-byte aligned).  The
+ * sources must not overlap the destination rows. */
+int ssa_commit_pages(const void* k_src, const void* v_src, long long src_token_stride, long long src_head_stride,
+                     const int32_t* order, int chunk_pages, const int32_t* slots, int dst_pages, void* k_dst,
+                     void* v_dst, long long dst_token_stride, long long dst_head_stride, int heads,
+                     hipStream_t stream);
+
 /* ssa_pset without the caller-owned scratch (cand, rows, pool): the library
  * keeps that scratch in a file-scope device array of 48.05 MB per device
  * (held until the process ends), sized for n_heads * blocks <= 216 scoped rows

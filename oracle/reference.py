@@ -261,6 +261,25 @@ def dense_attention(q, k, v, dtype=torch.float32, chunk=512):
     return out.transpose(0, 1)[None]
 
 
+# ---------------------------------------------------------------- stream ----
+
+def shift_temporal(keys, tokens, freqs, offset):
+    """Anchor rebase (LE/anchor_rebase.py:8-18 shift_temporal_, applied by
+    VB/phase.py:4-25): the first `tokens` rows of keys [1, L, H, D] get their
+    temporal RoPE pairs (the first D/2 - 2 (D/2 // 3) complex pairs)
+    multiplied by freqs[offset, :pairs] in complex128 and cast back to the
+    keys' dtype; the spatial pairs and the other rows stay bitwise equal.
+    Returns a new tensor."""
+    out = keys.clone()
+    if offset == 0 or tokens == 0:
+        return out
+    pairs = keys.shape[-1] // 2 - 2 * (keys.shape[-1] // 2 // 3)
+    part = out[:, :tokens, :, :pairs * 2]
+    z = torch.view_as_complex(part.double().reshape(*part.shape[:-1], pairs, 2).contiguous())
+    part.copy_(torch.view_as_real(z * freqs[offset, :pairs]).flatten(-2).to(keys.dtype))
+    return out
+
+
 # ---------------------------------------------------------------- checks ----
 
 def near_tie_rows(risk_, boundary, rel=1e-3):

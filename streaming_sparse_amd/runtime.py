@@ -1,66 +1,116 @@
-"""Per-chunk driver of the page-sparse attention path over a stack of layers.
+"""Streaming driver of the page-sparse attention path over a stack of layers,
+with a rolling KV window.
 
-Mirrors the attention part of the reference's streaming runtime
-(local_experiments/video_runtime_v1/runtime.py:169-350,
-reproduction/vbench_current/queue_policy.py:11-56) for one 3-frame chunk:
+Mirrors the attention side of the reference's streaming runtime:
+local_experiments/video_runtime_v1/runtime.py:169-370 (VideoRuntime.forward,
+commit_group), local_experiments/review_v1/runtime.py:14-55 (PageStore, the
+ring of history pages), reproduction/vbench_current/phase.py:4-25 with
+local_experiments/anchor_rebase.py:8-18 (anchor rebase) and
+reproduction/vbench_current/queue_policy.py:11-56 (quota schedule).
 
-* 4 denoise steps; per step and layer one attention call over the layer's
-  resident window of P pages:
-  - layer 0 is dense (runtime.py:209-211), run by the same fused kernel with
-    every page exact;
-  - layers 1.. refresh the current chunk's 72 page summaries (runtime.py:213-227),
-    route with the intersection quotas of their (step, layer) (graph.py:150-151),
-    correct the scheduled heads with Full_Pset at the scheduled (layer, step)
-    (runtime.py:228, graph.py:169-208), then attend;
-* the clean commit pass: every layer dense again, then the new 72 pages'
-  summaries and, on Full_Pset layers, their encodings (runtime.py:328-370;
-  pages stay chronological).
+Each layer keeps a resident K/V cache of history_pages + 72 pages and a
+summary slab of the same capacity.  A 3-frame chunk of 72 pages runs:
 
-The K/V window of each layer is resident in HBM; each (step, layer) call gets
-its own queries.  Timings cover the attention-path kernels only (no QKV
-projection, cache writes or window roll).
+* from chunk 6 on (the window is full), the anchor rebase: the first frame's
+  keys (24 pages, never overwritten) are re-rotated from their state after
+  chunk 0's commit so that the current frames sit 15..17 frames from the
+  anchor (offset 3c - 15, VB history/*/video.py), and the anchor pages'
+  summaries (and Full_Pset encodings) are rebuilt from them (VB/phase.py);
+* 4 denoise steps and the clean step; at each, every layer gets the chunk's
+  K/V written after its n valid history pages (pages [n, n + 72)) and runs one
+  attention call over the window of P = n + 72 pages:
+  - dense (every page exact, the same fused kernel) for layer 0, for the
+    clean step and while the history holds at most 72 pages
+    (runtime.py:209-211);
+  - otherwise the current pages' summaries are rebuilt, Full_Pset encodings
+    too where scheduled, then the intersection router with the
+    (window, step, layer) quotas, Full_Pset on the scheduled heads
+    (runtime.py:213-257, graph.py:169-210), and the attention;
+* the commit of the clean step: per layer, the chunk's pages are written into
+  the ring slots (PageStore.commit_slots: after the first commit the slots
+  wrap inside [24, history_pages), so the anchor frame stays), then their
+  summaries and, on Full_Pset layers, encodings at those slots
+  (runtime.py:356-370).
+
+Q/K/V are seeded N(0, 1) with Wan RoPE at the chunk's absolute frames,
+generated on the device before the chunk runs; writing K/V into the cache
+stands in for the projection that writes them there in the reference.
 """
 from __future__ import annotations
 
-import math
-import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import torch
 
-from . import pset, summary, workload
+from . import _lib, pset, summary, workload
 from .attention import Workspace
-from .legacy_components import attention, rep_values
+from .legacy_components import HEAD_DIM, attention, kv_strides
 from .ops import Summary
 from .route import route
 
 ANCHORS = 24
 CURRENT = 72
+ANCHOR_TOKENS = ANCHORS * 64
 PSET_LAYERS = (3, 4, 5, 8, 14, 17, 27)
 PSET_HEADS = (3, 4, 9)
 PSET_STEPS = (0,)
+TEMPORAL_PAIRS = 22          # complex RoPE pairs of the temporal axis at head_dim 128
+REBASE_FROM_CHUNK = 6        # first chunk whose window is full and whose anchor is rebased
 
 
 @dataclass
-class Layer:
-    k: torch.Tensor
-    v: torch.Tensor
-    summary: Summary
-    basis: torch.Tensor
-    encoding: pset.Encoding | None = None
-
-
-@dataclass
-class ChunkConfig:
+class StreamConfig:
     layers: int = 30
-    frames: int = 18
     heads: int = 12
     steps: int = 4
+    history_pages: int = 360       # with the 72 current pages: a 432-page (18-frame) window
+    sink_pages: int = 24           # the anchor frame, kept out of the ring's wrap
     seed: int = 4
     pset_layers: tuple = PSET_LAYERS
     pset_heads: tuple = PSET_HEADS
     pset_steps: tuple = PSET_STEPS
     quota_mean: float = 40.8
+    sparse_start_chunks: tuple = ()   # chunks with <= 72 history pages that still run sparse
+
+
+class PageRing:
+    """Ring bookkeeping of the history pages (RV/runtime.py:14-46): `n`
+    valid pages, the next write page and the commit count.  The first commit
+    writes pages [0, 72); later ones wrap inside [sink, history_pages)."""
+
+    def __init__(self, history_pages: int, sink_pages: int):
+        if history_pages < CURRENT + sink_pages or history_pages % 1 or sink_pages < 0:
+            raise ValueError("history_pages must hold a chunk beyond the sink")
+        self.history_pages = history_pages
+        self.sink = sink_pages
+        self.n = self.write = self.commits = 0
+
+    def commit_slots(self) -> list:
+        sink = self.sink if self.commits else 0
+        span = self.history_pages - sink
+        return [sink + (self.write + i - sink) % span for i in range(CURRENT)]
+
+    def commit(self):
+        end = self.write + CURRENT
+        self.write = self.sink + (end - self.sink) % (self.history_pages - self.sink)
+        self.n = min(self.history_pages, self.n + CURRENT)
+        self.commits += 1
+
+
+def runs(slots) -> list:
+    """Contiguous runs (first slot, length, offset into the chunk) of a slot list."""
+    out = []
+    for i, s in enumerate(slots):
+        if out and s == out[-1][0] + out[-1][1]:
+            out[-1][1] += 1
+        else:
+            out.append([s, 1, i])
+    return [tuple(r) for r in out]
+
+
+def rebase_offset(chunk: int) -> int:
+    """Temporal shift of the anchor frame for a chunk (0 before the window is full)."""
+    return 3 * chunk - 15 if chunk >= REBASE_FROM_CHUNK else 0
 
 
 def _rope_on_device(x, first_frame, freqs):
@@ -81,113 +131,229 @@ def _rope_on_device(x, first_frame, freqs):
     return torch.view_as_real(z * f).reshape(L, H, D)
 
 
-class ChunkRuntime:
-    """Resident state of every layer plus the per-(step, layer) queries of
-    one chunk, all generated on the device from seeds."""
+@dataclass
+class Layer:
+    k: torch.Tensor             # [1, 64 (history + 72), H, 128] bf16 resident cache
+    v: torch.Tensor
+    slab: Summary               # [H, history + 72, ...]
+    basis: torch.Tensor         # [H, 128, 8] bf16
+    encoding: pset.Encoding | None = None
+    canonical: torch.Tensor | None = None   # anchor keys after chunk 0's commit [1536, H, 128] bf16
 
-    def __init__(self, cfg: ChunkConfig, device, reader_weights=None):
+
+class StreamRuntime:
+    """Resident per-layer state of a stream of 3-frame chunks."""
+
+    def __init__(self, cfg: StreamConfig, device, reader_weights=None):
         self.cfg = cfg
         dev = torch.device(device)
         self.device = dev
-        self.P = cfg.frames * workload.PAGES_PER_FRAME
-        self.H = cfg.heads
-        self.N = workload.QUERY_FRAMES * workload.TOKENS_PER_FRAME
-        self.T = self.N // 64
-        P, H, D = self.P, self.H, workload.HEAD_DIM
-        freqs = workload.rope_table(D).to(torch.complex64).to(dev)
-        g = torch.Generator(device=dev).manual_seed(workload.seed_for(cfg.seed))
+        H, D = cfg.heads, HEAD_DIM
+        self.H = H
+        self.cap = cfg.history_pages + CURRENT
+        self.N = CURRENT * 64
+        self.T = CURRENT
+        self.ring = PageRing(cfg.history_pages, cfg.sink_pages)
+        self.chunk = 0
+        self.freqs = workload.rope_table(D)                      # complex128, CPU
+        self.freqs_dev = self.freqs.to(torch.complex64).to(dev)
         self.reader = pset.Reader(reader_weights or workload.reader_weights(cfg.seed), dev)
         self.ws = Workspace()
         self.layers = []
         for layer in range(cfg.layers):
-            k = _rope_on_device(torch.randn(64 * P, H, D, generator=g, device=dev), 0, freqs)
-            v = torch.randn(64 * P, H, D, generator=g, device=dev)
-            k = k.to(torch.bfloat16)[None].contiguous()
-            v = v.to(torch.bfloat16)[None].contiguous()
-            # contiguous bf16 once here, so no call of the chunk copies it
-            basis = workload.pca_basis(v[0].transpose(0, 1).reshape(H, P, 64, D).float()).to(torch.bfloat16).contiguous()
-            slab = Summary(torch.empty(H, P, 4, D, device=dev, dtype=torch.bfloat16),
-                           torch.empty(H, P, D, device=dev, dtype=torch.bfloat16),
-                           torch.empty(H, P, 3, 8, device=dev, dtype=torch.bfloat16),
-                           torch.empty(H, P, 4, 12, device=dev, dtype=torch.bfloat16))
-            init = workload.kmeans_init(H, P, torch.Generator().manual_seed(workload.seed_for(cfg.seed, layer, 0, 1)))
-            summary.build(k, v, basis, init.to(dev), slab, 0, P)
-            enc = pset.encode(slab, basis, self.reader) if layer in cfg.pset_layers else None
+            g = torch.Generator().manual_seed(workload.seed_for(cfg.seed, layer, 0, 2))
+            sample = torch.randn(H, ANCHORS, 64, D, generator=g)
+            basis = workload.pca_basis(sample).to(torch.bfloat16).to(dev).contiguous()
+            k = torch.zeros(1, 64 * self.cap, H, D, device=dev, dtype=torch.bfloat16)
+            v = torch.zeros_like(k)
+            slab = Summary(torch.zeros(H, self.cap, 4, D, device=dev, dtype=torch.bfloat16),
+                           torch.zeros(H, self.cap, D, device=dev, dtype=torch.bfloat16),
+                           torch.zeros(H, self.cap, 3, 8, device=dev, dtype=torch.bfloat16),
+                           torch.zeros(H, self.cap, 4, 12, device=dev, dtype=torch.bfloat16))
+            enc = pset.Encoding.empty(H, self.cap, dev) if layer in cfg.pset_layers else None
             self.layers.append(Layer(k, v, slab, basis, enc))
-        self.q = [[_rope_on_device(torch.randn(self.N, H, D, generator=g, device=dev), cfg.frames - 3, freqs)
-                   .to(torch.bfloat16)[None].contiguous() for _ in range(cfg.layers)] for _ in range(cfg.steps + 1)]
-        self.init_current = workload.kmeans_init(H, CURRENT, torch.Generator().manual_seed(
-            workload.seed_for(cfg.seed, 0, 0, 9))).to(device=dev, dtype=torch.int32)
-        quotas = workload.quota_table(cfg.seed, layers=max(cfg.layers - 1, 1), steps=cfg.steps, heads=H,
-                                      mean_total=cfg.quota_mean)
-        self.quota_a = quotas[..., 0].to(torch.int32).to(dev)           # [steps, layers-1, H]
-        self.quota_n = quotas[..., 0, :].sum(-1).tolist()                # [steps][layers-1]
+        self.init = workload.kmeans_init(H, CURRENT, torch.Generator().manual_seed(
+            workload.seed_for(cfg.seed, 0, 0, 9))).to(device=dev, dtype=torch.int32).contiguous()
         self.theta = torch.tensor([1.0, 1.0, 1.0, 0.5], device=dev).expand(H, 4).contiguous()
         self.lse = torch.empty(H, self.T, 16, device=dev)
-        own = torch.arange(self.T, device=dev) + P - self.T
-        rest = torch.arange(P, device=dev)
-        dense = torch.cat([own[:, None], rest[None].expand(self.T, -1)], 1)
-        keep = dense != own[:, None]
-        keep[:, 0] = True
-        self.dense_ids = dense[keep].reshape(self.T, P)[None].expand(H, -1, -1).to(torch.int32).contiguous()
+        self.own = None
+        self.quotas = {}
+        self.last = {}                # ids / out of the most recent call, for inspection
+        self.calls = dict(sparse=0, dense=0, full_pset=0)
 
-    def dense_call(self, layer: int, q):
-        L = self.layers[layer]
-        return attention(q, L.k, L.v, L.summary, L.basis, self.dense_ids, self.ws, all_pages=True)
+    # ------------------------------------------------------------- inputs --
 
-    def sparse_call(self, layer: int, step: int, q):
-        """One sparse attention call (layers >= 1): current summaries,
-        encodings when Full_Pset is scheduled, route (+ correction), attend."""
-        cfg, L, P = self.cfg, self.layers[layer], self.P
-        correct = layer in cfg.pset_layers and step in cfg.pset_steps
-        summary.build(L.k, L.v, L.basis, self.init_current, L.summary, P - CURRENT, CURRENT)
-        if correct:
-            pset.encode(L.summary, L.basis, self.reader, out=L.encoding, first=P - CURRENT, pages=CURRENT)
-        a = self.quota_a[step, layer - 1]
-        n = int(self.quota_n[step][layer - 1])
-        vrep = self.ws.tensor('rt_rep_values', (L.summary.mean.shape[0], P, 4, 128), q.device, torch.bfloat16)
-        ids, _, _, stats = route(q, L.summary, self.theta, tier='intersection', current_slots=a, n=n,
-                                 workspace=self.ws, want_mask=correct, lse_out=self.lse if correct else None,
-                                 full_pset=cfg.pset_heads if correct else None, encoding=L.encoding,
-                                 reader=self.reader, rep_basis=L.basis, rep_out=vrep)
-        return attention(q, L.k, L.v, L.summary, L.basis, ids, self.ws, rep_values=vrep)
-
-    def commit(self, layer: int, q):
-        """Clean step: dense attention, then the new pages' summaries (and
-        encodings on Full_Pset layers)."""
-        out = self.dense_call(layer, q)
-        L, P = self.layers[layer], self.P
-        summary.build(L.k, L.v, L.basis, self.init_current, L.summary, P - CURRENT, CURRENT)
-        if L.encoding is not None:
-            pset.encode(L.summary, L.basis, self.reader, out=L.encoding, first=P - CURRENT, pages=CURRENT)
+    def chunk_inputs(self, chunk: int | None = None):
+        """Seeded Q/K/V of every (step, layer) of a chunk, RoPE at its absolute
+        frames 3c..3c+2: list [steps + 1][layers] of (q [1,N,H,D], k, v
+        [N,H,D]) bf16 device tensors."""
+        c = self.chunk if chunk is None else chunk
+        cfg = self.cfg
+        dev = self.device
+        out = []
+        for step in range(cfg.steps + 1):
+            row = []
+            for layer in range(cfg.layers):
+                g = torch.Generator(device=dev).manual_seed(
+                    workload.seed_for(cfg.seed, layer, step, 1000 + 3 * c))
+                q, k, v = (torch.randn(self.N, self.H, HEAD_DIM, generator=g, device=dev) for _ in range(3))
+                q = _rope_on_device(q, 3 * c, self.freqs_dev).to(torch.bfloat16)[None].contiguous()
+                k = _rope_on_device(k, 3 * c, self.freqs_dev).to(torch.bfloat16).contiguous()
+                row.append((q, k, v.to(torch.bfloat16).contiguous()))
+            out.append(row)
         return out
 
-    def run_chunk(self):
-        for step in range(self.cfg.steps):
-            for layer in range(self.cfg.layers):
-                q = self.q[step][layer]
-                if layer == 0:
-                    self.dense_call(layer, q)
-                else:
-                    self.sparse_call(layer, step, q)
-        for layer in range(self.cfg.layers):
-            self.commit(layer, self.q[self.cfg.steps][layer])
+    def quota(self, chunk: int):
+        if chunk not in self.quotas:
+            tab = workload.quota_table(self.cfg.seed, layers=max(self.cfg.layers - 1, 1), steps=self.cfg.steps,
+                                       heads=self.H, mean_total=self.cfg.quota_mean, window=chunk)
+            self.quotas[chunk] = (tab[..., 0].to(torch.int32).to(self.device), tab[..., 0, :].sum(-1).tolist())
+        return self.quotas[chunk]
 
-    def run_dense_chunk(self, sdpa=False):
-        """The dense baseline: every call of the chunk dense (our kernel with
-        all pages exact, or torch's scaled_dot_product_attention)."""
+    # ------------------------------------------------------------ chunk ----
+
+    def begin_chunk(self):
+        """The chunk's commit slots on the device, and the anchor rebase from
+        the window-full chunk on (VB/phase.py:4-25)."""
+        c = self.chunk
+        self.slots = self.ring.commit_slots()
+        key = ('rt_slots', (CURRENT,), self.device, torch.int32)
+        if key not in self.ws.entries:
+            self.ws.entries[key] = torch.empty(CURRENT, device=self.device, dtype=torch.int32)
+        self.slots_dev = self.ws.entries[key]
+        self.slots_dev.copy_(torch.tensor(self.slots, dtype=torch.int32))
+        if c >= REBASE_FROM_CHUNK:
+            self.rebase_anchor(rebase_offset(c))
+
+    def rebase_anchor(self, offset: int):
+        """Anchor keys of every layer = the chunk-0 anchor keys with the
+        temporal RoPE pairs shifted by `offset` frames; the anchor pages'
+        summaries and encodings rebuilt from them."""
+        ph = self.freqs[offset, :TEMPORAL_PAIRS]
+        phase = torch.view_as_real(ph).to(torch.float64).contiguous().to(self.device)
+        H = self.H
+        for li, L in enumerate(self.layers):
+            src = L.canonical
+            tok, head = kv_strides(L.k, L.v)
+            _lib.check(_lib.lib().ssa_anchor_rebase(_lib.ptr(src), H * HEAD_DIM, HEAD_DIM, _lib.ptr(L.k), tok, head,
+                                                    _lib.ptr(phase), TEMPORAL_PAIRS, ANCHOR_TOKENS, H,
+                                                    _lib.stream_handle(self.device)), "ssa_anchor_rebase")
+            summary.build(L.k, L.v, L.basis, self.init[:, :ANCHORS], L.slab, 0, ANCHORS)
+            if L.encoding is not None:
+                pset.encode(L.slab, L.basis, self.reader, out=L.encoding, first=0, pages=ANCHORS)
+
+    def dense_window(self, chunk: int | None = None) -> bool:
+        n = self.ring.n
+        c = self.chunk if chunk is None else chunk
+        return n <= CURRENT and c not in self.cfg.sparse_start_chunks
+
+    def layer_call(self, step: int, layer: int, q, k, v):
+        """One attention call of the current chunk: the chunk's K/V written into
+        the window, then a dense or sparse call; the clean step commits."""
+        cfg, L = self.cfg, self.layers[layer]
+        n = self.ring.n
+        P = n + CURRENT
+        tok0 = 64 * n
+        L.k[0, tok0:tok0 + self.N].copy_(k)
+        L.v[0, tok0:tok0 + self.N].copy_(v)
+        kw = L.k[:, :64 * P]
+        vw = L.v[:, :64 * P]
+        s = L.slab.slice(0, P)
+        clean = step == cfg.steps
+        if clean or layer == 0 or self.dense_window():
+            out = attention(q, kw, vw, s, L.basis, self.dense_ids(P), self.ws, all_pages=True)
+            self.calls['dense'] += 1
+        else:
+            out = self.sparse_call(step, layer, q, kw, vw, P)
+        self.last = dict(step=step, layer=layer, pages=P, out=out)
+        if clean:
+            self.commit(layer, k, v)
+        return out
+
+    def sparse_call(self, step, layer, q, kw, vw, P):
+        cfg, L = self.cfg, self.layers[layer]
+        correct = L.encoding is not None and step in cfg.pset_steps
+        summary.build(L.k, L.v, L.basis, self.init, L.slab, P - CURRENT, CURRENT)
+        s = L.slab.slice(0, P)
+        if correct:
+            pset.encode(L.slab, L.basis, self.reader, out=L.encoding, first=P - CURRENT, pages=CURRENT)
+        a_tab, n_tab = self.quota(self.chunk)
+        a = a_tab[step, layer - 1]
+        n = int(n_tab[step][layer - 1])
+        vrep = self.ws.tensor('rt_rep_values', (self.H, P, 4, HEAD_DIM), q.device, torch.bfloat16)
+        ids, _, _, _ = route(q, s, self.theta, tier='intersection', current_slots=a, n=n, workspace=self.ws,
+                             want_mask=correct, lse_out=self.lse if correct else None,
+                             full_pset=cfg.pset_heads if correct else None, encoding=L.encoding,
+                             reader=self.reader, rep_basis=L.basis, rep_out=vrep)
+        self.calls['sparse'] += 1
+        self.calls['full_pset'] += int(correct)
+        self.last_ids = ids
+        return attention(q, kw, vw, s, L.basis, ids, self.ws, rep_values=vrep)
+
+    def commit(self, layer: int, k, v):
+        """The chunk's pages into the ring slots, then their summaries and
+        (Full_Pset layers) encodings at those slots (VR/runtime.py:356-370)."""
+        L = self.layers[layer]
+        tok, head = kv_strides(L.k, L.v)
+        _lib.check(_lib.lib().ssa_commit_pages(_lib.ptr(k), _lib.ptr(v), self.H * HEAD_DIM, HEAD_DIM, None, CURRENT,
+                                               _lib.ptr(self.slots_dev), self.cap, _lib.ptr(L.k), _lib.ptr(L.v), tok,
+                                               head, self.H, _lib.stream_handle(self.device)), "ssa_commit_pages")
+        for first, length, off in runs(self.slots):
+            summary.build(L.k, L.v, L.basis, self.init[:, off:off + length], L.slab, first, length)
+            if L.encoding is not None:
+                pset.encode(L.slab, L.basis, self.reader, out=L.encoding, first=first, pages=length)
+
+    def end_chunk(self):
+        if self.chunk == 0:
+            for L in self.layers:
+                L.canonical = L.k[0, :ANCHOR_TOKENS].clone()
+        self.ring.commit()
+        self.chunk += 1
+
+    def run_chunk(self, inputs):
+        self.begin_chunk()
         for step in range(self.cfg.steps + 1):
             for layer in range(self.cfg.layers):
-                q = self.q[step][layer]
+                q, k, v = inputs[step][layer]
+                self.layer_call(step, layer, q, k, v)
+        self.end_chunk()
+
+    def run_dense_chunk(self, inputs, sdpa=False):
+        """The same chunk's calls, every one dense over the window (this
+        library's kernel with every page exact, or torch's
+        scaled_dot_product_attention); the ring is not advanced."""
+        n = self.ring.n
+        P = n + CURRENT
+        for step in range(self.cfg.steps + 1):
+            for layer in range(self.cfg.layers):
+                q, k, v = inputs[step][layer]
+                L = self.layers[layer]
+                L.k[0, 64 * n:64 * n + self.N].copy_(k)
+                L.v[0, 64 * n:64 * n + self.N].copy_(v)
+                kw, vw = L.k[:, :64 * P], L.v[:, :64 * P]
                 if sdpa:
-                    L = self.layers[layer]
                     torch.nn.functional.scaled_dot_product_attention(
-                        q[0].transpose(0, 1)[None], L.k[0].transpose(0, 1)[None], L.v[0].transpose(0, 1)[None])
+                        q[0].transpose(0, 1)[None], kw[0].transpose(0, 1)[None], vw[0].transpose(0, 1)[None])
                 else:
-                    self.dense_call(layer, q)
+                    attention(q, kw, vw, L.slab.slice(0, P), L.basis, self.dense_ids(P), self.ws, all_pages=True)
+
+    def dense_ids(self, P: int):
+        """Every page of a P-page window per block, own page (P - 72 + t) first."""
+        key = ('rt_dense_ids', (self.H, self.T, P), self.device, torch.int32)
+        if key not in self.ws.entries:
+            own = torch.arange(self.T) + P - self.T
+            rest = torch.arange(P)
+            ids = torch.cat([own[:, None], rest[None].expand(self.T, -1)], 1)
+            keep = ids != own[:, None]
+            keep[:, 0] = True
+            self.ws.entries[key] = ids[keep].reshape(self.T, P)[None].expand(self.H, -1, -1).to(
+                device=self.device, dtype=torch.int32).contiguous()
+        return self.ws.entries[key]
 
     def calls_per_chunk(self):
         cfg = self.cfg
-        sparse = cfg.steps * (cfg.layers - 1)
-        return dict(sparse=sparse, dense=cfg.steps + cfg.layers,
-                    full_pset=len([l for l in cfg.pset_layers if l < cfg.layers]) * len(cfg.pset_steps))
+        dense_window = self.dense_window()
+        sparse = 0 if dense_window else cfg.steps * (cfg.layers - 1)
+        return dict(sparse=sparse, dense=cfg.steps * cfg.layers + cfg.layers - sparse,
+                    full_pset=0 if dense_window else
+                    len([l for l in cfg.pset_layers if 0 < l < cfg.layers]) * len(cfg.pset_steps))

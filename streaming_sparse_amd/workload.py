@@ -211,11 +211,13 @@ def make_call(cfg: int, frames: int, layer: int = 1, step: int = 0, heads: int =
 
 
 def quota_table(cfg: int, layers: int = 29, steps: int = 4, heads: int = HEADS,
-                mean_total: float = 40.8, a_range=(4, 36), b_range=(0, 40)) -> torch.Tensor:
+                mean_total: float = 40.8, a_range=(4, 36), b_range=(0, 40), window: int = 0) -> torch.Tensor:
     """Seeded per-(step, layer, head) (A, B) exact-page quotas with A+B
-    constant over the heads of each (step, layer) and averaging `mean_total`.
-    Returns int64 [steps, layers, heads, 2]."""
-    g = torch.Generator().manual_seed(seed_for(cfg, 0, 0, 7))
+    constant over the heads of each (step, layer) and averaging `mean_total`;
+    `window` seeds one table per window position (chunk) of a stream, as the
+    reference's table has one per window.  Returns int64 [steps, layers,
+    heads, 2]."""
+    g = torch.Generator().manual_seed(seed_for(cfg, window, 0, 7))
     lo_n = a_range[0] + b_range[0]
     hi_n = a_range[1] + b_range[1]
     out = torch.empty(steps, layers, heads, 2, dtype=torch.int64)

@@ -1,0 +1,115 @@
+"""The rolling-window runtime on the GPU: a 3-layer stack with a 168-page
+history ring (window up to 240 pages), one denoise step plus the clean step
+per chunk, Full_Pset on layer 2, run for 8 chunks so that the ring wraps
+(from the third commit) and the anchor is rebased (chunks 6 and 7).
+
+Checks against the oracle on the runtime's own state:
+* every history page of the ring holds, bit for bit, the K/V rows of the
+  chunk page that the ring's slot sequence put there last;
+* the anchor frame's keys are the chunk-0 keys rebased by 3c - 15 frames
+  (oracle shift_temporal, bit for bit), its values untouched, and its page
+  summaries are the summary oracle's of the rebased keys;
+* after the wrap and the rebase, a dense call (layer 0), a sparse call
+  (layer 1) and a Full_Pset-corrected sparse call (layer 2) against softmax
+  attention and SelectedAttention.fixed on the page tables they used."""
+import pytest
+import torch
+
+from oracle import reference as ref
+from oracle import summary as osum
+from streaming_sparse_amd import workload
+from streaming_sparse_amd.ops import Summary
+from streaming_sparse_amd.runtime import ANCHOR_TOKENS, CURRENT, StreamConfig, StreamRuntime, rebase_offset
+
+pytestmark = pytest.mark.gpu
+REL_L2, MAX_ABS = 5e-3, 2e-2
+TILES = [0, 17, 40, 71]
+
+
+def _check(got, want, tag):
+    g, w = got.detach().cpu().float(), want.float()
+    err = ref.rel_l2(g, w)
+    mx = float((g - w).abs().max())
+    print(f"{tag}: rel-L2 {err:.3e} max-abs {mx:.3e}", flush=True)
+    assert err <= REL_L2 and mx <= MAX_ABS, (tag, err, mx)
+
+
+def test_rolling_window(device):
+    cfg = StreamConfig(layers=3, steps=1, history_pages=168, pset_layers=(2,), seed=8)
+    rt = StreamRuntime(cfg, device)
+    committed = {}          # chunk -> layer-1 clean-step (k, v) on the CPU
+    anchor_v = None
+    owner = {}              # ring page -> (chunk, chunk page)
+    for c in range(7):
+        inputs = rt.chunk_inputs()
+        slots = rt.ring.commit_slots()
+        rt.run_chunk(inputs)
+        torch.cuda.synchronize()
+        k1, v1 = inputs[cfg.steps][1][1:]
+        committed[c] = (k1.cpu(), v1.cpu())
+        if c == 0:
+            anchor_k0 = inputs[cfg.steps][1][1][:ANCHOR_TOKENS].cpu()
+            anchor_v = inputs[cfg.steps][1][2][:ANCHOR_TOKENS].cpu()
+        for j, s in enumerate(slots):
+            owner[s] = (c, j)
+        print(f"chunk {c}: history {rt.ring.n} pages, calls {rt.calls}", flush=True)
+    assert rt.ring.n == 168 and rt.ring.commits == 7
+    L1 = rt.layers[1]
+    kc, vc = L1.k[0].cpu(), L1.v[0].cpu()
+    # ring contents: pages 24..167 hold the last writer's rows
+    for s in range(24, 168):
+        c, j = owner[s]
+        k, v = committed[c]
+        assert torch.equal(kc[64 * s:64 * s + 64].view(torch.int16), k[64 * j:64 * j + 64].view(torch.int16)), s
+        assert torch.equal(vc[64 * s:64 * s + 64].view(torch.int16), v[64 * j:64 * j + 64].view(torch.int16)), s
+    assert {owner[s][0] for s in range(24, 168)} == {5, 6}     # the 144-page span holds the last two chunks
+    # anchor: chunk-0 keys rebased for chunk 6 (3 frames), values untouched
+    freqs = workload.rope_table(128)
+    want_k = ref.shift_temporal(anchor_k0[None], ANCHOR_TOKENS, freqs, rebase_offset(6))[0]
+    assert torch.equal(kc[:ANCHOR_TOKENS].view(torch.int16), want_k.view(torch.int16))
+    assert torch.equal(vc[:ANCHOR_TOKENS].view(torch.int16), anchor_v.view(torch.int16))
+    assert not torch.equal(kc[:ANCHOR_TOKENS], anchor_k0)
+
+    # chunk 7: rebase by 6 frames, then one call of each kind after the wrap
+    inputs = rt.chunk_inputs()
+    rt.begin_chunk()
+    torch.cuda.synchronize()
+    want_k = ref.shift_temporal(anchor_k0[None], ANCHOR_TOKENS, freqs, rebase_offset(7))[0]
+    assert torch.equal(L1.k[0, :ANCHOR_TOKENS].cpu().view(torch.int16), want_k.view(torch.int16))
+    # anchor summaries rebuilt from the rebased keys
+    kp = want_k.transpose(0, 1).reshape(12, 24, 64, 128)
+    vp = anchor_v.transpose(0, 1).reshape(12, 24, 64, 128)
+    wsum = osum.summaries(kp, vp, L1.basis.cpu().float(), rt.init[:, :24].cpu())
+    ok = wsum['margin'] > 1e-5
+    for name in ('keys', 'mean'):
+        got = getattr(L1.slab, name)[:, :24].cpu().float()[ok]
+        w = wsum[name].float()[ok]
+        assert bool(((got - w).abs() <= w.abs() * 2.0 ** -7 + 1e-6).all()), name
+    P = rt.ring.n + CURRENT
+    rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in TILES])
+    for layer in range(3):
+        q, k, v = inputs[0][layer]
+        out = rt.layer_call(0, layer, q, k, v).clone()
+        torch.cuda.synchronize()
+        L = rt.layers[layer]
+        kw, vw = L.k[:, :64 * P].cpu(), L.v[:, :64 * P].cpu()
+        if layer == 0:
+            hs = [0, 7]
+            want = ref.dense_attention(q[:, rows][:, :, hs].cpu(), kw[:, :, hs], vw[:, :, hs]).bfloat16()
+            _check(out[:, rows][:, :, hs], want, "post-wrap dense layer")
+            continue
+        ids = rt.last_ids.cpu()
+        assert (ids[..., 0] == torch.arange(72) + P - 72).all()
+        s = Summary(*(getattr(L.slab, f)[:, :P].cpu() for f in Summary.FIELDS))
+        want = ref.selected_attention(q.cpu(), kw, vw, s, L.basis.cpu().float(), ids, tiles=TILES).bfloat16()
+        _check(out[:, rows], want[:, rows], f"post-wrap sparse layer {layer}")
+        # the call's current-page summaries are the summary oracle's of the chunk's K/V
+        kp = k.cpu().transpose(0, 1).reshape(12, 72, 64, 128)
+        vp = v.cpu().transpose(0, 1).reshape(12, 72, 64, 128)
+        wsum = osum.summaries(kp, vp, L.basis.cpu().float(), rt.init.cpu())
+        ok = wsum['margin'] > 1e-5
+        for name in ('keys', 'mean'):
+            got = getattr(s, name)[:, P - 72:].float()[ok]
+            w = wsum[name].float()[ok]
+            assert bool(((got - w).abs() <= w.abs() * 2.0 ** -7 + 1e-6).all()), (layer, name)
+    assert rt.calls['full_pset'] >= 1
