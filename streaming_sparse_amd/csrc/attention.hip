@@ -204,36 +204,57 @@ __device__ __forceinline__ float unit_max(f32x16& S, int e, int pair, int lane, 
 // (log2 units), so probabilities stay below 2^kSlack and the rescale is rare.
 constexpr float kSlack = 8.0f;
 
-__device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, f32x16 (&O)[4]) {
+// `ls` is the two-term path's denominator (a lane's fp32 partial sum), L the
+// single-term path's (matrix-pipe row sums); each path leaves the other zero.
+__device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, float& ls, f32x16 (&O)[4]) {
   if (__any(mloc > m + kSlack)) {
     const float mnew = fmaxf(m, mloc);
     const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
     L *= alpha;
+    ls *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) O[dt] *= alpha;
     m = mnew;
   }
 }
 
+// Word w of the two-term operands from two fp32 probabilities: hi = bf16(P)
+// pairs, lo = bf16(P - bf16(P)) pairs (LE/gap_exact_round_kernel.py:110-125).
+__device__ __forceinline__ u32x2 split_pair(float p0, float p1) {
+  const uint32_t hi = pack_bf16(p0, p1);
+  return u32x2{hi, pack_bf16(p0 - bf16_lo(hi), p1 - bf16_hi(hi))};
+}
+
 // P = 2^(S*scale + nb) as the bf16 B operands of the two k steps (pb; pl =
-// the low parts bf16(P - bf16(P)) for the two-term product).
+// the low parts bf16(P - bf16(P)) for the two-term product, whose
+// denominator `ls` gathers the fp32 P of the lane).
 template <bool PRECISE>
 __device__ __forceinline__ void probabilities(const f32x16& S, float nb, float scale_log2, u32x4 (&pb)[2],
-                                              u32x4 (&pl)[2]) {
+                                              u32x4 (&pl)[2], float& ls) {
   float P[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) P[i] = __builtin_amdgcn_exp2f(fmaf(S[i], scale_log2, nb));
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const int o = 8 * ks;
-    pb[ks] = u32x4{pack_bf16(P[o + 0], P[o + 1]), pack_bf16(P[o + 2], P[o + 3]), pack_bf16(P[o + 4], P[o + 5]),
-                   pack_bf16(P[o + 6], P[o + 7])};
     pl[ks] = u32x4{};
     if (PRECISE) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w)
-        pl[ks][w] = pack_bf16(P[o + 2 * w] - bf16_lo(pb[ks][w]), P[o + 2 * w + 1] - bf16_hi(pb[ks][w]));
+      for (int w = 0; w < 4; ++w) {
+        const u32x2 hl = split_pair(P[o + 2 * w], P[o + 2 * w + 1]);
+        pb[ks][w] = hl[0];
+        pl[ks][w] = hl[1];
+      }
+    } else {
+      pb[ks] = u32x4{pack_bf16(P[o + 0], P[o + 1]), pack_bf16(P[o + 2], P[o + 3]),
+                     pack_bf16(P[o + 4], P[o + 5]), pack_bf16(P[o + 6], P[o + 7])};
     }
+  }
+  if (PRECISE) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += P[i];
+    ls += s;
   }
 }
 
@@ -241,17 +262,17 @@ __device__ __forceinline__ void probabilities(const f32x16& S, float nb, float s
 // row sums of P in every row of the accumulator.
 constexpr uint32_t kOnes = 0x3F803F80u;
 
-// O^T += V^T P^T and L += 1 P^T (the softmax denominator of lane's query over
-// the pair's 32 keys, summed by the matrix pipe from the same bf16 P that
-// multiplies V).
+// O^T += V^T P^T, and in the single-term path L += 1 P^T (the softmax
+// denominator of lane's query over the pair's 32 keys, summed by the matrix
+// pipe from the same bf16 P that multiplies V; the two-term path sums fp32 P
+// on the vector unit instead, as the reference's l does).
 template <bool PRECISE>
 __device__ __forceinline__ void pv(const u32x4 (&pb)[2], const u32x4 (&pl)[2], const lds_u8* vbuf, int pair,
                                    int lane, f32x16& L, f32x16 (&O)[4]) {
   const u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    L = mfma32(ones, pb[ks], L);
-    if (PRECISE) L = mfma32(ones, pl[ks], L);
+    if (!PRECISE) L = mfma32(ones, pb[ks], L);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const u32x4 va = v_operand(vbuf, pair, ks, dt, lane);
@@ -353,6 +374,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 
   float m = -INFINITY;
   f32x16 L = {}, O[4];
+  float ls = 0.f;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
   const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63, NB, true);
@@ -368,7 +390,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   f32x16 S0 = s_tile(kslot(0), pair, lane, qop), S1;
   float mloc;
   float bias = unit_max(S0, unit(0), pair, lane, p.scale_log2, mloc);
-  update_max(mloc, m, L, O);
+  update_max(mloc, m, L, ls, O);
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
   // One unit with a successor: loads of K unit i+2 (clamped to the last
   // unit; a surplus load lands in a slot nobody reads again) and V unit i+1,
@@ -384,17 +406,71 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     const int u3 = __builtin_amdgcn_readfirstlane(u3raw);
     // the general call issues its loads first; the two-block call (8 waves,
     // half the loads each) spreads them over the first products
-    if (NB == 1 || PRECISE) {
+    if (NB == 1) {
       issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
       issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
     }
     const float nb = bias - (m == -INFINITY ? 0.0f : m);
     if (PRECISE) {
-      Sn = s_tile(kslot(nxt), pair, lane, qop);
-      u32x4 pb[2], pl[2];
-      probabilities<PRECISE>(Sc, nb, p.scale_log2, pb, pl);
+      // Two-term P.V in one instruction stream: the 8 products of S(i+1)
+      // each carry two exponentials of unit i, the hi/lo split of the
+      // previous pair of probabilities (whose exponentials are done by then)
+      // and one operand read 4 products ahead; the 16 P.V products (hi and
+      // lo) of unit i carry the second k step's V reads and the max of unit
+      // i+1.  The denominator is the lane's fp32 sum of P.
+      const lds_u8* kb = kslot(nxt);
+      const lds_u8* vb = vslot(cur);
+      const int r = lane & 31, hh = lane >> 5;
+      u32x4 ka[8], va[2][4], pb[2], pl[2];
+      float P[16];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) ka[st] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + hh));
+      __builtin_amdgcn_sched_barrier(0);
+      Sn = f32x16{};
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        Sn = mfma32(ka[st], qop[st], Sn);
+        if (NB == 2 && st == 0) issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
+        if (NB == 2 && st == 3) issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
+        if (st < 4)
+          ka[st + 4] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + 8 + hh));
+        else
+          va[0][st - 4] = v_operand(vb, pair, 0, st - 4, lane);
+        P[2 * st] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st], p.scale_log2, nb));
+        P[2 * st + 1] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st + 1], p.scale_log2, nb));
+        if (st > 0) {
+          const u32x2 hl = split_pair(P[2 * st - 2], P[2 * st - 1]);
+          pb[(st - 1) >> 2][(st - 1) & 3] = hl[0];
+          pl[(st - 1) >> 2][(st - 1) & 3] = hl[1];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      {
+        const u32x2 hl = split_pair(P[14], P[15]);
+        pb[1][3] = hl[0];
+        pl[1][3] = hl[1];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (NB == 1) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        O[dt] = mfma32(va[0][dt], pb[0], O[dt]);
+        va[1][dt] = v_operand(vb, pair, 1, dt, lane);
+        O[dt] = mfma32(va[0][dt], pl[0], O[dt]);
+        if (dt == 1) {
+          float s = 0.f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s += P[i];
+          ls += s;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
       bias = unit_max<K>(Sn, u1, pair, lane, p.scale_log2, mloc);
-      pv<PRECISE>(pb, pl, vslot(cur), pair, lane, L, O);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
+        O[dt] = mfma32(va[1][dt], pl[1], O[dt]);
+      }
     } else {
       // One instruction stream that keeps the matrix pipe fed: the 8
       // products of S(i+1) each carry two exponentials of unit i and one
@@ -447,8 +523,8 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
     }
-    update_max(mloc, m, L, O);
-    if (NB == 1 && !PRECISE) __builtin_amdgcn_s_setprio(0);
+    update_max(mloc, m, L, ls, O);
+    if (NB == 1) __builtin_amdgcn_s_setprio(0);
     u1 = u2;
     u2 = u3;
     u3raw = units[min(i + 4, nunits - 1)];
@@ -483,12 +559,18 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   // last unit
   {
     u32x4 pb[2], pl[2];
-    probabilities<PRECISE>(S0, bias - (m == -INFINITY ? 0.0f : m), p.scale_log2, pb, pl);
+    probabilities<PRECISE>(S0, bias - (m == -INFINITY ? 0.0f : m), p.scale_log2, pb, pl, ls);
     pv<PRECISE>(pb, pl, vslot(i & 1), pair, lane, L, O);
   }
   __syncthreads();
-  // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS
-  const float l = L[0];
+  // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS.
+  // Two-term path: lanes l and l ^ 32 hold the partial sums of one query's
+  // two 16-key halves.
+  float l = L[0];
+  if (PRECISE) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls), false, false);
+    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
   // [group][qw][64 items][64 lanes] fp32 = 32 KB per group
   float* xo = reinterpret_cast<float*>(ring) + grp * 8192;
   if (pair == 1) {
