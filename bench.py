@@ -426,6 +426,9 @@ def chunk_line(args):
     dense_kernel_ms = time_loop(lambda: rt.run_dense_chunk(inputs, False), 1, stream)
     dense_sdpa_ms = time_loop(lambda: rt.run_dense_chunk(inputs, True), 1, stream)
     calls = rt.calls_per_chunk()
+    from streaming_sparse_amd import group
+    grouping_ms = time_loop(lambda: group.order(inputs.clean_k, inputs.clean_v, rt.group_weights,
+                                                page_dst=rt.page_dst, workspace=rt.ws), 3, stream)
     torch.cuda.synchronize()
     chunk_ms = time_loop(lambda: rt.run_chunk(inputs), 1, stream)
     return {"workload": f"30 layers x (4 denoise steps + clean commit), rolling {rt.cap}-page window, 12 heads; "
@@ -433,7 +436,8 @@ def chunk_line(args):
             "calls": calls, "chunk_ms": round(chunk_ms, 3),
             "dense_chunk_ms_this_kernel": round(dense_kernel_ms, 3),
             "dense_chunk_ms_sdpa": round(dense_sdpa_ms, 3),
-            "ratio_vs_dense_sdpa": round(chunk_ms / dense_sdpa_ms, 4), "setup_s": round(setup_s, 2)}
+            "ratio_vs_dense_sdpa": round(chunk_ms / dense_sdpa_ms, 4),
+            "commit_grouping_30_layers_ms": round(grouping_ms, 3), "setup_s": round(setup_s, 2)}
 
 
 def _cpu_model():

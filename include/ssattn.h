@@ -173,6 +173,23 @@ int ssa_commit_pages(const void* k_src, const void* v_src, long long src_token_s
                      void* v_dst, long long dst_token_stride, long long dst_head_stride, int heads,
                      hipStream_t stream);
 
+/* Clean-commit token grouping (RV/runtime.py:57-68 GroupingOps.group with the
+ * features of LE/all_sparse_model.py:16-23, LE/response_hard.py:20-31
+ * balanced splits 3,3,2,2,2 then 2,2 inside each page, the page order of
+ * RV/ops.py:25-28 and, with first_chunk, the stable re-sort by frame of
+ * VR/runtime.py:358-363), in fp64 from the bf16 inputs.  For each of
+ * layers x heads rows b = layer*heads + head: k, v are the chunk's 4608
+ * tokens (element layer*layer_stride + token*token_stride + head*head_stride
+ * + dim), bank [B,32,128], group_v [B,128,32], gate [B,32] fp32, page_dst
+ * [72] (destination page of grouped page p, NULL: identity).  order [B,4608]
+ * int32 receives the chunk token of each destination position (the `order`
+ * ssa_commit_pages takes).  Scratch: scratch_x 2*B*4608*32 fp64,
+ * scratch_ids 2*B*4608 int32. */
+int ssa_group_order(const void* k, const void* v, long long layer_stride, long long token_stride,
+                    long long head_stride, const float* bank, const float* group_v, const float* gate,
+                    const int32_t* page_dst, int first_chunk, int layers, int heads, double* scratch_x,
+                    int32_t* scratch_ids, int32_t* order, hipStream_t stream);
+
 /* ssa_pset without the caller-owned scratch (cand, rows, pool): the library
  * keeps that scratch in a file-scope device array of 48.05 MB per device
  * (held until the process ends), sized for n_heads * blocks <= 216 scoped rows

@@ -26,6 +26,7 @@ SIGNATURES = {
                  _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "ssa_anchor_rebase": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _i, _i, _i, _vp],
     "ssa_commit_pages": [_vp, _vp, _ll, _ll, _vp, _i, _vp, _i, _vp, _vp, _ll, _ll, _i, _vp],
+    "ssa_group_order": [_vp, _vp, _ll, _ll, _ll, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp],
     "ssa_pset_noalloc": [_vp, _ll, _ll, _ll, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                          _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
 }

@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libssattn.so")
-SOURCES = ("attention.hip", "route.hip", "pset.hip", "summary.hip", "runtime.hip")
+SOURCES = ("attention.hip", "route.hip", "pset.hip", "summary.hip", "runtime.hip", "group.hip")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
          # packed fp32 VALU forms are excluded from code generation
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

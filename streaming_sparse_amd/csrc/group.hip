@@ -1,0 +1,417 @@
+// Clean-commit token grouping for gfx950: the order in which a committed
+// chunk's 4608 tokens fill its 72 pages (RV/runtime.py:57-68 GroupingOps.group).
+//
+//   features  f = (k - mean k).bank / sqrt(128) scaled to unit RMS, plus
+//             0.1 tanh(gate) times the unit-RMS centred softmax response of
+//             v.group_v                                  (LE/all_sparse_model.py:16-23)
+//   balanced  7 levels of splits (3,3,2,2,2 over the chunk, then 2,2 inside
+//             each page): each group is centred, a direction starts at the
+//             one-hot of its highest-variance feature, takes 4 power steps,
+//             and the group is stably sorted by its projection
+//                                                        (LE/response_hard.py:20-31)
+//   pages     a page permutation (Config.page_order, RV/ops.py:25-28)
+//   chunk 0   a stable re-sort by frame, so the anchor frame fills pages
+//             0..23                                      (VR/runtime.py:358-363)
+//
+// Everything after the bf16 inputs is fp64, so the order does not hinge on
+// float32 rounding.  The batch is layers x heads independent rows b.
+//   project_kernel   grid (72 token blocks, B): raw key and value projections
+//   features_kernel  grid (B), 1024 threads: head-wide reductions, features
+//   level_kernel     grid (B x groups): stats, power steps, bitonic sort
+//   frames_kernel    grid (B): the first chunk's stable partition by frame
+#include "common.h"
+
+using namespace ssa;
+
+namespace {
+
+constexpr int kTokens = 4608;      // 3 frames x 1536
+constexpr int kFrame = 1536;
+constexpr int kR = 32;             // feature width
+constexpr int kPages = 72;
+constexpr int kLevels = 7;
+constexpr int kLevelSize[kLevels] = {4608, 1536, 512, 256, 128, 64, 32};
+constexpr double kInvSqrtD = 11.313708498984761;   // sqrt(128), divided by as the reference does
+
+struct GroupParams {
+  const uint16_t* k;
+  const uint16_t* v;
+  long long layer_stride, tok_stride, head_stride;   // elements
+  const float* bank;       // [B][32][128]
+  const float* gv;         // [B][128][32]
+  const float* gate;       // [B][32]
+  const int32_t* page_dst; // [72] destination page of grouped page p, or null
+  double* x[2];            // [B][4608][32] ping-pong
+  int32_t* ids[2];         // [B][4608] ping-pong
+  int32_t* order;          // [B][4608]
+  int H, B;
+};
+
+__device__ __forceinline__ const uint16_t* row_ptr(const uint16_t* base, const GroupParams& p, int b, int t) {
+  const int l = b / p.H, h = b % p.H;
+  return base + (long long)l * p.layer_stride + (long long)t * p.tok_stride + (long long)h * p.head_stride;
+}
+
+// raw[b][t][r] = k_t . bank_r and vp[b][t][r] = v_t . gv[:, r] in fp64 (exact
+// products of bf16 and fp32 values, summed in dimension order).
+__global__ __launch_bounds__(256) void project_kernel(GroupParams p) {
+  __shared__ float ks[64][kHeadDim + 1], vs[64][kHeadDim + 1];
+  __shared__ float bk[kR][kHeadDim + 1], gvs[kHeadDim][kR + 1];
+  const int blk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  for (int i = tid; i < 64 * kHeadDim; i += 256) {
+    const int t = i / kHeadDim, d = i % kHeadDim;
+    ks[t][d] = bf16_to_f32(row_ptr(p.k, p, b, blk * 64 + t)[d]);
+    vs[t][d] = bf16_to_f32(row_ptr(p.v, p, b, blk * 64 + t)[d]);
+  }
+  for (int i = tid; i < kR * kHeadDim; i += 256) {
+    bk[i / kHeadDim][i % kHeadDim] = p.bank[(long long)b * kR * kHeadDim + i];
+    gvs[i / kR][i % kR] = p.gv[(long long)b * kR * kHeadDim + i];
+  }
+  __syncthreads();
+  const int r = tid & 31, tg = tid >> 5;
+  double ak[8], av[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ak[i] = av[i] = 0.0;
+  for (int d = 0; d < kHeadDim; ++d) {
+    const double bkd = bk[r][d], gvd = gvs[d][r];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ak[i] = fma((double)ks[tg + 8 * i][d], bkd, ak[i]);
+      av[i] = fma((double)vs[tg + 8 * i][d], gvd, av[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const long long e = ((long long)b * kTokens + blk * 64 + tg + 8 * i) * kR + r;
+    p.x[0][e] = ak[i];
+    p.x[1][e] = av[i];
+  }
+}
+
+// Sum of a per-thread value over the 32 threads sharing r (tid & 31) of a
+// 1024-thread block; every thread gets the result.  red: 1024 doubles.
+__device__ __forceinline__ double sum_over_tokens(double x, double* red, int tid) {
+  red[tid] = x;
+  __syncthreads();
+  if (tid < 32) {
+    double s = 0.0;
+    for (int g = 0; g < 32; ++g) s += red[g * 32 + tid];
+    red[1024 + tid] = s;
+  }
+  __syncthreads();
+  const double s = red[1024 + (tid & 31)];
+  __syncthreads();
+  return s;
+}
+
+__device__ __forceinline__ double max_over_tokens(double x, double* red, int tid) {
+  red[tid] = x;
+  __syncthreads();
+  if (tid < 32) {
+    double s = -INFINITY;
+    for (int g = 0; g < 32; ++g) s = fmax(s, red[g * 32 + tid]);
+    red[1024 + tid] = s;
+  }
+  __syncthreads();
+  const double s = red[1024 + (tid & 31)];
+  __syncthreads();
+  return s;
+}
+
+__device__ __forceinline__ double sum_all(double x, double* red, int tid) {
+  const double s = sum_over_tokens(x, red, tid);   // per r
+  red[tid] = s;
+  __syncthreads();
+  double t = 0.0;
+  for (int r = 0; r < 32; ++r) t += red[r];
+  __syncthreads();
+  return t;
+}
+
+// Features of one row b (the head-wide reductions need the whole chunk):
+// x[0] holds raw key projections on entry and the features on exit; x[1]
+// the value projections; ids[0] = 0..4607.  Thread: r = tid & 31, tokens
+// tid / 32 + 32 i.
+__global__ __launch_bounds__(1024) void features_kernel(GroupParams p) {
+  __shared__ double red[1024 + 32];
+  const int b = blockIdx.x, tid = threadIdx.x, r = tid & 31, t0 = tid >> 5;
+  double* raw = p.x[0] + (long long)b * kTokens * kR;
+  const double* vp = p.x[1] + (long long)b * kTokens * kR;
+  constexpr int kPer = kTokens / 32;
+  double s = 0.0;
+  for (int i = 0; i < kPer; ++i) s += raw[(t0 + 32 * i) * kR + r];
+  const double mean_raw = sum_over_tokens(s, red, tid) / kTokens;
+  // score = centred key projection / sqrt(D); its RMS over (t, r) and max over t
+  double sq = 0.0, mx = -INFINITY;
+  for (int i = 0; i < kPer; ++i) {
+    const double sc = (raw[(t0 + 32 * i) * kR + r] - mean_raw) / kInvSqrtD;
+    sq = fma(sc, sc, sq);
+    mx = fmax(mx, sc);
+  }
+  const double rms = fmax(sqrt(sum_all(sq, red, tid) / (kTokens * kR)), 1e-6);
+  mx = max_over_tokens(mx, red, tid);
+  // softmax over tokens: denominator and sum of e * vp
+  double den = 0.0, num = 0.0;
+  for (int i = 0; i < kPer; ++i) {
+    const int e = (t0 + 32 * i) * kR + r;
+    const double ex = exp((raw[e] - mean_raw) / kInvSqrtD - mx);
+    den += ex;
+    num = fma(ex, vp[e], num);
+  }
+  den = sum_over_tokens(den, red, tid);
+  const double mean_a = sum_over_tokens(num, red, tid) / den;
+  double sq2 = 0.0;
+  for (int i = 0; i < kPer; ++i) {
+    const int e = (t0 + 32 * i) * kR + r;
+    const double a = exp((raw[e] - mean_raw) / kInvSqrtD - mx) / den;
+    const double resp = a * kTokens * (vp[e] - mean_a);
+    sq2 = fma(resp, resp, sq2);
+  }
+  const double rms2 = fmax(sqrt(sum_all(sq2, red, tid) / (kTokens * kR)), 1e-6);
+  const double g = 0.1 * tanh((double)p.gate[b * kR + r]);
+  for (int i = 0; i < kPer; ++i) {
+    const int t = t0 + 32 * i, e = t * kR + r;
+    const double sc = (raw[e] - mean_raw) / kInvSqrtD;
+    const double a = exp(sc - mx) / den;
+    const double resp = a * kTokens * (vp[e] - mean_a);
+    raw[e] = sc / rms + g * (resp / rms2);
+  }
+  for (int t = tid; t < kTokens; t += 1024) p.ids[0][(long long)b * kTokens + t] = t;
+}
+
+// Ascending key of a double (-0.0 and +0.0 equal, as the sort compares them).
+__device__ __forceinline__ unsigned long long order_key(double s) {
+  if (s == 0.0) s = 0.0;
+  const unsigned long long u = (unsigned long long)__double_as_longlong(s);
+  return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
+
+// Sum over the 8 lanes of a lane group (lanes 8q..8q+7).
+__device__ __forceinline__ double sum8(double x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  return x;
+}
+
+// One level of the balanced split: each workgroup takes one group of n rows
+// of one b, in the current order (rows in[0..n) of the group), and writes
+// them stably sorted by their projection on the power-iteration direction.
+// Thread: features 4 q .. 4 q + 3 (q = tid & 7), rows tid / 8 + 32 i.  The
+// last level writes the final order (page permutation applied) instead of
+// features.
+template <int SORTN, bool LAST>
+__global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int groups, int src, int32_t* last_out) {
+  __shared__ unsigned long long key[SORTN];
+  __shared__ unsigned short pos[SORTN];
+  __shared__ double red[32][kR + 1];
+  __shared__ double vec[3][kR];   // mean, direction, scratch
+  __shared__ int axis;
+  const int tid = threadIdx.x, q = tid & 7, rs = tid >> 3;
+  const int b = blockIdx.x / groups, gi = blockIdx.x % groups;
+  const long long row0 = (long long)b * kTokens + (long long)gi * n;
+  const double* x = p.x[src] + row0 * kR;
+  const int32_t* ids = p.ids[src] + row0;
+  auto reduce_rows = [&](const double (&a)[4], int slot) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[rs][4 * q + c] = a[c];
+    __syncthreads();
+    if (tid < kR) {
+      double s = 0.0;
+      for (int g = 0; g < 32; ++g) s += red[g][tid];
+      vec[slot][tid] = s;
+    }
+    __syncthreads();
+  };
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int i = rs; i < n; i += 32) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] += x[(long long)i * kR + 4 * q + c];
+  }
+  reduce_rows(acc, 0);
+  if (tid < kR) vec[0][tid] /= n;
+  __syncthreads();
+  double mean[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) mean[c] = vec[0][4 * q + c];
+  // highest-variance feature (first of equals) -> one-hot start direction
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = 0.0;
+  for (int i = rs; i < n; i += 32) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const double xc = x[(long long)i * kR + 4 * q + c] - mean[c];
+      acc[c] = fma(xc, xc, acc[c]);
+    }
+  }
+  reduce_rows(acc, 2);
+  if (tid == 0) {
+    int best = 0;
+    double bv = vec[2][0] / n;
+    for (int d = 1; d < kR; ++d) {
+      const double vd = vec[2][d] / n;
+      if (vd > bv) {
+        bv = vd;
+        best = d;
+      }
+    }
+    axis = best;
+  }
+  __syncthreads();
+  double dir[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) dir[c] = (4 * q + c == axis) ? 1.0 : 0.0;
+  // 4 power steps: dir <- X_c^T (X_c dir), normalised (norm clamped at 1e-8)
+  for (int it = 0; it < 4; ++it) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = 0.0;
+    for (int i = rs; i < n; i += 32) {
+      double xc[4], pr = 0.0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        xc[c] = x[(long long)i * kR + 4 * q + c] - mean[c];
+        pr = fma(xc[c], dir[c], pr);
+      }
+      pr = sum8(pr);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = fma(xc[c], pr, acc[c]);
+    }
+    reduce_rows(acc, 1);
+    double nrm = 0.0;
+    for (int d = 0; d < kR; ++d) nrm = fma(vec[1][d], vec[1][d], nrm);
+    nrm = fmax(sqrt(nrm), 1e-8);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dir[c] = vec[1][4 * q + c] / nrm;
+    __syncthreads();
+  }
+  // projections -> sort keys (ascending score, ties -> current position)
+  for (int i = rs; i < SORTN; i += 32) {
+    if (i < n) {
+      double pr = 0.0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) pr = fma(x[(long long)i * kR + 4 * q + c] - mean[c], dir[c], pr);
+      pr = sum8(pr);
+      if (q == 0) {
+        key[i] = order_key(pr);
+        pos[i] = (unsigned short)i;
+      }
+    } else if (q == 0) {
+      key[i] = ~0ull;
+      pos[i] = 0xFFFF;
+    }
+  }
+  __syncthreads();
+  for (int kk = 2; kk <= SORTN; kk <<= 1) {
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+      for (int e = tid; e < SORTN / 2; e += 256) {
+        const int a = (e / j) * 2 * j + (e % j), c = a + j;
+        const bool asc = (a & kk) == 0;
+        const unsigned long long ka = key[a], kc = key[c];
+        const unsigned short pa = pos[a], pc = pos[c];
+        const bool greater = ka > kc || (ka == kc && pa > pc);
+        if (greater == asc) {
+          key[a] = kc;
+          key[c] = ka;
+          pos[a] = pc;
+          pos[c] = pa;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (!LAST) {
+    double* xo = p.x[src ^ 1] + row0 * kR;
+    int32_t* io = p.ids[src ^ 1] + row0;
+    for (int j = rs; j < n; j += 32) {
+      const int s = pos[j];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xo[(long long)j * kR + 4 * q + c] = x[(long long)s * kR + 4 * q + c];
+      if (q == 0) io[j] = ids[s];
+    }
+  } else {
+    // groups of 32 are page halves: destination page of this group's page
+    const int in_head = gi * n, page = in_head / 64;
+    const int dpage = p.page_dst ? min(max(p.page_dst[page], 0), kPages - 1) : page;   // clamped: memory safety
+    const int dst = dpage * 64 + in_head % 64;
+    for (int j = tid; j < n; j += 256) last_out[(long long)b * kTokens + dst + j] = ids[pos[j]];
+  }
+}
+
+// Stable partition of each row's order by frame (token / 1536): the first
+// chunk's anchor frame fills pages 0..23 (VR/runtime.py:358-363).
+__global__ __launch_bounds__(256) void frames_kernel(const int32_t* in, int32_t* out) {
+  __shared__ int wsum[4];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int32_t* src = in + (long long)b * kTokens;
+  int32_t* dst = out + (long long)b * kTokens;
+  int cursor = 0;
+  for (int f = 0; f < 3; ++f) {
+    for (int c0 = 0; c0 < kTokens; c0 += 256) {
+      const int val = src[c0 + tid];
+      const bool on = val / kFrame == f;
+      const unsigned long long bal = __ballot(on);
+      if (lane == 0) wsum[w] = __popcll(bal);
+      __syncthreads();
+      int off = cursor;
+      for (int u = 0; u < w; ++u) off += wsum[u];
+      if (on) dst[off + __popcll(bal & ((1ull << lane) - 1ull))] = val;
+      cursor += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+      __syncthreads();
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssa_group_order(const void* k, const void* v, long long layer_stride, long long token_stride,
+                    long long head_stride, const float* bank, const float* group_v, const float* gate,
+                    const int32_t* page_dst, int first_chunk, int layers, int heads, double* scratch_x,
+                    int32_t* scratch_ids, int32_t* order, hipStream_t stream) {
+  if (layers <= 0 || heads <= 0 || !k || !v || !bank || !group_v || !gate || !scratch_x || !scratch_ids || !order ||
+      layer_stride < 0 || token_stride < 0 || head_stride < 0)
+    return (int)hipErrorInvalidValue;
+  GroupParams p;
+  p.k = (const uint16_t*)k;
+  p.v = (const uint16_t*)v;
+  p.layer_stride = layer_stride;
+  p.tok_stride = token_stride;
+  p.head_stride = head_stride;
+  p.bank = bank;
+  p.gv = group_v;
+  p.gate = gate;
+  p.page_dst = page_dst;
+  p.H = heads;
+  p.B = layers * heads;
+  const long long rows = (long long)p.B * kTokens;
+  p.x[0] = scratch_x;
+  p.x[1] = scratch_x + rows * kR;
+  p.ids[0] = scratch_ids;
+  p.ids[1] = scratch_ids + rows;
+  p.order = order;
+  hipLaunchKernelGGL(project_kernel, dim3(kTokens / 64, p.B), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(features_kernel, dim3(p.B), dim3(1024), 0, stream, p);
+  // levels alternate buffers 0 -> 1 -> 0 ...; the last writes the order (or
+  // the frame partition's input)
+  int32_t* last_out = first_chunk ? p.ids[1] : order;
+  int src = 0;
+  for (int lv = 0; lv < kLevels; ++lv) {
+    const int n = kLevelSize[lv], groups = kTokens / n;
+    const dim3 grid(p.B * groups);
+    switch (lv) {
+      case 0: hipLaunchKernelGGL((level_kernel<8192, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
+      case 1: hipLaunchKernelGGL((level_kernel<2048, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
+      case 2: hipLaunchKernelGGL((level_kernel<512, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
+      case 3: hipLaunchKernelGGL((level_kernel<256, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
+      case 4: hipLaunchKernelGGL((level_kernel<128, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
+      case 5: hipLaunchKernelGGL((level_kernel<64, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
+      default: hipLaunchKernelGGL((level_kernel<32, true>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
+    }
+    src ^= 1;
+  }
+  if (first_chunk) hipLaunchKernelGGL(frames_kernel, dim3(p.B), dim3(256), 0, stream, p.ids[1], order);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

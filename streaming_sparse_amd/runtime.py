@@ -26,11 +26,14 @@ summary slab of the same capacity.  A 3-frame chunk of 72 pages runs:
     too where scheduled, then the intersection router with the
     (window, step, layer) quotas, Full_Pset on the scheduled heads
     (runtime.py:213-257, graph.py:169-210), and the attention;
-* the commit of the clean step: per layer, the chunk's pages are written into
-  the ring slots (PageStore.commit_slots: after the first commit the slots
-  wrap inside [24, history_pages), so the anchor frame stays), then their
-  summaries and, on Full_Pset layers, encodings at those slots
-  (runtime.py:356-370).
+* the commit of the clean step, after all its calls: the chunk's tokens of
+  every layer are grouped into pages in one batch (GroupingOps.group,
+  RV/runtime.py:57-68; the first chunk re-sorted by frame so the anchor frame
+  fills pages 0..23, runtime.py:358-363), then per layer the grouped pages
+  are written into the ring slots (PageStore.commit_slots: after the first
+  commit the slots wrap inside [24, history_pages), so the anchor frame
+  stays), with their summaries and, on Full_Pset layers, encodings at those
+  slots (runtime.py:330-370).
 
 Q/K/V are seeded N(0, 1) with Wan RoPE at the chunk's absolute frames,
 generated on the device before the chunk runs; writing K/V into the cache
@@ -42,7 +45,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import _lib, pset, summary, workload
+from . import _lib, group, pset, summary, workload
 from .attention import Workspace
 from .legacy_components import HEAD_DIM, attention, kv_strides
 from .ops import Summary
@@ -71,6 +74,7 @@ class StreamConfig:
     pset_steps: tuple = PSET_STEPS
     quota_mean: float = 40.8
     sparse_start_chunks: tuple = ()   # chunks with <= 72 history pages that still run sparse
+    grouping: bool = True             # group the committed tokens into pages (False: token order)
 
 
 class PageRing:
@@ -131,6 +135,12 @@ def _rope_on_device(x, first_frame, freqs):
     return torch.view_as_real(z * f).reshape(L, H, D)
 
 
+class ChunkInputs(list):
+    """[steps + 1][layers] of (q, k, v), plus the clean step's K/V of all
+    layers as [L, N, H, D] blocks (clean_k, clean_v) whose per-layer views
+    are the clean step's entries."""
+
+
 @dataclass
 class Layer:
     k: torch.Tensor             # [1, 64 (history + 72), H, 128] bf16 resident cache
@@ -176,6 +186,9 @@ class StreamRuntime:
             workload.seed_for(cfg.seed, 0, 0, 9))).to(device=dev, dtype=torch.int32).contiguous()
         self.theta = torch.tensor([1.0, 1.0, 1.0, 0.5], device=dev).expand(H, 4).contiguous()
         self.lse = torch.empty(H, self.T, 16, device=dev)
+        self.group_weights = group.GroupWeights.seeded(cfg.layers, H, cfg.seed, dev) if cfg.grouping else None
+        self.page_dst = group.page_destinations(cfg.history_pages)
+        self.last_order = None
         self.own = None
         self.quotas = {}
         self.last = {}                # ids / out of the most recent call, for inspection
@@ -190,6 +203,10 @@ class StreamRuntime:
         c = self.chunk if chunk is None else chunk
         cfg = self.cfg
         dev = self.device
+        # the clean step's K/V of all layers in one [L, N, H, D] block each, so
+        # the commit groups every layer in one batch
+        clean_k = torch.empty(cfg.layers, self.N, self.H, HEAD_DIM, device=dev, dtype=torch.bfloat16)
+        clean_v = torch.empty_like(clean_k)
         out = []
         for step in range(cfg.steps + 1):
             row = []
@@ -198,9 +215,17 @@ class StreamRuntime:
                     workload.seed_for(cfg.seed, layer, step, 1000 + 3 * c))
                 q, k, v = (torch.randn(self.N, self.H, HEAD_DIM, generator=g, device=dev) for _ in range(3))
                 q = _rope_on_device(q, 3 * c, self.freqs_dev).to(torch.bfloat16)[None].contiguous()
-                k = _rope_on_device(k, 3 * c, self.freqs_dev).to(torch.bfloat16).contiguous()
-                row.append((q, k, v.to(torch.bfloat16).contiguous()))
+                k = _rope_on_device(k, 3 * c, self.freqs_dev).to(torch.bfloat16)
+                if step == cfg.steps:
+                    clean_k[layer].copy_(k)
+                    clean_v[layer].copy_(v)
+                    k, v = clean_k[layer], clean_v[layer]
+                else:
+                    k, v = k.contiguous(), v.to(torch.bfloat16).contiguous()
+                row.append((q, k, v))
             out.append(row)
+        out = ChunkInputs(out)
+        out.clean_k, out.clean_v = clean_k, clean_v
         return out
 
     def quota(self, chunk: int):
@@ -249,7 +274,8 @@ class StreamRuntime:
 
     def layer_call(self, step: int, layer: int, q, k, v):
         """One attention call of the current chunk: the chunk's K/V written into
-        the window, then a dense or sparse call; the clean step commits."""
+        the window, then a dense or sparse call (the clean step's commits
+        follow all its calls, see commit_chunk)."""
         cfg, L = self.cfg, self.layers[layer]
         n = self.ring.n
         P = n + CURRENT
@@ -266,8 +292,6 @@ class StreamRuntime:
         else:
             out = self.sparse_call(step, layer, q, kw, vw, P)
         self.last = dict(step=step, layer=layer, pages=P, out=out)
-        if clean:
-            self.commit(layer, k, v)
         return out
 
     def sparse_call(self, step, layer, q, kw, vw, P):
@@ -290,14 +314,30 @@ class StreamRuntime:
         self.last_ids = ids
         return attention(q, kw, vw, s, L.basis, ids, self.ws, rep_values=vrep)
 
-    def commit(self, layer: int, k, v):
-        """The chunk's pages into the ring slots, then their summaries and
-        (Full_Pset layers) encodings at those slots (VR/runtime.py:356-370)."""
+    def commit_chunk(self, inputs):
+        """The clean step's commit of every layer: one batched grouping of the
+        chunk's tokens (the first chunk re-sorted by frame so the anchor frame
+        fills pages 0..23), then per layer the grouped pages into the ring
+        slots with their summaries and encodings."""
+        order = None
+        if self.cfg.grouping:
+            order = group.order(inputs.clean_k, inputs.clean_v, self.group_weights, first_chunk=self.chunk == 0,
+                                page_dst=self.page_dst, workspace=self.ws)
+        self.last_order = order
+        for layer in range(self.cfg.layers):
+            self.commit(layer, inputs.clean_k[layer], inputs.clean_v[layer],
+                        None if order is None else order[layer])
+
+    def commit(self, layer: int, k, v, order=None):
+        """The chunk's pages (tokens in `order` [H, 4608], None: token order)
+        into the ring slots, then their summaries and (Full_Pset layers)
+        encodings at those slots (VR/runtime.py:356-370)."""
         L = self.layers[layer]
         tok, head = kv_strides(L.k, L.v)
-        _lib.check(_lib.lib().ssa_commit_pages(_lib.ptr(k), _lib.ptr(v), self.H * HEAD_DIM, HEAD_DIM, None, CURRENT,
-                                               _lib.ptr(self.slots_dev), self.cap, _lib.ptr(L.k), _lib.ptr(L.v), tok,
-                                               head, self.H, _lib.stream_handle(self.device)), "ssa_commit_pages")
+        _lib.check(_lib.lib().ssa_commit_pages(_lib.ptr(k), _lib.ptr(v), self.H * HEAD_DIM, HEAD_DIM, _lib.ptr(order),
+                                               CURRENT, _lib.ptr(self.slots_dev), self.cap, _lib.ptr(L.k),
+                                               _lib.ptr(L.v), tok, head, self.H, _lib.stream_handle(self.device)),
+                   "ssa_commit_pages")
         for first, length, off in runs(self.slots):
             summary.build(L.k, L.v, L.basis, self.init[:, off:off + length], L.slab, first, length)
             if L.encoding is not None:
@@ -316,6 +356,7 @@ class StreamRuntime:
             for layer in range(self.cfg.layers):
                 q, k, v = inputs[step][layer]
                 self.layer_call(step, layer, q, k, v)
+        self.commit_chunk(inputs)
         self.end_chunk()
 
     def run_dense_chunk(self, inputs, sdpa=False):

@@ -5,7 +5,9 @@ per chunk, Full_Pset on layer 2, run for 8 chunks so that the ring wraps
 
 Checks against the oracle on the runtime's own state:
 * every history page of the ring holds, bit for bit, the K/V rows of the
-  chunk page that the ring's slot sequence put there last;
+  grouped chunk page that the ring's slot sequence put there last (each
+  head's rows in that head's grouped token order, a permutation of the
+  chunk; the first chunk's anchor frame fills pages 0..23);
 * the anchor frame's keys are the chunk-0 keys rebased by 3c - 15 frames
   (oracle shift_temporal, bit for bit), its values untouched, and its page
   summaries are the summary oracle's of the rebased keys;
@@ -37,26 +39,29 @@ def _check(got, want, tag):
 def test_rolling_window(device):
     cfg = StreamConfig(layers=3, steps=1, history_pages=168, pset_layers=(2,), seed=8)
     rt = StreamRuntime(cfg, device)
-    committed = {}          # chunk -> layer-1 clean-step (k, v) on the CPU
-    anchor_v = None
+    committed = {}          # chunk -> layer-1 clean-step (k, v) in its grouped order, on the CPU
     owner = {}              # ring page -> (chunk, chunk page)
+    heads = torch.arange(12)
     for c in range(7):
         inputs = rt.chunk_inputs()
         slots = rt.ring.commit_slots()
         rt.run_chunk(inputs)
         torch.cuda.synchronize()
         k1, v1 = inputs[cfg.steps][1][1:]
-        committed[c] = (k1.cpu(), v1.cpu())
+        order = rt.last_order[1].cpu().long()                      # [H, 4608]
+        assert torch.equal(order.sort(-1).values, torch.arange(4608).expand(12, -1))
+        grouped = lambda x: x.cpu()[order.t(), heads[None, :]]    # row j, head h <- token order[h, j]
+        committed[c] = (grouped(k1), grouped(v1))
         if c == 0:
-            anchor_k0 = inputs[cfg.steps][1][1][:ANCHOR_TOKENS].cpu()
-            anchor_v = inputs[cfg.steps][1][2][:ANCHOR_TOKENS].cpu()
+            assert bool((order[:, :ANCHOR_TOKENS] < ANCHOR_TOKENS).all())   # anchor frame in pages 0..23
+            anchor_k0, anchor_v = (x[:ANCHOR_TOKENS].clone() for x in committed[0])
         for j, s in enumerate(slots):
             owner[s] = (c, j)
         print(f"chunk {c}: history {rt.ring.n} pages, calls {rt.calls}", flush=True)
     assert rt.ring.n == 168 and rt.ring.commits == 7
     L1 = rt.layers[1]
     kc, vc = L1.k[0].cpu(), L1.v[0].cpu()
-    # ring contents: pages 24..167 hold the last writer's rows
+    # ring contents: pages 24..167 hold the last writer's grouped rows
     for s in range(24, 168):
         c, j = owner[s]
         k, v = committed[c]
