@@ -63,6 +63,8 @@ def parse():
     ap.add_argument("--cpu-sample-blocks", type=int, default=4)
     ap.add_argument("--headline-only", action="store_true",
                     help="only the headline call (for a profiler run whose kernel averages are the headline's)")
+    ap.add_argument("--chunk-only", action="store_true",
+                    help="only the streaming chunk line (for a profiler run of the 30-layer chunk)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (scales rocprof FETCH/WRITE_SIZE)")
     return ap.parse_args()
@@ -164,6 +166,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.chunk_only:
+        print(json.dumps({"metric": "ms per 3-frame chunk, 30 layers", "chunk": chunk_line(args)}), flush=True)
         return
     import torch
     from streaming_sparse_amd import _lib, workload

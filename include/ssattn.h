@@ -183,7 +183,8 @@ int ssa_commit_pages(const void* k_src, const void* v_src, long long src_token_s
  * + dim), bank [B,32,128], group_v [B,128,32], gate [B,32] fp32, page_dst
  * [72] (destination page of grouped page p, NULL: identity).  order [B,4608]
  * int32 receives the chunk token of each destination position (the `order`
- * ssa_commit_pages takes).  Scratch: scratch_x 2*B*4608*32 fp64,
+ * ssa_commit_pages takes).  k, v, bank and group_v 16-byte aligned, strides
+ * multiples of 8 elements.  Scratch: scratch_x 2*B*4608*32 fp64,
  * scratch_ids 2*B*4608 int32. */
 int ssa_group_order(const void* k, const void* v, long long layer_stride, long long token_stride,
                     long long head_stride, const float* bank, const float* group_v, const float* gate,

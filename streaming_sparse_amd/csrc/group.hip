@@ -53,38 +53,75 @@ __device__ __forceinline__ const uint16_t* row_ptr(const uint16_t* base, const G
 }
 
 // raw[b][t][r] = k_t . bank_r and vp[b][t][r] = v_t . gv[:, r] in fp64 (exact
-// products of bf16 and fp32 values, summed in dimension order).
-__global__ __launch_bounds__(256) void project_kernel(GroupParams p) {
-  __shared__ float ks[64][kHeadDim + 1], vs[64][kHeadDim + 1];
-  __shared__ float bk[kR][kHeadDim + 1], gvs[kHeadDim][kR + 1];
+// products of bf16 and fp32 values, summed in dimension order).  The 64
+// tokens sit in LDS as bf16 rows (16-byte loads from memory), both weight
+// matrices (gv transposed) as fp32 rows padded to 132 (16-byte reads,
+// conflict-free across 16 consecutive rows): 68 KB, two workgroups per CU.
+// Thread: tokens 4 tq .. 4 tq + 3 and features rp, rp + 16 of both
+// projections, 16 fp64 accumulators.
+constexpr int kRowPad = 132;
+constexpr int kTokPad = 136;
+
+__device__ __forceinline__ f32x4 bf16x4_to_f32(u32x2 w) {
+  return f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
+}
+
+__global__ __launch_bounds__(256, 2) void project_kernel(GroupParams p) {
+  __shared__ alignas(16) uint16_t ks[64][kTokPad], vs[64][kTokPad];
+  __shared__ alignas(16) float bk[kR][kRowPad], gvt[kR][kRowPad];
   const int blk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  for (int i = tid; i < 64 * kHeadDim; i += 256) {
-    const int t = i / kHeadDim, d = i % kHeadDim;
-    ks[t][d] = bf16_to_f32(row_ptr(p.k, p, b, blk * 64 + t)[d]);
-    vs[t][d] = bf16_to_f32(row_ptr(p.v, p, b, blk * 64 + t)[d]);
+  // 64 rows x 16 pieces of 16 bytes, for K and V
+  for (int i = tid; i < 64 * 16; i += 256) {
+    const int t = i >> 4, c = i & 15;
+    *reinterpret_cast<u32x4*>(&ks[t][8 * c]) = ldg16(row_ptr(p.k, p, b, blk * 64 + t) + 8 * c);
+    *reinterpret_cast<u32x4*>(&vs[t][8 * c]) = ldg16(row_ptr(p.v, p, b, blk * 64 + t) + 8 * c);
   }
-  for (int i = tid; i < kR * kHeadDim; i += 256) {
-    bk[i / kHeadDim][i % kHeadDim] = p.bank[(long long)b * kR * kHeadDim + i];
-    gvs[i / kR][i % kR] = p.gv[(long long)b * kR * kHeadDim + i];
+  for (int i = tid; i < kR * kHeadDim / 4; i += 256) {
+    const f32x4 w = reinterpret_cast<const f32x4*>(p.bank + (long long)b * kR * kHeadDim)[i];
+    *reinterpret_cast<f32x4*>(&bk[(4 * i) / kHeadDim][(4 * i) % kHeadDim]) = w;
+    const f32x4 g = reinterpret_cast<const f32x4*>(p.gv + (long long)b * kR * kHeadDim)[i];
+    const int d = (4 * i) / kR, r = (4 * i) % kR;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) gvt[r + c][d] = g[c];
   }
   __syncthreads();
-  const int r = tid & 31, tg = tid >> 5;
-  double ak[8], av[8];
+  const int rp = tid & 15, tq = tid >> 4;
+  double ak[4][2], av[4][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) ak[i] = av[i] = 0.0;
-  for (int d = 0; d < kHeadDim; ++d) {
-    const double bkd = bk[r][d], gvd = gvs[d][r];
+  for (int i = 0; i < 4; ++i) ak[i][0] = ak[i][1] = av[i][0] = av[i][1] = 0.0;
+  for (int d = 0; d < kHeadDim; d += 4) {
+    f32x4 kk[4], vv[4], bb[2], gg[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ak[i] = fma((double)ks[tg + 8 * i][d], bkd, ak[i]);
-      av[i] = fma((double)vs[tg + 8 * i][d], gvd, av[i]);
+    for (int i = 0; i < 4; ++i) {
+      kk[i] = bf16x4_to_f32(*reinterpret_cast<const u32x2*>(&ks[4 * tq + i][d]));
+      vv[i] = bf16x4_to_f32(*reinterpret_cast<const u32x2*>(&vs[4 * tq + i][d]));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bb[j] = *reinterpret_cast<const f32x4*>(&bk[rp + 16 * j][d]);
+      gg[j] = *reinterpret_cast<const f32x4*>(&gvt[rp + 16 * j][d]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const double b0 = bb[0][c], b1 = bb[1][c], g0 = gg[0][c], g1 = gg[1][c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const double kd = kk[i][c], vd = vv[i][c];
+        ak[i][0] = fma(kd, b0, ak[i][0]);
+        ak[i][1] = fma(kd, b1, ak[i][1]);
+        av[i][0] = fma(vd, g0, av[i][0]);
+        av[i][1] = fma(vd, g1, av[i][1]);
+      }
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const long long e = ((long long)b * kTokens + blk * 64 + tg + 8 * i) * kR + r;
-    p.x[0][e] = ak[i];
-    p.x[1][e] = av[i];
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const long long e = ((long long)b * kTokens + blk * 64 + 4 * tq + i) * kR + rp + 16 * j;
+      p.x[0][e] = ak[i][j];
+      p.x[1][e] = av[i][j];
+    }
   }
 }
 
@@ -371,6 +408,10 @@ int ssa_group_order(const void* k, const void* v, long long layer_stride, long l
                     int32_t* scratch_ids, int32_t* order, hipStream_t stream) {
   if (layers <= 0 || heads <= 0 || !k || !v || !bank || !group_v || !gate || !scratch_x || !scratch_ids || !order ||
       layer_stride < 0 || token_stride < 0 || head_stride < 0)
+    return (int)hipErrorInvalidValue;
+  // rows are read 16 bytes at a time
+  if ((((uintptr_t)k | (uintptr_t)v | (uintptr_t)bank | (uintptr_t)group_v) & 15) != 0 ||
+      ((layer_stride | token_stride | head_stride) & 7) != 0)
     return (int)hipErrorInvalidValue;
   GroupParams p;
   p.k = (const uint16_t*)k;

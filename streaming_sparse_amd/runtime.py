@@ -21,7 +21,9 @@ summary slab of the same capacity.  A 3-frame chunk of 72 pages runs:
   attention call over the window of P = n + 72 pages:
   - dense (every page exact, the same fused kernel) for layer 0, for the
     clean step and while the history holds at most 72 pages
-    (runtime.py:209-211);
+    (runtime.py:209-211); the reference runs these through its ordinary
+    dense attention (engine.dense), whose P.V is one bf16 product, so they
+    run single-term here too;
   - otherwise the current pages' summaries are rebuilt, Full_Pset encodings
     too where scheduled, then the intersection router with the
     (window, step, layer) quotas, Full_Pset on the scheduled heads
@@ -189,6 +191,7 @@ class StreamRuntime:
         self.group_weights = group.GroupWeights.seeded(cfg.layers, H, cfg.seed, dev) if cfg.grouping else None
         self.page_dst = group.page_destinations(cfg.history_pages)
         self.last_order = None
+        self.record = None            # a list to collect a copy of every call's output, or None
         self.own = None
         self.quotas = {}
         self.last = {}                # ids / out of the most recent call, for inspection
@@ -287,11 +290,13 @@ class StreamRuntime:
         s = L.slab.slice(0, P)
         clean = step == cfg.steps
         if clean or layer == 0 or self.dense_window():
-            out = attention(q, kw, vw, s, L.basis, self.dense_ids(P), self.ws, all_pages=True)
+            out = attention(q, kw, vw, s, L.basis, self.dense_ids(P), self.ws, all_pages=True, single_av=True)
             self.calls['dense'] += 1
         else:
             out = self.sparse_call(step, layer, q, kw, vw, P)
         self.last = dict(step=step, layer=layer, pages=P, out=out)
+        if self.record is not None:
+            self.record.append(out.clone())
         return out
 
     def sparse_call(self, step, layer, q, kw, vw, P):
@@ -376,7 +381,8 @@ class StreamRuntime:
                     torch.nn.functional.scaled_dot_product_attention(
                         q[0].transpose(0, 1)[None], kw[0].transpose(0, 1)[None], vw[0].transpose(0, 1)[None])
                 else:
-                    attention(q, kw, vw, L.slab.slice(0, P), L.basis, self.dense_ids(P), self.ws, all_pages=True)
+                    attention(q, kw, vw, L.slab.slice(0, P), L.basis, self.dense_ids(P), self.ws, all_pages=True,
+                              single_av=True)
 
     def dense_ids(self, P: int):
         """Every page of a P-page window per block, own page (P - 72 + t) first."""
