@@ -220,8 +220,11 @@ __device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, floa
 
 // Word w of the two-term operands from two fp32 probabilities: hi = bf16(P)
 // pairs, lo = bf16(P - bf16(P)) pairs (LE/gap_exact_round_kernel.py:110-125).
+// The empty asm hands the packed word on opaquely: otherwise the compiler
+// rebuilds bf16(p0) for the low half with a second conversion.
 __device__ __forceinline__ u32x2 split_pair(float p0, float p1) {
-  const uint32_t hi = pack_bf16(p0, p1);
+  uint32_t hi = pack_bf16(p0, p1);
+  asm volatile("" : "+v"(hi));
   return u32x2{hi, pack_bf16(p0 - bf16_lo(hi), p1 - bf16_hi(hi))};
 }
 
