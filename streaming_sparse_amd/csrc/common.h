@@ -64,14 +64,6 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
 // so the compiler's own wait-count tracking sees it.
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// s_waitcnt vmcnt(N): at most N of this wave's vector memory loads still
-// outstanding (they complete in issue order).
-template <int N>
-__device__ __forceinline__ void wait_loads_upto() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
 // 16-byte global->LDS load of one wave: lane l's 16 bytes at base + off
 // (bytes; base wave-uniform in SGPRs, off per lane) land at lds + 16*l.
 // The LDS base goes in through the "{m0}" operand, so the compiler writes
