@@ -415,12 +415,12 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     }
     const float nb = bias - (m == -INFINITY ? 0.0f : m);
     if (PRECISE) {
-      // Two-term P.V in one instruction stream: the 8 products of S(i+1)
-      // each carry two exponentials of unit i, the hi/lo split of the
-      // previous pair of probabilities (whose exponentials are done by then)
-      // and one operand read 4 products ahead; the 16 P.V products (hi and
-      // lo) of unit i carry the second k step's V reads and the max of unit
-      // i+1.  The denominator is the lane's fp32 sum of P.
+      // Two-term P.V in three stages of 8 matrix products, each carrying a
+      // similar share of the vector work, so that the matrix and vector
+      // work of this wave overlap throughout the step: S(i+1) with k step 0
+      // of unit i's exponentials and splits, the hi/lo products of k step 0
+      // with those of k step 1, the products of k step 1 with the max of
+      // unit i+1 and the denominator (the lane's fp32 sum of P).
       const lds_u8* kb = kslot(nxt);
       const lds_u8* vb = vslot(cur);
       const int r = lane & 31, hh = lane >> 5;
@@ -430,6 +430,8 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       for (int st = 0; st < 4; ++st) ka[st] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + hh));
       __builtin_amdgcn_sched_barrier(0);
       Sn = f32x16{};
+      // stage A: the 8 products of S(i+1), each with one exponential of
+      // k step 0 of unit i, a split every second product, one operand read
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
         Sn = mfma32(ka[st], qop[st], Sn);
@@ -439,40 +441,43 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
           ka[st + 4] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + 8 + hh));
         else
           va[0][st - 4] = v_operand(vb, pair, 0, st - 4, lane);
-        P[2 * st] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st], p.scale_log2, nb));
-        P[2 * st + 1] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st + 1], p.scale_log2, nb));
-        if (st > 0) {
-          const u32x2 hl = split_pair(P[2 * st - 2], P[2 * st - 1]);
-          pb[(st - 1) >> 2][(st - 1) & 3] = hl[0];
-          pl[(st - 1) >> 2][(st - 1) & 3] = hl[1];
+        P[st] = __builtin_amdgcn_exp2f(fmaf(Sc[st], p.scale_log2, nb));
+        if (st & 1) {
+          const u32x2 hl = split_pair(P[st - 1], P[st]);
+          pb[0][st >> 1] = hl[0];
+          pl[0][st >> 1] = hl[1];
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      {
-        const u32x2 hl = split_pair(P[14], P[15]);
-        pb[1][3] = hl[0];
-        pl[1][3] = hl[1];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (NB == 1) __builtin_amdgcn_s_setprio(1);
+      // stage B: the 8 P.V products of k step 0 (hi, lo), each pair with two
+      // exponentials and the split of k step 1, and its V operand read
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         O[dt] = mfma32(va[0][dt], pb[0], O[dt]);
         va[1][dt] = v_operand(vb, pair, 1, dt, lane);
+        P[8 + 2 * dt] = __builtin_amdgcn_exp2f(fmaf(Sc[8 + 2 * dt], p.scale_log2, nb));
+        P[9 + 2 * dt] = __builtin_amdgcn_exp2f(fmaf(Sc[9 + 2 * dt], p.scale_log2, nb));
         O[dt] = mfma32(va[0][dt], pl[0], O[dt]);
-        if (dt == 1) {
-          float s = 0.f;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) s += P[i];
-          ls += s;
-        }
+        const u32x2 hl = split_pair(P[8 + 2 * dt], P[9 + 2 * dt]);
+        pb[1][dt] = hl[0];
+        pl[1][dt] = hl[1];
         __builtin_amdgcn_sched_barrier(0);
       }
-      bias = unit_max<K>(Sn, u1, pair, lane, p.scale_log2, mloc);
+      // stage C: the 8 P.V products of k step 1 with the max of unit i+1
+      // and the lane's fp32 sum of P (the denominator)
+      if (NB == 1) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
+        if (dt == 0) bias = unit_max<K>(Sn, u1, pair, lane, p.scale_log2, mloc);
         O[dt] = mfma32(va[1][dt], pl[1], O[dt]);
+        if (dt == 1) {
+          float s = 0.f;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) s += P[k];
+          ls += s;
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else {
       // One instruction stream that keeps the matrix pipe fed: the 8
