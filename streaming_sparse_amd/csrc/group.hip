@@ -17,7 +17,9 @@
 // float32 rounding.  The batch is layers x heads independent rows b.
 //   project_kernel   grid (72 token blocks, B): raw key and value projections
 //   features_kernel  grid (B), 1024 threads: head-wide reductions, features
-//   level_kernel     grid (B x groups): stats, power steps, bitonic sort
+//   level_kernel     grid (B x groups): levels 0 and 1 (groups of 4608, 1536):
+//                    stats, power steps, bitonic sort, rows through memory
+//   fused_levels_kernel  grid (B x 9): levels 2..6 inside each 512-row group
 //   frames_kernel    grid (B): the first chunk's stable partition by frame
 #include "common.h"
 
@@ -29,8 +31,6 @@ constexpr int kTokens = 4608;      // 3 frames x 1536
 constexpr int kFrame = 1536;
 constexpr int kR = 32;             // feature width
 constexpr int kPages = 72;
-constexpr int kLevels = 7;
-constexpr int kLevelSize[kLevels] = {4608, 1536, 512, 256, 128, 64, 32};
 constexpr double kInvSqrtD = 11.313708498984761;   // sqrt(128), divided by as the reference does
 
 struct GroupParams {
@@ -234,11 +234,9 @@ __device__ __forceinline__ double sum8(double x) {
 // One level of the balanced split: each workgroup takes one group of n rows
 // of one b, in the current order (rows in[0..n) of the group), and writes
 // them stably sorted by their projection on the power-iteration direction.
-// Thread: features 4 q .. 4 q + 3 (q = tid & 7), rows tid / 8 + 32 i.  The
-// last level writes the final order (page permutation applied) instead of
-// features.
-template <int SORTN, bool LAST>
-__global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int groups, int src, int32_t* last_out) {
+// Thread: features 4 q .. 4 q + 3 (q = tid & 7), rows tid / 8 + 32 i.
+template <int SORTN>
+__global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int groups, int src) {
   __shared__ unsigned long long key[SORTN];
   __shared__ unsigned short pos[SORTN];
   __shared__ double red[32][kR + 1];
@@ -356,21 +354,183 @@ __global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int gr
       __syncthreads();
     }
   }
-  if (!LAST) {
-    double* xo = p.x[src ^ 1] + row0 * kR;
-    int32_t* io = p.ids[src ^ 1] + row0;
-    for (int j = rs; j < n; j += 32) {
-      const int s = pos[j];
+  double* xo = p.x[src ^ 1] + row0 * kR;
+  int32_t* io = p.ids[src ^ 1] + row0;
+  for (int j = rs; j < n; j += 32) {
+    const int s = pos[j];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) xo[(long long)j * kR + 4 * q + c] = x[(long long)s * kR + 4 * q + c];
-      if (q == 0) io[j] = ids[s];
+    for (int c = 0; c < 4; ++c) xo[(long long)j * kR + 4 * q + c] = x[(long long)s * kR + 4 * q + c];
+    if (q == 0) io[j] = ids[s];
+  }
+}
+
+// Levels 2..6 of the balanced split in one workgroup per 512-row group (a
+// ninth of the chunk, as level 1 leaves it): the group's fp64 rows and token
+// ids stay in LDS; level l sorts every aligned block of n = 512 >> (l - 2)
+// rows by the block's own projection, all blocks at once, and a permutation
+// of row slots carries the order from level to level.  Per block the steps
+// and their arithmetic are level_kernel's.  Thread: features 4 q .. 4 q + 3
+// (q = tid & 7), 8 rows of its block; the 512 / G threads of a block (G
+// blocks) sum through LDS.  The last level writes the final order.
+constexpr int kFuse = 512;
+constexpr int kFuseLevels = 5;
+constexpr int kFuseThreads = 512;
+constexpr int kFuseGroups = kFuseThreads / 8;    // row groups of 8 threads
+constexpr int kFuseRows = kFuse / kFuseGroups;   // rows per thread
+
+__global__ __launch_bounds__(kFuseThreads, 1) void fused_levels_kernel(GroupParams p, int src, int32_t* last_out) {
+  __shared__ alignas(16) double xs[kFuse][kR];   // 128 KB: rows in level 2's input order
+  __shared__ unsigned short perm[2][kFuse];      // row slot at each position
+  __shared__ int tok[kFuse];
+  // the sums of the statistics and the sort keys are never live together
+  __shared__ union {
+    double red[kFuseGroups][kR + 1];
+    struct {
+      unsigned long long key[kFuse];
+      unsigned short pos[kFuse];
+    } s;
+  } u;
+  __shared__ double vec[2][kFuse / 32][kR];      // per block: mean | variance, then power-step sums
+  __shared__ int axis[kFuse / 32];
+  auto& red = u.red;
+  auto& key = u.s.key;
+  auto& pos = u.s.pos;
+  const int tid = threadIdx.x, q = tid & 7, rg = tid >> 3;
+  const int b = blockIdx.x / (kTokens / kFuse), gi = blockIdx.x % (kTokens / kFuse);
+  const long long row0 = (long long)b * kTokens + (long long)gi * kFuse;
+  {
+    const f32x4* xsrc = reinterpret_cast<const f32x4*>(p.x[src] + row0 * kR);
+    f32x4* xdst = reinterpret_cast<f32x4*>(&xs[0][0]);
+    for (int e = tid; e < kFuse * kR / 2; e += kFuseThreads) xdst[e] = xsrc[e];
+    for (int i = tid; i < kFuse; i += kFuseThreads) {
+      tok[i] = p.ids[src][row0 + i];
+      perm[0][i] = (unsigned short)i;
     }
-  } else {
-    // groups of 32 are page halves: destination page of this group's page
-    const int in_head = gi * n, page = in_head / 64;
+  }
+  __syncthreads();
+  int cur = 0;
+  for (int lv = 0; lv < kFuseLevels; ++lv) {
+    const int n = kFuse >> lv, G = kFuse / n, T = kFuseThreads / G;   // block size, blocks, threads per block
+    const int blk = tid / T, nrg = T >> 3, rgl = (tid % T) >> 3;
+    const unsigned short* pm = perm[cur];
+    // this thread's rows: positions blk * n + rgl + nrg * i, i < kFuseRows
+    auto xrow = [&](int i) -> const double* { return xs[pm[blk * n + rgl + nrg * i]] + 4 * q; };
+    // per-block sums of a per-thread partial over the block's row groups
+    auto reduce_blocks = [&](const double (&a)[4], int slot) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[rg][4 * q + c] = a[c];
+      __syncthreads();
+      for (int e = tid; e < G * kR; e += kFuseThreads) {
+        const int bb = e / kR, f = e % kR;
+        double s = 0.0;
+        for (int g = 0; g < nrg; ++g) s += red[bb * nrg + g][f];
+        vec[slot][bb][f] = s;
+      }
+      __syncthreads();
+    };
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int i = 0; i < kFuseRows; ++i) {
+      const double* xr = xrow(i);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] += xr[c];
+    }
+    reduce_blocks(acc, 0);
+    double mean[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) mean[c] = vec[0][blk][4 * q + c] / n;
+    // highest-variance feature (first of equals) -> one-hot start direction
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = 0.0;
+    for (int i = 0; i < kFuseRows; ++i) {
+      const double* xr = xrow(i);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const double xc = xr[c] - mean[c];
+        acc[c] = fma(xc, xc, acc[c]);
+      }
+    }
+    reduce_blocks(acc, 1);
+    if (tid < G) {
+      int best = 0;
+      double bv = vec[1][tid][0] / n;
+      for (int d = 1; d < kR; ++d) {
+        const double vd = vec[1][tid][d] / n;
+        if (vd > bv) {
+          bv = vd;
+          best = d;
+        }
+      }
+      axis[tid] = best;
+    }
+    __syncthreads();
+    double dir[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dir[c] = (4 * q + c == axis[blk]) ? 1.0 : 0.0;
+    for (int it = 0; it < 4; ++it) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = 0.0;
+      for (int i = 0; i < kFuseRows; ++i) {
+        const double* xr = xrow(i);
+        double xc[4], pr = 0.0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          xc[c] = xr[c] - mean[c];
+          pr = fma(xc[c], dir[c], pr);
+        }
+        pr = sum8(pr);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = fma(xc[c], pr, acc[c]);
+      }
+      reduce_blocks(acc, 1);
+      double nrm = 0.0;
+      for (int d = 0; d < kR; ++d) nrm = fma(vec[1][blk][d], vec[1][blk][d], nrm);
+      nrm = fmax(sqrt(nrm), 1e-8);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dir[c] = vec[1][blk][4 * q + c] / nrm;
+      __syncthreads();
+    }
+    // projections -> sort keys (ascending score, ties -> current position)
+    for (int i = 0; i < kFuseRows; ++i) {
+      const double* xr = xrow(i);
+      double pr = 0.0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) pr = fma(xr[c] - mean[c], dir[c], pr);
+      pr = sum8(pr);
+      if (q == 0) {
+        const int at = blk * n + rgl + nrg * i;
+        key[at] = order_key(pr);
+        pos[at] = (unsigned short)at;
+      }
+    }
+    __syncthreads();
+    // bitonic stages up to size n: every aligned block of n sorts on its own,
+    // ascending (the direction bit of the last stage is masked to the block);
+    // threads 0..255 each take one compare-exchange
+    for (int kk = 2; kk <= n; kk <<= 1) {
+      for (int j = kk >> 1; j > 0; j >>= 1) {
+        const int e = tid & (kFuse / 2 - 1), a = (e / j) * 2 * j + (e % j), c = a + j;
+        const bool asc = (a & kk & (n - 1)) == 0;
+        const unsigned long long ka = key[a], kc = key[c];
+        const unsigned short pa = pos[a], pc = pos[c];
+        const bool greater = ka > kc || (ka == kc && pa > pc);
+        if (tid < kFuse / 2 && greater == asc) {
+          key[a] = kc;
+          key[c] = ka;
+          pos[a] = pc;
+          pos[c] = pa;
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = tid; i < kFuse; i += kFuseThreads) perm[cur ^ 1][i] = pm[pos[i]];
+    cur ^= 1;
+    __syncthreads();
+  }
+  // final order: position j is grouped page (gi * 512 + j) / 64, row j % 64
+  for (int j = tid; j < kFuse; j += kFuseThreads) {
+    const int in_head = gi * kFuse + j, page = in_head / 64;
     const int dpage = p.page_dst ? min(max(p.page_dst[page], 0), kPages - 1) : page;   // clamped: memory safety
-    const int dst = dpage * 64 + in_head % 64;
-    for (int j = tid; j < n; j += 256) last_out[(long long)b * kTokens + dst + j] = ids[pos[j]];
+    last_out[(long long)b * kTokens + dpage * 64 + in_head % 64] = tok[perm[cur][j]];
   }
 }
 
@@ -433,24 +593,14 @@ int ssa_group_order(const void* k, const void* v, long long layer_stride, long l
   p.order = order;
   hipLaunchKernelGGL(project_kernel, dim3(kTokens / 64, p.B), dim3(256), 0, stream, p);
   hipLaunchKernelGGL(features_kernel, dim3(p.B), dim3(1024), 0, stream, p);
-  // levels alternate buffers 0 -> 1 -> 0 ...; the last writes the order (or
-  // the frame partition's input)
+  // levels 0 and 1 (4608 -> 3 x 1536 -> 9 x 512) through global memory,
+  // buffers 0 -> 1 -> 0; levels 2..6 inside each 512-row group, which
+  // writes the order (or the frame partition's input)
   int32_t* last_out = first_chunk ? p.ids[1] : order;
-  int src = 0;
-  for (int lv = 0; lv < kLevels; ++lv) {
-    const int n = kLevelSize[lv], groups = kTokens / n;
-    const dim3 grid(p.B * groups);
-    switch (lv) {
-      case 0: hipLaunchKernelGGL((level_kernel<8192, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
-      case 1: hipLaunchKernelGGL((level_kernel<2048, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
-      case 2: hipLaunchKernelGGL((level_kernel<512, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
-      case 3: hipLaunchKernelGGL((level_kernel<256, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
-      case 4: hipLaunchKernelGGL((level_kernel<128, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
-      case 5: hipLaunchKernelGGL((level_kernel<64, false>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
-      default: hipLaunchKernelGGL((level_kernel<32, true>), grid, dim3(256), 0, stream, p, n, groups, src, last_out); break;
-    }
-    src ^= 1;
-  }
+  hipLaunchKernelGGL(level_kernel<8192>, dim3(p.B), dim3(256), 0, stream, p, kTokens, 1, 0);
+  hipLaunchKernelGGL(level_kernel<2048>, dim3(p.B * 3), dim3(256), 0, stream, p, kTokens / 3, 3, 1);
+  hipLaunchKernelGGL(fused_levels_kernel, dim3(p.B * (kTokens / kFuse)), dim3(kFuseThreads), 0, stream, p, 0,
+                     last_out);
   if (first_chunk) hipLaunchKernelGGL(frames_kernel, dim3(p.B), dim3(256), 0, stream, p.ids[1], order);
   return (int)hipGetLastError();
 }
