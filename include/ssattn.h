@@ -19,6 +19,8 @@
  *   ssa_route       <- VB/graph.py:102-211 BatchGraphs.compute (probe QK, risk,
  *                      quota_mask / base selection, final LUT) and
  *                      VR/legacy_components.py:14-22 risk(probes,z,summary,theta)
+ *   ssa_select      <- RV/ops.py:113-138 RouteOps.select(scores,own,config,
+ *                      threshold,valid): counts, overflow, -1 padding, residual
  *   ssa_encode      <- VR/page.py:6-14 encode(summary,reader,phi,B) and
  *                      VideoRuntime.encode (VR/runtime.py:160-164)
  *   ssa_summary     <- the current-chunk summary recompute of VideoRuntime.forward
@@ -102,6 +104,23 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
               int pages, int head_pages, int count, int mode, int total, const void* mean, const void* detail,
               const void* basis, void* rep_values, int rep_head_pages, hipStream_t stream);
+
+/* Page selection from given scores (RV/ops.py:113-138 RouteOps.select), one
+ * row per (head, block): scores [rows,pages] fp32, own [rows] int32, valid
+ * [rows,pages] 0/1 bytes or NULL (all valid).  Pages rank with own first,
+ * then valid pages by descending score (ties -> lower page), invalid pages
+ * last.  use_threshold != 0: count = clamp(#(valid and score > threshold, own
+ * counted), 1, cap) and overflow[row] = max(that number - cap, 0), with cap =
+ * min(id_capacity, ceil(max_fraction * pages)) computed by the caller;
+ * use_threshold == 0: count = min(fixed_count, #valid) (fixed_count =
+ * max(1, floor(pages * density))) and overflow 0.  ids [rows,id_capacity]
+ * int32: the first count ranked pages, then -1 (never to be read); counts
+ * [rows] int32; mask [rows,pages] 0/1 bytes; residual [rows] fp32: the sum
+ * of the scores of the valid unselected pages.  pages <= 512, 1 <= cap <=
+ * min(id_capacity, pages). */
+int ssa_select(const float* scores, const int32_t* own, const uint8_t* valid, int rows, int pages, float threshold,
+               int use_threshold, int fixed_count, int cap, int id_capacity, int32_t* ids, int32_t* counts,
+               uint8_t* mask, int32_t* overflow, float* residual, hipStream_t stream);
 
 /* Page summaries of pages [first_page, first_page + pages) of the resident
  * cache (k, v addressed as in ssa_attention): a 4-way k-means of each page's

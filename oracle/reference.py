@@ -185,6 +185,41 @@ def select_topk(risk_, own, count):
     return ids.int(), mask
 
 
+def select_counts(scores, own, *, threshold=None, valid=None, density=0.10, max_fraction=0.25,
+                  id_capacity=128):
+    """RouteOps.select (RV/ops.py:113-138): the pages ranked by score with
+    invalid pages at -inf and own at +inf (ties -> lower page); with a
+    threshold, count = clamp(#(score > threshold and valid, own forced), 1,
+    cap) and overflow the excess over cap = min(id_capacity, ceil(max_fraction
+    P)); without, count = min(max(1, floor(P density)), #valid) and no
+    overflow.  ids = the top count pages then -1 up to id_capacity; mask the
+    selected pages; residual_risk = the sum of the scores of the valid
+    unselected pages (float64 here)."""
+    h, t, p = scores.shape
+    if valid is None:
+        valid = torch.ones(h, t, p, dtype=torch.bool)
+    valid = valid.expand(h, t, p)
+    cap = min(id_capacity, math.ceil(max_fraction * p))
+    ranked = scores.double().masked_fill(~valid, -torch.inf).scatter(-1, own[..., None].long(), torch.inf)
+    order = ranked.sort(dim=-1, descending=True, stable=True).indices[..., :min(id_capacity, p)]
+    if threshold is None:
+        count = torch.full((h, t), max(1, math.floor(p * density)), dtype=torch.long)
+        count = torch.minimum(count, valid.sum(-1))
+        overflow = torch.zeros_like(count)
+    else:
+        eligible = ((scores > threshold) & valid).scatter(-1, own[..., None].long(), True)
+        wanted = eligible.sum(-1)
+        overflow = (wanted - cap).clamp_min(0)
+        count = wanted.clamp(1, cap)
+    active = torch.arange(order.shape[-1]) < count[..., None]
+    ids = order.masked_fill(~active, -1)
+    if ids.shape[-1] < id_capacity:
+        ids = torch.nn.functional.pad(ids, (0, id_capacity - ids.shape[-1]), value=-1)
+    mask = torch.zeros(h, t, p, dtype=torch.bool).scatter(-1, order, active)
+    residual = scores.double().masked_fill(mask | ~valid, 0).sum(-1)
+    return dict(ids=ids.int(), counts=count.int(), mask=mask, overflow=overflow.int(), residual_risk=residual)
+
+
 def mask_from_ids(ids, pages):
     """Selected-page set of each (head, block) from its LUT
     (RV/tuned_attention.py:37-40; LE high_sparse_runtime.py:12-17); entries

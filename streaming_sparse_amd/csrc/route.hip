@@ -635,6 +635,112 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   }
 }
 
+
+// RouteOps.select (RV/ops.py:113-138) on caller-given scores: one
+// workgroup of 128 threads per (head, block) row, 4 pages per thread, and the
+// router's descending sort of 512 64-bit keys: own first, then the valid
+// pages by descending score (ties -> lower page), invalid and absent pages
+// last.  count = clamp(#eligible, 1, cap) with overflow the excess over cap
+// (threshold mode: eligible = valid and score > threshold, own forced), or
+// min(fixed_count, #valid) without overflow; ids = the first count pages,
+// then -1 up to id_capacity; residual = the sum of the scores of the valid
+// unselected pages.
+struct SelectParams {
+  const float* scores;     // [rows, P]
+  const int32_t* own;      // [rows]
+  const uint8_t* valid;    // [rows, P] or null: every page valid
+  int32_t* ids;            // [rows, id_capacity]
+  int32_t* counts;         // [rows]
+  uint8_t* mask;           // [rows, P]
+  int32_t* overflow;       // [rows]
+  float* residual;         // [rows]
+  int P, id_capacity, cap, fixed_count, use_threshold;
+  float threshold;
+};
+
+// Sum over the 128 threads of a workgroup (two waves); every thread gets it.
+template <typename T>
+__device__ __forceinline__ T sum128(T x, T* part, int bt) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  if ((bt & 63) == 0) part[bt >> 6] = x;
+  __syncthreads();
+  const T s = part[0] + part[1];
+  __syncthreads();
+  return s;
+}
+
+__global__ __launch_bounds__(128) void select_kernel(SelectParams p) {
+  __shared__ unsigned long long xchg[kMaxPages];
+  __shared__ uint8_t sel[kMaxPages];
+  __shared__ int ipart[2];
+  __shared__ float fpart[2];
+  const int row = blockIdx.x, bt = threadIdx.x;
+  const float* sc = p.scores + (long long)row * p.P;
+  const uint8_t* vl = p.valid ? p.valid + (long long)row * p.P : nullptr;
+  // an own page outside the window is clamped into it (memory safety of the
+  // per-page state; a valid own is in [0, P))
+  const int own = min(max(p.own[row], 0), p.P - 1);
+  unsigned long long keys[4];
+  float sv[4];
+  bool vv[4];
+  int elig = 0, nvalid = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pg = 4 * bt + i;
+    unsigned long long key = 0ull;
+    sv[i] = 0.f;
+    vv[i] = false;
+    if (pg < p.P) {
+      const bool v = vl ? vl[pg] != 0 : true;
+      const float x = sc[pg];
+      sv[i] = x;
+      vv[i] = v;
+      if (pg == own) key = ~0ull - (unsigned long long)pg;   // top, and decodes to pg
+      else if (v) key = (1ull << 62) | ((unsigned long long)orderable(x) << 30) | (unsigned long long)(1023 - pg);
+      elig += ((v && x > p.threshold) || pg == own) ? 1 : 0;
+      nvalid += v ? 1 : 0;
+    }
+    keys[i] = key;
+    sel[pg] = 0;
+  }
+  elig = sum128(elig, ipart, bt);
+  nvalid = sum128(nvalid, ipart, bt);
+  sort512_desc(keys, bt, xchg);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xchg[4 * bt + i] = keys[i];
+  __syncthreads();
+  int count, over = 0;
+  if (p.use_threshold) {
+    count = min(max(elig, 1), p.cap);
+    over = max(elig - p.cap, 0);
+  } else {
+    count = min(p.fixed_count, nvalid);
+  }
+  int32_t* idrow = p.ids + (long long)row * p.id_capacity;
+  for (int i = bt; i < p.id_capacity; i += 128) {
+    const int pg = i < count ? 1023 - (int)(xchg[i] & 1023ull) : -1;
+    idrow[i] = pg;
+    if (pg >= 0) sel[pg] = 1;
+  }
+  __syncthreads();
+  float res = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pg = 4 * bt + i;
+    if (pg < p.P) {
+      p.mask[(long long)row * p.P + pg] = sel[pg];
+      if (vv[i] && !sel[pg]) res += sv[i];
+    }
+  }
+  res = sum128(res, fpart, bt);
+  if (bt == 0) {
+    p.counts[row] = count;
+    p.overflow[row] = over;
+    p.residual[row] = res;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -691,6 +797,35 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
   const int np = (blocks + 1) / 2;
   const int nrv = rep_values ? (heads * pages + kRvPages - 1) / kRvPages : 0;
   hipLaunchKernelGGL(route_kernel, dim3(heads * np + nrv), dim3(kThreads), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+
+// RouteOps.select on given scores; see select_kernel.  use_threshold = 0:
+// count = min(fixed_count, #valid).
+int ssa_select(const float* scores, const int32_t* own, const uint8_t* valid, int rows, int pages, float threshold,
+               int use_threshold, int fixed_count, int cap, int id_capacity, int32_t* ids, int32_t* counts,
+               uint8_t* mask, int32_t* overflow, float* residual, hipStream_t stream) {
+  if (rows <= 0 || pages <= 0 || pages > kMaxPages || id_capacity < 1 || cap < 1 || cap > id_capacity ||
+      cap > pages || (!use_threshold && (fixed_count < 1 || fixed_count > id_capacity)) || !scores || !own ||
+      !ids || !counts || !mask || !overflow || !residual)
+    return (int)hipErrorInvalidValue;
+  SelectParams p;
+  p.scores = scores;
+  p.own = own;
+  p.valid = valid;
+  p.ids = ids;
+  p.counts = counts;
+  p.mask = mask;
+  p.overflow = overflow;
+  p.residual = residual;
+  p.P = pages;
+  p.id_capacity = id_capacity;
+  p.cap = cap;
+  p.fixed_count = fixed_count;
+  p.use_threshold = use_threshold;
+  p.threshold = threshold;
+  hipLaunchKernelGGL(select_kernel, dim3(rows), dim3(128), 0, stream, p);
   return (int)hipGetLastError();
 }
 

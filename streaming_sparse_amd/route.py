@@ -138,3 +138,42 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
         stats = workspace.entries[key]
     # uint8 0/1 storage viewed as bool without a conversion kernel
     return ids, (mask.view(torch.bool) if mask is not None else None), risk, stats
+
+
+@torch.no_grad()
+def select(scores, own, config=None, threshold=None, valid=None, *, density=0.10, max_fraction=0.25,
+           id_capacity=128):
+    """RouteOps.select (local_experiments/review_v1/ops.py:113-138) on the HIP
+    library: scores [H,T,P] (a page risk), own [H,T] (one protected page per
+    row), `config` any object with density / max_fraction / id_capacity (the
+    reference's Config; keyword defaults otherwise), optional threshold and
+    valid [H,T,P] bool.  Returns dict(ids [H,T,id_capacity] int32 with -1
+    padding, counts [H,T] int32, mask [H,T,P] bool, overflow [H,T] int32,
+    residual_risk [H,T] fp32) as the reference does."""
+    if config is not None:
+        density, max_fraction, id_capacity = config.density, config.max_fraction, config.id_capacity
+    h, t, p = scores.shape
+    if not 0 < density <= max_fraction <= 1 or id_capacity < math.ceil(max_fraction * p):
+        raise ValueError("need 0 < density <= max_fraction <= 1 and id_capacity >= ceil(max_fraction * P)")
+    if p > 512:
+        raise ValueError("at most 512 pages")
+    dev = scores.device
+    sc = scores.float().contiguous()
+    ow = own.to(device=dev, dtype=torch.int32).expand(h, t).contiguous()
+    vd = None
+    if valid is not None:
+        vd = valid.expand(h, t, p).to(device=dev, dtype=torch.uint8).contiguous()
+    cap = min(id_capacity, math.ceil(max_fraction * p))
+    fixed = max(1, math.floor(p * density))
+    ids = torch.empty(h, t, id_capacity, device=dev, dtype=torch.int32)
+    counts = torch.empty(h, t, device=dev, dtype=torch.int32)
+    mask = torch.empty(h, t, p, device=dev, dtype=torch.uint8)
+    overflow = torch.empty(h, t, device=dev, dtype=torch.int32)
+    residual = torch.empty(h, t, device=dev, dtype=torch.float32)
+    thr = 0.0 if threshold is None else float(threshold)
+    _lib.check(_lib.lib().ssa_select(_lib.ptr(sc), _lib.ptr(ow), _lib.ptr(vd), h * t, p, thr,
+                                     int(threshold is not None), fixed, cap, id_capacity, _lib.ptr(ids),
+                                     _lib.ptr(counts), _lib.ptr(mask), _lib.ptr(overflow), _lib.ptr(residual),
+                                     _lib.stream_handle(dev)), "ssa_select")
+    return dict(ids=ids, counts=counts, mask=mask.view(torch.bool), overflow=overflow, residual_risk=residual)
+

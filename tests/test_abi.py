@@ -21,8 +21,9 @@ def declared():
 
 
 def test_header_declares_entry_points():
-    assert set(declared()) == {"ssa_rep_values", "ssa_attention", "ssa_route", "ssa_encode", "ssa_pset", "ssa_summary",
-                               "ssa_pset_noalloc", "ssa_anchor_rebase", "ssa_commit_pages", "ssa_group_order"}
+    assert set(declared()) == {"ssa_rep_values", "ssa_attention", "ssa_route", "ssa_select", "ssa_encode", "ssa_pset",
+                               "ssa_summary", "ssa_pset_noalloc", "ssa_anchor_rebase", "ssa_commit_pages",
+                               "ssa_group_order"}
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libssattn.so not built")

@@ -11,7 +11,7 @@ from streaming_sparse_amd import _lib, workload
 from streaming_sparse_amd.attention import Workspace
 from streaming_sparse_amd.legacy_components import attention, kv_strides
 from streaming_sparse_amd.ops import Summary
-from streaming_sparse_amd.route import route, tier_count
+from streaming_sparse_amd.route import route, select, tier_count
 
 INVALID = 1   # hipErrorInvalidValue
 H, D = 2, 128
@@ -150,6 +150,18 @@ def test_c_abi_rejects_bad_shapes():
     assert rt(80, 44, 1, 20, cur=8) == INVALID                        # 72 < P < 96: no such window
     assert rt(432, 64, 0, 0, rv=16, mean=None) == INVALID            # rep values without mean/detail/basis
     assert rt(432, 64, 0, 0, rv=16, mean=8) == INVALID               # misaligned
+    # ssa_select: 0 < pages <= 512, 1 <= cap <= min(id_capacity, pages), density count <= id_capacity,
+    # scores / own / outputs present (valid may be NULL)
+    sel = lambda rows, pages, thr, fixed, cap, idcap, sc=8: L.ssa_select(sc, 8, N, rows, pages, 0.0, thr, fixed, cap,
+                                                                           idcap, 8, 8, 8, 8, 8, N)
+    assert sel(0, 410, 1, 41, 103, 128) == INVALID
+    assert sel(6, 513, 1, 41, 103, 128) == INVALID
+    assert sel(6, 410, 1, 41, 129, 128) == INVALID                    # cap > id_capacity
+    assert sel(6, 90, 1, 9, 100, 128) == INVALID                      # cap > pages
+    assert sel(6, 410, 1, 41, 0, 128) == INVALID
+    assert sel(6, 410, 0, 0, 103, 128) == INVALID                     # density count < 1
+    assert sel(6, 410, 0, 129, 103, 128) == INVALID                   # density count > id_capacity
+    assert sel(6, 410, 1, 41, 103, 128, sc=None) == INVALID
     # ssa_summary: page range inside the slab, iters >= 1
     sm = lambda first, pages, iters, init: L.ssa_summary(N, N, 1536, 128, init, N, N, N, N, N, 432, 12, first, pages,
                                                          iters, N)
@@ -167,3 +179,18 @@ def test_c_abi_rejects_bad_shapes():
     assert ps(96, 40) == INVALID
     assert ps(432, 400) == INVALID
     assert L.ssa_rep_values(N, N, N, N, 0, 432, 432, 432, N) == INVALID
+
+
+def test_select_rejects_bad_config():
+    """select checks the reference Config's invariants
+    (RV/ops.py:21-24) before it calls the library."""
+    from types import SimpleNamespace
+    scores = torch.zeros(1, 1, 410)
+    own = torch.zeros(1, 1, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        select(scores, own, SimpleNamespace(density=0.3, max_fraction=0.25, id_capacity=128))
+    with pytest.raises(ValueError):
+        select(scores, own, SimpleNamespace(density=0.1, max_fraction=0.25, id_capacity=100))
+    with pytest.raises(ValueError):
+        select(torch.zeros(1, 1, 600), own, id_capacity=200)
+

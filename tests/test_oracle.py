@@ -338,3 +338,57 @@ def test_quota_table_contract():
     n = a + b
     assert (n == n[..., :1]).all()
     assert abs(float(n.float().mean()) - 40.8) < 1.5
+
+
+def test_select_counts_reference_contract():
+    """The reference's own CPU contract for RouteOps.select
+    (RV/test_ops.py:39-47): every page eligible at threshold -1 on a 410-page
+    window caps the count at ceil(0.25 * 410) = 103 with 307 overflow, own is
+    selected, ids past the count are -1, the mask holds count pages."""
+    g = torch.Generator().manual_seed(192)
+    scores = torch.rand(2, 3, 410, generator=g)
+    own = torch.tensor([[338, 339, 340]]).expand(2, -1)
+    s = ref.select_counts(scores, own, threshold=-1)
+    assert (s['counts'] == 103).all() and (s['overflow'] == 307).all()
+    assert s['mask'].gather(-1, own[..., None]).all()
+    assert (s['ids'][..., 103:] == -1).all() and s['ids'].shape[-1] == 128
+    assert (s['mask'].sum(-1) == s['counts']).all()
+
+
+def _brute_select(sc, own, valid, threshold, density, max_fraction, cap_ids):
+    """Plain-Python RouteOps.select of one row."""
+    p = len(sc)
+    cap = min(cap_ids, math.ceil(max_fraction * p))
+    key = lambda i: (2, 0.0) if i == own else ((1, sc[i]) if valid[i] else (0, 0.0))
+    order = sorted(range(p), key=lambda i: (key(i)[0], key(i)[1], -i), reverse=True)
+    if threshold is None:
+        count, over = min(max(1, math.floor(p * density)), sum(valid)), 0
+    else:
+        wanted = sum(1 for i in range(p) if (valid[i] and sc[i] > threshold) or i == own)
+        count, over = min(max(wanted, 1), cap), max(wanted - cap, 0)
+    chosen = order[:count]
+    resid = sum(sc[i] for i in range(p) if valid[i] and i not in chosen)
+    return chosen, count, over, resid
+
+
+@pytest.mark.parametrize("threshold", [None, 0.0, 3.5, 100.0])
+def test_select_counts_brute_force(threshold):
+    """Integer-binned scores (many ties), a random valid mask with own valid,
+    thresholds below, inside and above the score range: ids, counts, overflow,
+    mask and residual risk equal a plain-Python restatement."""
+    g = torch.Generator().manual_seed(7)
+    h, t, p = 2, 3, 96
+    scores = torch.randint(-3, 8, (h, t, p), generator=g).float()
+    valid = torch.rand(h, t, p, generator=g) > 0.2
+    own = torch.randint(0, p, (h, t), generator=g)
+    valid.scatter_(-1, own[..., None], True)
+    s = ref.select_counts(scores, own, threshold=threshold, valid=valid, density=0.1, max_fraction=0.25,
+                          id_capacity=40)
+    for hh in range(h):
+        for tt in range(t):
+            chosen, count, over, resid = _brute_select(scores[hh, tt].tolist(), int(own[hh, tt]),
+                                                      valid[hh, tt].tolist(), threshold, 0.1, 0.25, 40)
+            assert int(s['counts'][hh, tt]) == count and int(s['overflow'][hh, tt]) == over
+            assert s['ids'][hh, tt].tolist() == chosen + [-1] * (40 - count)
+            assert sorted(torch.nonzero(s['mask'][hh, tt]).flatten().tolist()) == sorted(chosen)
+            assert float(s['residual_risk'][hh, tt]) == resid
