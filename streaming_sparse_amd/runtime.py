@@ -202,10 +202,13 @@ class StreamRuntime:
     def chunk_inputs(self, chunk: int | None = None):
         """Seeded Q/K/V of every (step, layer) of a chunk, RoPE at its absolute
         frames 3c..3c+2: list [steps + 1][layers] of (q [1,N,H,D], k, v
-        [N,H,D]) bf16 device tensors."""
+        [N,H,D]) bf16 device tensors.  The chunk's quota table (the policy
+        table the reference loads, VB/queue_policy.py:18-33) is prepared with
+        them."""
         c = self.chunk if chunk is None else chunk
         cfg = self.cfg
         dev = self.device
+        self.quota(c)
         # the clean step's K/V of all layers in one [L, N, H, D] block each, so
         # the commit groups every layer in one batch
         clean_k = torch.empty(cfg.layers, self.N, self.H, HEAD_DIM, device=dev, dtype=torch.bfloat16)
@@ -233,9 +236,13 @@ class StreamRuntime:
 
     def quota(self, chunk: int):
         if chunk not in self.quotas:
+            for done in [c for c in self.quotas if c < chunk - 1]:
+                del self.quotas[done]
             tab = workload.quota_table(self.cfg.seed, layers=max(self.cfg.layers - 1, 1), steps=self.cfg.steps,
                                        heads=self.H, mean_total=self.cfg.quota_mean, window=chunk)
-            self.quotas[chunk] = (tab[..., 0].to(torch.int32).to(self.device), tab[..., 0, :].sum(-1).tolist())
+            # pinned staging: the copy does not wait for the stream's earlier work
+            cur = tab[..., 0].to(torch.int32).pin_memory().to(self.device, non_blocking=True)
+            self.quotas[chunk] = (cur, tab[..., 0, :].sum(-1).tolist())
         return self.quotas[chunk]
 
     # ------------------------------------------------------------ chunk ----
@@ -249,7 +256,7 @@ class StreamRuntime:
         if key not in self.ws.entries:
             self.ws.entries[key] = torch.empty(CURRENT, device=self.device, dtype=torch.int32)
         self.slots_dev = self.ws.entries[key]
-        self.slots_dev.copy_(torch.tensor(self.slots, dtype=torch.int32))
+        self.slots_dev.copy_(torch.tensor(self.slots, dtype=torch.int32, pin_memory=True), non_blocking=True)
         if c >= REBASE_FROM_CHUNK:
             self.rebase_anchor(rebase_offset(c))
 
@@ -258,7 +265,7 @@ class StreamRuntime:
         temporal RoPE pairs shifted by `offset` frames; the anchor pages'
         summaries and encodings rebuilt from them."""
         ph = self.freqs[offset, :TEMPORAL_PAIRS]
-        phase = torch.view_as_real(ph).to(torch.float64).contiguous().to(self.device)
+        phase = torch.view_as_real(ph).to(torch.float64).contiguous().pin_memory().to(self.device, non_blocking=True)
         H = self.H
         for li, L in enumerate(self.layers):
             src = L.canonical
