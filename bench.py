@@ -39,7 +39,7 @@ sys.path.insert(0, ROOT)
 # HBM bytes per attn_kernel launch of the base-tier call, keyed by (pages, exact pages, single-term P.V),
 # measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this bench (profiles/attn_kernel_base432_traffic.md):
 # 116.5 MB read + 14.2 MB written in either P.V arithmetic
-MEASURED_TRAFFIC = {(432, 64, False): 130.6e6, (432, 64, True): 130.6e6}
+MEASURED_TRAFFIC = {(432, 64, False): 123.3e6, (432, 64, True): 123.3e6}
 METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
@@ -108,24 +108,23 @@ def call_timings(g, P, C, single, steps, warmup, stream):
     calls, kept out of the timed region whose calls they would space out)."""
     import torch
     from streaming_sparse_amd.attention import Workspace
-    from streaming_sparse_amd.legacy_components import attention
+    from streaming_sparse_amd.legacy_components import REP_OP_ELEMS, attention, rep_tiles
     from streaming_sparse_amd.route import route
     dev = g.q.device
     H, D = 12, 128
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()   # the caller keeps the basis bf16-rounded
-    vrep = ws.tensor('call_rep_values', (H, P, 4, D), dev, torch.bfloat16)
+    ops = ws.tensor('call_rep_ops', (H, rep_tiles(P), REP_OP_ELEMS), dev, torch.bfloat16)
 
     def step(marks=None):
         # own page of block t is P-72+t (the router's default when own is None); the router also writes
-        # the call's rep value rows, which the attention kernel reads
+        # the call's detail operand tiles, which the attention kernel reads
         if marks:
             marks[0].record(stream)
-        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_basis=basis,
-                             rep_out=vrep)
+        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_out=ops)
         if marks:
             marks[1].record(stream)
-        o = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, single_av=single, rep_values=vrep)
+        o = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, single_av=single, rep_ops=ops)
         if marks:
             marks[2].record(stream)
         return o
@@ -173,7 +172,7 @@ def main():
     import torch
     from streaming_sparse_amd import _lib, workload
     from streaming_sparse_amd.attention import Workspace
-    from streaming_sparse_amd.legacy_components import attention, rep_values, kv_strides
+    from streaming_sparse_amd.legacy_components import REP_OP_ELEMS, attention, kv_strides, rep_operands, rep_tiles
     from streaming_sparse_amd.route import route
 
     dev = torch.device("cuda:0")
@@ -200,31 +199,31 @@ def main():
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()
     ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
-    vrep = ws.tensor('ssa_rep_values', (H, P, 4, D), dev, torch.bfloat16)
-    rep_values(g.summary, basis, P, vrep)
+    ops = ws.tensor('ssa_rep_ops', (H, rep_tiles(P), REP_OP_ELEMS), dev, torch.bfloat16)
+    rep_operands(g.summary, P, ops)
     out = torch.empty_like(g.q)
     tok, head = kv_strides(g.k, g.v)
     L = _lib.lib()
 
     def attn_only(flags):
         _lib.check(L.ssa_attention(_lib.ptr(g.q), _lib.ptr(g.k), _lib.ptr(g.v), _lib.ptr(g.summary.keys),
-                                   _lib.ptr(vrep), _lib.ptr(ids), _lib.ptr(out), N, H, P,
-                                   g.summary.head_pages, P, C, tok, head, flags, _lib.stream_handle(dev)),
-                   "ssa_attention")
+                                   _lib.ptr(g.summary.mean), _lib.ptr(basis), _lib.ptr(ops), _lib.ptr(ids),
+                                   _lib.ptr(out), N, H, P, g.summary.head_pages, ops.shape[1], C, tok, head, flags,
+                                   _lib.stream_handle(dev)), "ssa_attention")
 
     iters = max(10, args.steps)
     attn_ms = {name: time_loop(lambda f=f: attn_only(f), iters, stream) for name, f in (("two_term", 1),
                                                                                        ("single_term", 0))}
     rids, _, rrisk, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
-    vrep_call = torch.empty(H, P, 4, D, device=dev, dtype=torch.bfloat16)
+    ops_call = torch.empty(H, rep_tiles(P), REP_OP_ELEMS, device=dev, dtype=torch.bfloat16)
     theta32 = g.theta.float().contiguous()
 
     def route_only():
         _lib.check(L.ssa_route(_lib.ptr(g.q), D, 64 * H * D, H * D, 0, _lib.ptr(g.summary.keys),
                                _lib.ptr(g.summary.stats), _lib.ptr(theta32), None, None, _lib.ptr(rrisk),
                                _lib.ptr(rids), None, None, H, N // 64, P, g.summary.head_pages, C, 0, 0,
-                               _lib.ptr(g.summary.mean), _lib.ptr(g.summary.detail), _lib.ptr(basis),
-                               _lib.ptr(vrep_call), P, _lib.stream_handle(dev)), "ssa_route")
+                               _lib.ptr(g.summary.detail), _lib.ptr(ops_call), ops_call.shape[1],
+                               _lib.stream_handle(dev)), "ssa_route")
 
     route_ms = time_loop(route_only, iters, stream)
     log(f"kernels back to back: attention {attn_ms}, route {route_ms:.4f} ms")
@@ -314,7 +313,7 @@ def main():
                                f"{'single-term' if single else 'two-term (reference)'} bf16 P.V",
                    "tier": "base", "pages": P, "exact_pages": C, "heads": H, "queries": N, "head_dim": D,
                    "single_av": single},
-        "breakdown_ms": {"route_and_rep_values": round(route_in_ms, 4), "attention_kernel": round(attn_in_ms, 4),
+        "breakdown_ms": {"route_and_rep_operands": round(route_in_ms, 4), "attention_kernel": round(attn_in_ms, 4),
                          "route_back_to_back": round(route_ms, 4),
                          "attention_back_to_back_two_term": round(attn_ms["two_term"], 4),
                          "attention_back_to_back_single_term": round(attn_ms["single_term"], 4)},
@@ -346,7 +345,7 @@ def intersection_lines(args, dense_ms, iters):
     import torch
     from streaming_sparse_amd import pset, summary, workload
     from streaming_sparse_amd.attention import Workspace
-    from streaming_sparse_amd.legacy_components import attention
+    from streaming_sparse_amd.legacy_components import REP_OP_ELEMS, attention, rep_tiles
     from streaming_sparse_amd.route import route
 
     dev = torch.device("cuda:0")
@@ -366,19 +365,19 @@ def intersection_lines(args, dense_ms, iters):
         device=dev, dtype=torch.int32)
     recompute = lambda: summary.build(g.k, g.v, basis, init, g.summary, P - 72, 72)
 
-    vrep = ws.tensor('call_rep_values', (12, P, 4, 128), dev, torch.bfloat16)
+    ops = ws.tensor('call_rep_ops', (12, rep_tiles(P), REP_OP_ELEMS), dev, torch.bfloat16)
 
     def plain(single=None):
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
-                             want_mask=False, rep_basis=basis, rep_out=vrep)
-        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep, single_av=single)
+                             want_mask=False, rep_out=ops)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_ops=ops, single_av=single)
 
     def corrected():
         recompute()
         pset.encode(g.summary, basis, reader, out=enc, first=P - 72, pages=72)
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='intersection', current_slots=ac, n=n, workspace=ws,
-                             full_pset=PSET_HEADS, encoding=enc, reader=reader, rep_basis=basis, rep_out=vrep)
-        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep)
+                             full_pset=PSET_HEADS, encoding=enc, reader=reader, rep_out=ops)
+        return attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_ops=ops)
 
     out = {}
     for name, fn in (("intersection", plain), ("intersection_single_term", lambda: plain(True)),

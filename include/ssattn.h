@@ -14,7 +14,7 @@
  *                      workspace,*,bf16_av) fused _tail path (RV/tuned_attention.py:
  *                      20-81) and the SM80 ctypes ABI `int run(...)`
  *                      (VR/csrc/fixed15_attention.cu:407-409, VR/fixed15_attention.py:13-32)
- *   ssa_rep_values  <- the summary half of VR/csrc/fixed15_attention.cu:551-578
+ *   ssa_rep_operands <- the summary half of VR/csrc/fixed15_attention.cu:551-578
  *                      (prepare_fixed15: per-page summary tiles for the tail)
  *   ssa_route       <- VB/graph.py:102-211 BatchGraphs.compute (probe QK, risk,
  *                      quota_mask / base selection, final LUT) and
@@ -42,33 +42,40 @@
 extern "C" {
 #endif
 
-/* Pre-projected rep values: rep_values[h,p,r,:] = bf16(mean[h,p,:] +
- * sum_k (sum_a HAAR[a,r] detail[h,p,a,k]) basis[h,:,k]) for p < pages.
- * mean [H,head_pages,128], detail [H,head_pages,3,8], basis [H,128,8] bf16;
- * rep_values [H,rep_head_pages,4,128] bf16. */
-int ssa_rep_values(const void* mean, const void* detail, const void* basis, void* rep_values, int heads,
-                   int pages, int head_pages, int rep_head_pages, hipStream_t stream);
+/* Detail operand tiles of the compensation: for each head and each tile of
+ * 16 pages (rt < ceil(pages/16)), 1536 bytes holding the detail rows
+ * detail[h,p,a,:] (a = 0..2 Haar contrasts, rank 8) of the tile's pages in
+ * the order the attention kernel's matrix products read them; pages >=
+ * `pages` hold zeros.  detail [H,head_pages,3,8] bf16; rep_ops
+ * [H,rep_tiles,768] bf16 (16-byte aligned), rep_tiles >= ceil(pages/16).
+ * Recompute when the detail rows change. */
+int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, int head_pages, int rep_tiles,
+                     hipStream_t stream);
 
 /* One page-sparse attention call: exact attention over the `count` LUT pages
  * of each (query block, head) + compensation over the reps of the unselected
  * pages + softmax-mass merge, one fused kernel.
  * q, out [1,n_tokens,H,128] bf16 contiguous; k, v: page p, token j, head h at
  * element (64p+j)*kv_token_stride + h*kv_head_stride (+ dim); keys
- * [H,head_pages,4,128] bf16 (rep keys); rep_values from ssa_rep_values;
+ * [H,head_pages,4,128] bf16 (rep keys); mean [H,head_pages,128] bf16 (page V
+ * means); basis [H,128,8] bf16; rep_ops [H,rep_tiles,768] from
+ * ssa_rep_operands (mean, basis and rep_ops 16-byte aligned; not read by a
+ * dense call, flags bit 1);
  * ids [H,n_tokens/64,count] int32: page ids, own page first; entries
  * outside [0,pages) (the -1 padding of a shorter table, RV/ops.py:115) are
  * not read and select nothing; a page listed twice is attended twice.
  * flags bit 0: two-term bf16 P.V (hi + lo parts of each probability, the
  * reference's HIGH_PRECISION_AV / BF16_AV arithmetic,
  * LE/gap_exact_round_kernel.py:98-125, RV/tuned_attention.py:16-18);
- * clear: single-term bf16 P.V.
+ * clear: single-term bf16 P.V.  The compensation weighs the page means and
+ * detail rows in the same arithmetic (two-term or one-term bf16 weights).
  * flags bit 1: the caller guarantees every row of ids lists each page of the
  * window exactly once (count == pages, a dense call); ids are then not read
  * and two query blocks share each K/V page load. */
-int ssa_attention(const void* q, const void* k, const void* v, const void* keys, const void* rep_values,
-                  const int32_t* ids, void* out, int n_tokens, int heads, int pages, int head_pages,
-                  int rep_head_pages, int count, long long kv_token_stride, long long kv_head_stride, int flags,
-                  hipStream_t stream);
+int ssa_attention(const void* q, const void* k, const void* v, const void* keys, const void* mean, const void* basis,
+                  const void* rep_ops, const int32_t* ids, void* out, int n_tokens, int heads, int pages,
+                  int head_pages, int rep_tiles, int count, long long kv_token_stride, long long kv_head_stride,
+                  int flags, hipStream_t stream);
 
 /* Router: risk [H,blocks,pages] fp32 and, unless mode == -1, the page table.
  * Probe rows: gathered=1 -> q is probes [H,blocks,16,128] addressed
@@ -94,16 +101,15 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
  * ids [H,blocks,count] int32 and mask [H,blocks,pages] uint8 may be NULL; lse
  * [H,blocks,16] fp32 (NULL to skip) receives each probe's log-sum-exp over
  * all reps of the window (natural log), the input ssa_pset needs.
- * rep_values [H,rep_head_pages,4,128] bf16 (NULL to skip) receives, on the
- * side, exactly what ssa_rep_values writes for pages [0,pages) from mean,
- * detail and basis (as in ssa_rep_values), so a call that routes needs no
- * separate rep-value launch; mean, detail, basis and rep_values must then be
- * 16-byte aligned. */
+ * rep_ops [H,rep_tiles,768] bf16 (NULL to skip; 16-byte aligned, rep_tiles >=
+ * ceil(pages/16)) receives, on the side, exactly what ssa_rep_operands
+ * writes from detail [H,head_pages,3,8], so a call that routes needs no
+ * separate operand launch. */
 int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
-              int pages, int head_pages, int count, int mode, int total, const void* mean, const void* detail,
-              const void* basis, void* rep_values, int rep_head_pages, hipStream_t stream);
+              int pages, int head_pages, int count, int mode, int total, const void* detail, void* rep_ops,
+              int rep_tiles, hipStream_t stream);
 
 /* Page selection from given scores (RV/ops.py:113-138 RouteOps.select), one
  * row per (head, block): scores [rows,pages] fp32, own [rows] int32, valid

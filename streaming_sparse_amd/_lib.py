@@ -15,10 +15,10 @@ _lib = None
 
 _vp, _i, _ll, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float
 SIGNATURES = {
-    "ssa_rep_values": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
-    "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp],
+    "ssa_rep_operands": [_vp, _vp, _i, _i, _i, _i, _vp],
+    "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp],
     "ssa_route": [_vp, _ll, _ll, _ll, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
-                  _vp, _vp, _vp, _vp, _i, _vp],
+                  _vp, _vp, _i, _vp],
     "ssa_select": [_vp, _vp, _vp, _i, _i, _f, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     "ssa_encode": [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                    _i, _vp],

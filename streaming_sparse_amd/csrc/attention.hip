@@ -1,5 +1,5 @@
 // Fused exact-page attention + summary compensation + softmax-mass merge for
-// gfx950 (one kernel), plus the per-rep value prep it reads.
+// gfx950 (one kernel), plus the detail-operand prep it reads.
 //
 // The reference computes, per (query block t, head h) (RV/tuned_attention.py:
 // 20-81 and RV/runtime.py:107-133):
@@ -13,8 +13,12 @@
 // mean_p + code_r . basis^T).  This kernel runs that union softmax: it walks
 // "units" of 64 keys -- first the C exact pages (rows of the resident
 // [L,H,D] cache), then the rep tiles of 16 pages x 4 reps whose pages are not
-// all selected -- with one running max/sum per query.  Rep values are
-// pre-projected by rep_values_kernel (bf16 rows, like the V rows of a page).
+// all selected -- with one running max/sum per query.  A rep tile's values
+// are never formed: with w_pr its rep weights, its share of the numerator is
+//   sum_p a_p mean_p + (sum_{p,a} b_pa detail_pa) . basis^T,
+// a_p = sum_r w_pr, b_pa = sum_r HAAR[a,r] w_pr, so the tile costs one
+// 8-page product against the page means and three rank-8 products into a
+// per-query code accumulator, which meets the basis once at the end.
 //
 // Workgroup: 4 waves, 64 queries of one head.  Wave w: pair w/2 takes keys
 // 32*pair..32*pair+31 of every unit, queries 32*(w%2)..+31.  Per unit:
@@ -49,13 +53,15 @@ struct AttnParams {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
-  const uint16_t* rk;   // rep keys   [H, HP, 4, D]
-  const uint16_t* rv;   // rep values [H, HPV, 4, D]
-  const int32_t* ids;   // [H, T, C]
+  const uint16_t* rk;     // rep keys    [H, HP, 4, D]
+  const uint16_t* mean;   // page means  [H, HP, D]
+  const uint16_t* basis;  // [H, D, 8]
+  const uint16_t* rops;   // detail operand tiles [H, RT, kRepOpBytes / 2]
+  const int32_t* ids;     // [H, T, C]
   uint16_t* out;
   long long kv_tok, kv_head;   // element strides of a K/V token row and a head
   long long q_tok, q_head;     // element strides of q / out
-  int H, T, P, HP, HPV, C;
+  int H, T, P, HP, RT, C;
   float scale_log2;            // log2(e) / sqrt(D)
 };
 
@@ -97,10 +103,32 @@ __device__ __forceinline__ UnitOffsets unit_offsets(int wave, int lane, long lon
   return o;
 }
 
-// Where a workgroup's units come from: head h's K, V, rep key and rep value
-// rows as byte pointers, and the byte stride of a page.
+// Per-lane byte offsets of a rep tile's loads: the K rows (instruction-
+// offset form, as unit_offsets) and, for the general call's waves 0 and 2,
+// the mean row of V-slot row rho = lane / 16 of the wave's first 1 KB within
+// the tile's first page pair: pair-local page 2 (lane / 16), its 16-byte
+// chunk lane % 16 swizzled by rho % 4 = lane / 16 (rows rho + 4 and rho + 8
+// repeat it and add one page, 256 bytes).
+struct RepOffsets {
+  uint32_t k[4];
+  uint32_t mean;
+};
+
+__device__ __forceinline__ RepOffsets rep_offsets(int wave, int lane, int nb) {
+  RepOffsets o;
+  const UnitOffsets u = unit_offsets(wave, lane, kHeadDim, 63, nb, true);
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) o.k[jj] = u.k[jj];
+  const int g = lane >> 4;
+  o.mean = (uint32_t)((8 * (wave >> 1) + 2 * g) * 256 + 16 * ((lane & 15) ^ vswz(g)));
+  return o;
+}
+
+// Where a workgroup's units come from: head h's K, V, rep key and page mean
+// rows and detail operand tiles as byte pointers, and the byte stride of a
+// page.
 struct UnitSources {
-  const uint8_t *k, *v, *rk, *rv;
+  const uint8_t *k, *v, *rk, *mean, *rops;
   uint32_t page_bytes;
 };
 
@@ -109,34 +137,72 @@ __device__ __forceinline__ UnitSources unit_sources(const AttnParams& p, int h) 
   u.k = (const uint8_t*)(p.k + (long long)h * p.kv_head);
   u.v = (const uint8_t*)(p.v + (long long)h * p.kv_head);
   u.rk = (const uint8_t*)(p.rk + (long long)h * p.HP * 4 * kHeadDim);
-  u.rv = (const uint8_t*)(p.rv + (long long)h * p.HPV * 4 * kHeadDim);
+  u.mean = (const uint8_t*)(p.mean + (long long)h * p.HP * kHeadDim);
+  u.rops = (const uint8_t*)(p.rops + (long long)h * p.RT * (kRepOpBytes / 2));
   u.page_bytes = (uint32_t)(128 * p.kv_tok);
   return u;
 }
 
+// Byte offset of a rep tile's detail operands in its V slot (rows 16..31,
+// which the mean rows leave free).
+constexpr int kDetailOff = 16 * 256;
+
 // Enqueue the global->LDS loads of the K rows (kv = 0) or V rows (kv = 1)
 // of unit e (a page, or a rep tile) into `buf`: wave w of the 4*NB waves
 // loads rows (16/NB) w .. (16/NB) w + 16/NB - 1.  page_off / rep_off are the
-// instruction-offset forms of unit_offsets.
+// instruction-offset forms of unit_offsets.  The V slot of a rep tile
+// (general call only) holds instead the page means of each key pair twice,
+// row rho (0..15) of the pair's 32-row half = pair-local page 2 (rho % 4) +
+// rho / 8 (waves 0 and 2), and the tile's detail operands at kDetailOff
+// (wave 1).
 template <int NB, int KIND = 2>
 __device__ __forceinline__ void issue_rows(const AttnParams& p, const UnitSources& src, int e, int kv, int wave,
-                                           int lane, const UnitOffsets& page_off, const UnitOffsets& rep_off,
+                                           int lane, const UnitOffsets& page_off, const RepOffsets& rep_off,
                                            lds_u8* buf) {
   constexpr int kLoads = 4 / NB;    // 1 KB loads per wave
   const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)buf + wave * 1024 * kLoads);
   if (KIND == 0 || (KIND == 2 && e >= 0)) {
     dma_rows<kLoads>((kv ? src.v : src.k) + (uint32_t)e * src.page_bytes, kv ? page_off.v : page_off.k, l);
-  } else {
+  } else if (kv == 0) {
     const int rt = rep_tile(e);
-    const uint8_t* base = (kv ? src.rv : src.rk) + (uint32_t)rt * (64 * 256);
+    const uint8_t* base = src.rk + (uint32_t)rt * (64 * 256);
     // rows of pages >= P re-read the last valid rep (masked in compute)
     const int last = p.P * 4 - rt * 64 - 1;
     if (last >= 63) {
-      dma_rows<kLoads>(base, kv ? rep_off.v : rep_off.k, l);
+      dma_rows<kLoads>(base, rep_off.k, l);
     } else {
       const UnitOffsets o = unit_offsets(wave, lane, kHeadDim, last, NB, false);
 #pragma unroll
-      for (int jj = 0; jj < kLoads; ++jj) dma16(base, kv ? o.v[jj] : o.k[jj], l + jj * 1024);
+      for (int jj = 0; jj < kLoads; ++jj) dma16(base, o.k[jj], l + jj * 1024);
+    }
+  } else if constexpr (NB == 1) {
+    const int rt = rep_tile(e);
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+    if (w == 1) {
+      // 96 chunks of 16 bytes: lanes 0..63, then lanes 0..31 for the rest
+      const uint8_t* base = src.rops + (uint32_t)rt * kRepOpBytes;
+      const uint32_t off = 16u * (uint32_t)lane;
+      dma16(base, off, l);
+      if (lane < 32) dma16(base + 1024, off, l + 1024);
+    } else if (w != 3) {
+      // rows rho and rho + 4 hold page pg, rows rho + 8 and rho + 12 page
+      // pg + 1; pages >= P re-read page P - 1 (their weights are zero)
+      const uint8_t* base = src.mean + (uint32_t)rt * 4096u;
+      if (16 * rt + 16 <= p.P) {
+        dma16(base, rep_off.mean, l);
+        dma16(base, rep_off.mean, l + 1024);
+        dma16(base + 256, rep_off.mean, l + 2048);
+        dma16(base + 256, rep_off.mean, l + 3072);
+      } else {
+        const int pg = 16 * rt + 8 * (w >> 1) + 2 * (lane >> 4);
+        const uint32_t cpart = rep_off.mean & 255u;
+        const uint32_t o0 = (uint32_t)(min(pg, p.P - 1) - 16 * rt) * 256u + cpart;
+        const uint32_t o1 = (uint32_t)(min(pg + 1, p.P - 1) - 16 * rt) * 256u + cpart;
+        dma16(base, o0, l);
+        dma16(base, o0, l + 1024);
+        dma16(base, o1, l + 2048);
+        dma16(base, o1, l + 3072);
+      }
     }
   }
 }
@@ -152,6 +218,34 @@ __device__ __forceinline__ u32x4 v_operand(const lds_u8* vbuf, int pair, int ks,
   const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vbuf + v_off(row0 + 8, chunk) + half));
   const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
   return u32x4{ua[0], ua[1], ub[0], ub[1]};
+}
+
+// Lane parts of the K and V operand read addresses within a slot.  K: the
+// chunk 2 x + hh of row 32 pair + lane % 32 sits at k_base ^ (x << 5) (the
+// swizzle XOR touches address bits 4..7 only).  V: the first transpose read
+// of k step ks, dim tile dt sits at 4096 ks + (v_base ^ (dt << 6)), the
+// second 8 rows (2048 bytes) further.  The loop bodies form the addresses
+// from these two values, so that only they stay live across units.
+__device__ __forceinline__ uint32_t k_base(int pair, int lane) {
+  const int row = 32 * pair + (lane & 31);
+  return (uint32_t)(row * 256 + (((lane >> 5) ^ (row & 15)) << 4));
+}
+__device__ __forceinline__ uint32_t v_base(int pair, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int row0 = 32 * pair + 4 * (g >> 1) + (i >> 2);
+  const int c0 = 2 * (g & 1) + ((i & 3) >> 1);
+  return (uint32_t)(row0 * 256 + ((c0 ^ vswz(row0)) << 4) + (i & 1) * 8);
+}
+__device__ __forceinline__ u32x4 k_read(const lds_u8* kb, uint32_t kl, int x) {
+  return *(lds_u32x4*)(kb + (kl ^ (uint32_t)(x << 5)));
+}
+// the V^T operand of v_operand from the address base
+__device__ __forceinline__ u32x4 v_read(const lds_u8* vb, uint32_t vl, int ks, int dt) {
+  const lds_u8* a = vb + 4096 * ks + (vl ^ (uint32_t)(dt << 6));
+  const bf16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a);
+  const bf16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(a + 2048));
+  const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
+  return u32x4{ux[0], ux[1], uy[0], uy[1]};
 }
 
 // S^T = K . Q^T for this pair's 32 keys of the unit in `kbuf`; S[i] is key
@@ -204,9 +298,10 @@ __device__ __forceinline__ float unit_max(f32x16& S, int e, int pair, int lane, 
 // (log2 units), so probabilities stay below 2^kSlack and the rescale is rare.
 constexpr float kSlack = 8.0f;
 
-// `ls` is the two-term path's denominator (a lane's fp32 partial sum), L the
-// single-term path's (matrix-pipe row sums); each path leaves the other zero.
-__device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, float& ls, f32x16 (&O)[4]) {
+// `ls` is a lane's fp32 partial denominator (the two-term path's exact
+// pages and every rep tile), L the single-term path's exact pages (matrix-pipe
+// row sums).  C holds the code accumulator in items 0..3 (ranks 4 hh + i).
+__device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, float& ls, f32x16 (&O)[4], f32x16& C) {
   if (__any(mloc > m + kSlack)) {
     const float mnew = fmaxf(m, mloc);
     const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
@@ -214,6 +309,8 @@ __device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, floa
     ls *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) O[dt] *= alpha;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) C[i] *= alpha;
     m = mnew;
   }
 }
@@ -259,6 +356,27 @@ __device__ __forceinline__ void probabilities(const f32x16& S, float nb, float s
     for (int i = 0; i < 16; ++i) s += P[i];
     ls += s;
   }
+}
+
+// Haar view of one page's 4 rep probabilities w: hw = {a, b0, b1, b2}, the
+// mean weight a = sum_r w_r and the contrast weights b_a = sum_r HAAR[a,r] w_r
+// (HAAR rows (1,1,-1,-1), (1,-1,1,-1), (1,-1,-1,1); RV/ops.py:10).
+__device__ __forceinline__ void haar4(const float* w, float* hw) {
+  const float s01 = w[0] + w[1], s23 = w[2] + w[3], d01 = w[0] - w[1], d23 = w[2] - w[3];
+  hw[0] = s01 + s23;
+  hw[1] = s01 - s23;
+  hw[2] = d01 + d23;
+  hw[3] = d01 - d23;
+}
+
+// Exchange of lane halves (v_permlane32_swap): lanes l < 32 get {lo of lane
+// l, lo of lane l + 32}, lanes l >= 32 get {hi of lane l - 32, hi of lane l}.
+// A word of hi parts and one of lo parts, spread over the two halves of a
+// query's lanes, so become the k = 8 hh .. 8 hh + 7 operand items of the
+// half that holds that part for all of them.
+__device__ __forceinline__ u32x2 halves(uint32_t lo, uint32_t hi) {
+  const auto s = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+  return u32x2{s[0], s[1]};
 }
 
 // bf16 1.0 in both halves: the A operand whose product with P^T puts the
@@ -376,13 +494,17 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   auto vslot = [&](int slot) { return vbase + slot * kBuf; };
 
   float m = -INFINITY;
-  f32x16 L = {}, O[4];
+  f32x16 L = {}, O[4], C = {};
   float ls = 0.f;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
   const UnitOffsets page_off = unit_offsets(wave, lane, p.kv_tok, 63, NB, true);
-  const UnitOffsets rep_off = unit_offsets(wave, lane, kHeadDim, 63, NB, true);
+  const RepOffsets rep_off = rep_offsets(wave, lane, NB);
   const UnitSources src = unit_sources(p, h);
+  // this lane's detail operand rows (rank r % 8 of its half's 12 pairs) in a
+  // rep tile's V slot
+  const uint32_t det_off = kDetailOff + ((pair * 2 + hh) * 8 + (r & 7)) * 48;
+  const uint32_t klane = k_base(pair, lane), vlane = v_base(pair, lane);
   auto unit = [&](int i) { return __builtin_amdgcn_readfirstlane(units[i]); };
   // prologue: K0, V0, K1 in flight; S of unit 0 and its max
   issue_rows<NB>(p, src, unit(0), 0, wave, lane, page_off, rep_off, kslot(0));
@@ -393,41 +515,33 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   f32x16 S0 = s_tile(kslot(0), pair, lane, qop), S1;
   float mloc;
   float bias = unit_max(S0, unit(0), pair, lane, p.scale_log2, mloc);
-  update_max(mloc, m, L, ls, O);
+  update_max(mloc, m, L, ls, O, C);
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
-  // One unit with a successor: loads of K unit i+2 (clamped to the last
-  // unit; a surplus load lands in a slot nobody reads again) and V unit i+1,
-  // S of unit i+1, the probabilities of unit i, the max of unit i+1 (before
-  // the P.V products, so it does not wait behind them in the matrix pipe),
-  // then P.V of unit i.  Unit ids run ahead in registers; the id of unit
-  // i+3 is read from LDS in step i-1, so the read completes at its barrier.
-  int u1 = unit(min(1, nunits - 1)), u2 = unit(min(2, nunits - 1));
+  // Unit ids run ahead in registers (u0 = unit i); the id of unit i+3 is
+  // read from LDS in step i-1, so the read completes at its barrier.
+  int u0 = unit(0), u1 = unit(min(1, nunits - 1)), u2 = unit(min(2, nunits - 1));
   int u3raw = units[min(3, nunits - 1)];
-  auto step = [&](auto kind, int i, f32x16& Sc, f32x16& Sn) {
+
+  // P.V of exact page i (probabilities of Sc, V slot cur), with S(i+1) from
+  // the other K slot and its max.  K: the kind of units i+1 and i+2.
+  auto page_body = [&](auto kind, int cur, const f32x16& Sc, f32x16& Sn, float nb) {
     constexpr int K = decltype(kind)::value;
-    const int cur = i & 1, nxt = cur ^ 1;
-    const int u3 = __builtin_amdgcn_readfirstlane(u3raw);
-    // the general call issues its loads first; the two-block call (8 waves,
-    // half the loads each) spreads them over the first products
-    if (NB == 1) {
-      issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
-      issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
-    }
-    const float nb = bias - (m == -INFINITY ? 0.0f : m);
+    const lds_u8* kb = kslot(cur ^ 1);
+    const lds_u8* vb = vslot(cur);
+    uint32_t kl = klane, vl = vlane;
+    asm volatile("" : "+v"(kl), "+v"(vl));
     if (PRECISE) {
       // Two-term P.V in three stages of 8 matrix products, each carrying a
       // similar share of the vector work, so that the matrix and vector
       // work of this wave overlap throughout the step: S(i+1) with k step 0
       // of unit i's exponentials and splits, the hi/lo products of k step 0
       // with those of k step 1, the products of k step 1 with the max of
-      // unit i+1 and the denominator (the lane's fp32 sum of P).
-      const lds_u8* kb = kslot(nxt);
-      const lds_u8* vb = vslot(cur);
-      const int r = lane & 31, hh = lane >> 5;
+      // unit i+1 and the denominator (the lane's fp32 sum of P, gathered in
+      // index order as the exponentials form).
       u32x4 ka[8], va[2][4], pb[2], pl[2];
-      float P[16];
+      float P[16], ps = 0.f;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) ka[st] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + hh));
+      for (int st = 0; st < 4; ++st) ka[st] = k_read(kb, kl, st);
       __builtin_amdgcn_sched_barrier(0);
       Sn = f32x16{};
       // stage A: the 8 products of S(i+1), each with one exponential of
@@ -436,12 +550,13 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       for (int st = 0; st < 8; ++st) {
         Sn = mfma32(ka[st], qop[st], Sn);
         if (NB == 2 && st == 0) issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
-        if (NB == 2 && st == 3) issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
+        if (NB == 2 && st == 3) issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(cur ^ 1));
         if (st < 4)
-          ka[st + 4] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + 8 + hh));
+          ka[st + 4] = k_read(kb, kl, st + 4);
         else
-          va[0][st - 4] = v_operand(vb, pair, 0, st - 4, lane);
+          va[0][st - 4] = v_read(vb, vl, 0, st - 4);
         P[st] = __builtin_amdgcn_exp2f(fmaf(Sc[st], p.scale_log2, nb));
+        ps += P[st];
         if (st & 1) {
           const u32x2 hl = split_pair(P[st - 1], P[st]);
           pb[0][st >> 1] = hl[0];
@@ -454,9 +569,11 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         O[dt] = mfma32(va[0][dt], pb[0], O[dt]);
-        va[1][dt] = v_operand(vb, pair, 1, dt, lane);
+        va[1][dt] = v_read(vb, vl, 1, dt);
         P[8 + 2 * dt] = __builtin_amdgcn_exp2f(fmaf(Sc[8 + 2 * dt], p.scale_log2, nb));
         P[9 + 2 * dt] = __builtin_amdgcn_exp2f(fmaf(Sc[9 + 2 * dt], p.scale_log2, nb));
+        ps += P[8 + 2 * dt];
+        ps += P[9 + 2 * dt];
         O[dt] = mfma32(va[0][dt], pl[0], O[dt]);
         const u32x2 hl = split_pair(P[8 + 2 * dt], P[9 + 2 * dt]);
         pb[1][dt] = hl[0];
@@ -464,19 +581,14 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
         __builtin_amdgcn_sched_barrier(0);
       }
       // stage C: the 8 P.V products of k step 1 with the max of unit i+1
-      // and the lane's fp32 sum of P (the denominator)
+      // and the denominator update
       if (NB == 1) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
         if (dt == 0) bias = unit_max<K>(Sn, u1, pair, lane, p.scale_log2, mloc);
         O[dt] = mfma32(va[1][dt], pl[1], O[dt]);
-        if (dt == 1) {
-          float s = 0.f;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) s += P[k];
-          ls += s;
-        }
+        if (dt == 1) ls += ps;
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -484,24 +596,21 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       // products of S(i+1) each carry two exponentials of unit i and one
       // operand read 4 products ahead; the P.V products of unit i then
       // carry the max of unit i+1.  Scheduling barriers hold the order.
-      const lds_u8* kb = kslot(nxt);
-      const lds_u8* vb = vslot(cur);
-      const int r = lane & 31, hh = lane >> 5;
       u32x4 ka[8], va[2][4], pb[2];
       float P[16];
 #pragma unroll
-      for (int st = 0; st < 4; ++st) ka[st] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + hh));
+      for (int st = 0; st < 4; ++st) ka[st] = k_read(kb, kl, st);
       __builtin_amdgcn_sched_barrier(0);
       Sn = f32x16{};
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
         Sn = mfma32(ka[st], qop[st], Sn);
         if (NB == 2 && st == 0) issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
-        if (NB == 2 && st == 3) issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(nxt));
+        if (NB == 2 && st == 3) issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(cur ^ 1));
         if (st < 4)
-          ka[st + 4] = *(lds_u32x4*)(kb + k_off(32 * pair + r, 2 * st + 8 + hh));
+          ka[st + 4] = k_read(kb, kl, st + 4);
         else
-          va[0][st - 4] = v_operand(vb, pair, 0, st - 4, lane);
+          va[0][st - 4] = v_read(vb, vl, 0, st - 4);
         P[2 * st] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st], p.scale_log2, nb));
         P[2 * st + 1] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st + 1], p.scale_log2, nb));
         __builtin_amdgcn_sched_barrier(0);
@@ -523,7 +632,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         O[dt] = mfma32(va[0][dt], pb[0], O[dt]);
-        va[1][dt] = v_operand(vb, pair, 1, dt, lane);
+        va[1][dt] = v_read(vb, vl, 1, dt);
         __builtin_amdgcn_sched_barrier(0);
       }
       L = mfma32(ones, pb[1], L);
@@ -531,53 +640,190 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
     }
-    update_max(mloc, m, L, ls, O);
+  };
+
+  // The compensation of rep tile i (probabilities of Sc), with two-term
+  // (hi, lo) weights in the two-term path and one bf16 term (lo = 0) in the
+  // single-term path; with NEXT also S(i+1) from K slot kb and its max.  Lane (query r, half hh) holds the 4 reps of
+  // pair-local page 2 jp + hh in Sc[4 jp .. 4 jp + 3] (jp = 0..3).
+  //  * contrasts: C += D^T B^T in 3 products; product mm takes, in k =
+  //    8 hh + j, the weights v = 4 mm + (j & 3) of lane half hh's 12
+  //    (page, contrast) pairs v = 3 jp + a as hi parts (j < 4) and lo parts
+  //    (j >= 4), against A rows = detail[page][a][rank] (the operand tile);
+  //  * means: O^T += M^T A^T, one product per dim tile over the pair's 8
+  //    pages, k = 8 hh + e holding page e < 4 ? 2 e : 2 e - 7, the lo parts
+  //    of its mean weight in half 0 and the hi parts in half 1; M^T is read
+  //    as the V operand of k step 0 from the mean rows the loads placed.
+  auto rep_body = [&](auto next_c, auto kind, int cur, const f32x16& Sc, f32x16& Sn, float nb) {
+    constexpr bool NEXT = decltype(next_c)::value;
+    constexpr int K = decltype(kind)::value;
+    const lds_u8* kb = kslot(cur ^ 1);
+    const lds_u8* vb = vslot(cur);
+    uint32_t kl = klane, vl = vlane, dl = det_off;
+    asm volatile("" : "+v"(kl), "+v"(vl), "+v"(dl));
+    u32x4 ka[8], va[4], dop[3];
+    float hw[16];   // probabilities, then at 4 jp the Haar view of page jp
+    if constexpr (NEXT) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) ka[st] = k_read(kb, kl, st);
+      __builtin_amdgcn_sched_barrier(0);
+      Sn = f32x16{};
+    }
+    // the products of S(i+1), each with two exponentials; every second one
+    // completes a page and its Haar view
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      if constexpr (NEXT) {
+        Sn = mfma32(ka[st], qop[st], Sn);
+        if (st < 4) ka[st + 4] = k_read(kb, kl, st + 4);
+      }
+      if (st >= 4 && st < 7) dop[st - 4] = *(lds_u32x4*)(vb + dl + 16 * (st - 4));
+      hw[2 * st] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st], p.scale_log2, nb));
+      hw[2 * st + 1] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st + 1], p.scale_log2, nb));
+      if (st & 1) haar4(hw + 4 * (st >> 1), hw + 4 * (st >> 1));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the contrast products, each with the splits of its 4 weights and the
+    // read of one mean operand
+    auto bw = [&](int v) { return hw[4 * (v / 3) + 1 + v % 3]; };
+    auto wsplit = [&](float a, float b) { return PRECISE ? split_pair(a, b) : u32x2{pack_bf16(a, b), 0u}; };
+#pragma unroll
+    for (int mm = 0; mm < 3; ++mm) {
+      const u32x2 s0 = wsplit(bw(4 * mm), bw(4 * mm + 1)), s1 = wsplit(bw(4 * mm + 2), bw(4 * mm + 3));
+      C = mfma32(dop[mm], u32x4{s0[0], s1[0], s0[1], s1[1]}, C);
+      va[mm] = v_read(vb, vl, 0, mm);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    va[3] = v_read(vb, vl, 0, 3);
+    const u32x2 a01 = wsplit(hw[0], hw[4]), a23 = wsplit(hw[8], hw[12]);
+    const u32x2 x0 = halves(a01[1], a01[0]), x1 = halves(a23[1], a23[0]);
+    const u32x4 am = {x0[0], x1[0], x0[1], x1[1]};
+    if (NEXT && NB == 1) __builtin_amdgcn_s_setprio(1);
+    // the mean products with the max of unit i+1 and the denominator
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      O[dt] = mfma32(va[dt], am, O[dt]);
+      if constexpr (NEXT) {
+        if (dt == 0) bias = unit_max<K>(Sn, u1, pair, lane, p.scale_log2, mloc);
+      }
+      if (dt == 1) ls += (hw[0] + hw[4]) + (hw[8] + hw[12]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // One unit with a successor: loads of K unit i+2 (clamped to the last
+  // unit; a surplus load lands in a slot nobody reads again) and V unit i+1,
+  // S of unit i+1, the P.V (or compensation) of unit i, the max of unit i+1
+  // (before the last products, so it does not wait behind them in the matrix
+  // pipe).  KP: the kind of unit i (page or rep tile); K: that of units
+  // i+1 and i+2.
+  auto step = [&](auto pvkind, auto kind, int i, f32x16& Sc, f32x16& Sn) {
+    constexpr int KP = decltype(pvkind)::value;
+    constexpr int K = decltype(kind)::value;
+    const int cur = i & 1;
+    const int u3 = __builtin_amdgcn_readfirstlane(u3raw);
+    // the general call issues its loads first; the two-block call (8 waves,
+    // half the loads each) spreads them over the first products
+    if (NB == 1) {
+      issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
+      issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(cur ^ 1));
+    }
+    const float nb = bias - (m == -INFINITY ? 0.0f : m);
+    if constexpr (NB == 1 && KP == 1)
+      rep_body(std::true_type{}, kind, cur, Sc, Sn, nb);
+    else
+      page_body(kind, cur, Sc, Sn, nb);
+    update_max(mloc, m, L, ls, O, C);
     if (NB == 1) __builtin_amdgcn_s_setprio(0);
+    u0 = u1;
     u1 = u2;
     u2 = u3;
     u3raw = units[min(i + 4, nunits - 1)];
     wait_loads();
     __syncthreads();
   };
-  // Units are the exact pages, then the rep tiles: steps whose two units in
-  // flight are both pages or both rep tiles take their loads and maxima
-  // without testing the kind of unit
+  // Units are the exact pages, then the rep tiles; every step knows the kind
+  // of its units at compile time (i is even in the paired loops, so the
+  // parity of npages fixes where the kinds change)
   using PageUnits = std::integral_constant<int, 0>;
   using RepUnits = std::integral_constant<int, 1>;
   using AnyUnits = std::integral_constant<int, 2>;
   const int npages = nexact_s;
   int i = 0;
   for (; i + 2 < nunits && i + 3 < npages; i += 2) {
-    step(PageUnits{}, i, S0, S1);
-    step(PageUnits{}, i + 1, S1, S0);
+    step(PageUnits{}, PageUnits{}, i, S0, S1);
+    step(PageUnits{}, PageUnits{}, i + 1, S1, S0);
   }
   for (; i + 2 < nunits && i + 1 < npages; i += 2) {
-    step(AnyUnits{}, i, S0, S1);
-    step(AnyUnits{}, i + 1, S1, S0);
+    step(PageUnits{}, AnyUnits{}, i, S0, S1);
+    step(PageUnits{}, AnyUnits{}, i + 1, S1, S0);
   }
-  for (; i + 2 < nunits; i += 2) {
-    step(RepUnits{}, i, S0, S1);
-    step(RepUnits{}, i + 1, S1, S0);
+  if constexpr (NB == 1) {
+    // here unit i+1 is a rep tile; unit i is the last page when npages is odd
+    if (i + 2 < nunits && i < npages) {
+      step(PageUnits{}, RepUnits{}, i, S0, S1);
+      step(RepUnits{}, RepUnits{}, i + 1, S1, S0);
+      i += 2;
+    }
+    for (; i + 2 < nunits; i += 2) {
+      step(RepUnits{}, RepUnits{}, i, S0, S1);
+      step(RepUnits{}, RepUnits{}, i + 1, S1, S0);
+    }
   }
+  // one unit with a successor left (units i and i+1 = nunits - 1): the same
+  // work without the interleaving, each kind chosen at run time
+  auto unit_pv = [&](int cur, const f32x16& Sc, float nb) {
+    bool rep = false;
+    if constexpr (NB == 1) rep = u0 < 0;
+    if (rep) {
+      f32x16 unused;
+      if constexpr (NB == 1) rep_body(std::false_type{}, AnyUnits{}, cur, Sc, unused, nb);
+    } else {
+      u32x4 pb[2], pl[2];
+      probabilities<PRECISE>(Sc, nb, p.scale_log2, pb, pl, ls);
+      pv<PRECISE>(pb, pl, vslot(cur), pair, lane, L, O);
+    }
+  };
   if (i + 1 < nunits) {
-    step(AnyUnits{}, i, S0, S1);
+    issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot((i + 1) & 1));
+    S1 = s_tile(kslot((i + 1) & 1), pair, lane, qop);
+    unit_pv(i & 1, S0, bias - (m == -INFINITY ? 0.0f : m));
+    bias = unit_max(S1, u1, pair, lane, p.scale_log2, mloc);
+    update_max(mloc, m, L, ls, O, C);
+    u0 = u1;
+    wait_loads();
+    __syncthreads();
     ++i;
     S0 = S1;
   }
   // last unit
   {
-    u32x4 pb[2], pl[2];
-    probabilities<PRECISE>(S0, bias - (m == -INFINITY ? 0.0f : m), p.scale_log2, pb, pl, ls);
-    pv<PRECISE>(pb, pl, vslot(i & 1), pair, lane, L, O);
+    u32x4 bop[4];
+    if constexpr (NB == 1) {
+      // basis rows of dims 32 dt + r (ranks 0..7), for the code accumulator
+      const uint16_t* bp = p.basis + ((long long)h * kHeadDim + r) * 8;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) bop[dt] = ldg16(bp + 256 * dt);
+    }
+    unit_pv(i & 1, S0, bias - (m == -INFINITY ? 0.0f : m));
+    if constexpr (NB == 1) {
+      // O^T += basis . C^T: the two-term operand of C holds the lo parts of
+      // ranks 0..7 in k 0..7 and the hi parts in k 8..15
+      const u32x2 c01 = split_pair(C[0], C[1]), c23 = split_pair(C[2], C[3]);
+      const u32x2 y0 = halves(c01[1], c01[0]), y1 = halves(c23[1], c23[0]);
+      const u32x4 cb = {y0[0], y1[0], y0[1], y1[1]};
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) O[dt] = mfma32(bop[dt], cb, O[dt]);
+    }
   }
   __syncthreads();
   // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS.
-  // Two-term path: lanes l and l ^ 32 hold the partial sums of one query's
-  // two 16-key halves.
-  float l = L[0];
-  if (PRECISE) {
+  // Lanes l and l ^ 32 hold the fp32 partial sums of one query's two 16-key
+  // halves (ls); the single-term path adds its matrix-pipe sums L.
+  float l = PRECISE ? 0.0f : L[0];
+  {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls), false, false);
-    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    l += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
   // [group][qw][64 items][64 lanes] fp32 = 32 KB per group
   float* xo = reinterpret_cast<float*>(ring) + grp * 8192;
@@ -612,43 +858,41 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   }
 }
 
-// vrep[h,p,r,:] = bf16(mean[h,p,:] + sum_k (sum_a HAAR[a,r] detail[h,p,a,k]) basis[h,:,k])
-__global__ __launch_bounds__(128) void rep_values_kernel(const uint16_t* mean, const uint16_t* detail,
-                                                         const uint16_t* basis, uint16_t* vrep, int HP, int HPV) {
-  const int pg = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-  __shared__ float det[24];
-  if (d < 24) det[d] = bf16_to_f32(detail[((long long)h * HP + pg) * 24 + d]);
-  __syncthreads();
-  const float mu = bf16_to_f32(mean[((long long)h * HP + pg) * kHeadDim + d]);
-  float b[8], dv[24], o[4];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) b[k] = bf16_to_f32(basis[((long long)h * kHeadDim + d) * 8 + k]);
-#pragma unroll
-  for (int k = 0; k < 24; ++k) dv[k] = det[k];
-  rep_value_rows(mu, dv, b, o);
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) vrep[(((long long)h * HPV + pg) * 4 + rr) * kHeadDim + d] = to_bf16(o[rr]);
+// Detail operand tiles of one head per block row: rops[h, rt] for the
+// ceil(P/16) tiles of the window (96 chunks of 16 bytes each).
+__global__ __launch_bounds__(kRepOpChunks) void rep_operands_kernel(const uint16_t* detail, uint16_t* rops, int P,
+                                                                   int HP, int RT) {
+  const int rt = blockIdx.x, h = blockIdx.y, c = threadIdx.x;
+  const u32x4 w = rep_operand_chunk(detail + (long long)h * HP * 24, P, rt, c);
+  *reinterpret_cast<u32x4*>(rops + ((long long)h * RT + rt) * (kRepOpBytes / 2) + 8 * c) = w;
 }
 
 }  // namespace
 
 extern "C" {
 
-int ssa_rep_values(const void* mean, const void* detail, const void* basis, void* rep_values, int heads, int pages,
-                   int head_pages, int rep_head_pages, hipStream_t stream) {
-  if (heads <= 0 || pages <= 0 || head_pages < pages || rep_head_pages < pages) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(rep_values_kernel, dim3(pages, heads), dim3(128), 0, stream, (const uint16_t*)mean,
-                     (const uint16_t*)detail, (const uint16_t*)basis, (uint16_t*)rep_values, head_pages,
-                     rep_head_pages);
+int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, int head_pages, int rep_tiles,
+                     hipStream_t stream) {
+  if (heads <= 0 || pages <= 0 || pages > 512 || head_pages < pages || rep_tiles < (pages + 15) / 16 || !detail ||
+      !rep_ops || ((uintptr_t)rep_ops & 15))
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(rep_operands_kernel, dim3((pages + 15) / 16, heads), dim3(kRepOpChunks), 0, stream,
+                     (const uint16_t*)detail, (uint16_t*)rep_ops, pages, head_pages, rep_tiles);
   return (int)hipGetLastError();
 }
 
-int ssa_attention(const void* q, const void* k, const void* v, const void* keys, const void* rep_values,
-                  const int32_t* ids, void* out, int n_tokens, int heads, int pages, int head_pages,
-                  int rep_head_pages, int count, long long kv_token_stride, long long kv_head_stride, int flags,
-                  hipStream_t stream) {
+int ssa_attention(const void* q, const void* k, const void* v, const void* keys, const void* mean, const void* basis,
+                  const void* rep_ops, const int32_t* ids, void* out, int n_tokens, int heads, int pages,
+                  int head_pages, int rep_tiles, int count, long long kv_token_stride, long long kv_head_stride,
+                  int flags, hipStream_t stream) {
   if (n_tokens <= 0 || n_tokens % 64 || heads <= 0 || pages <= 0 || pages > 512 || count <= 0 ||
-      count > kMaxCount || count > pages || head_pages < pages || rep_head_pages < pages)
+      count > kMaxCount || count > pages || head_pages < pages)
+    return (int)hipErrorInvalidValue;
+  const bool dense = (flags & 2) && count == pages && (n_tokens / 64) % 2 == 0;
+  // the general call reads page means, the basis and the operand tiles (in
+  // 16-byte rows)
+  if (!dense && (rep_tiles < (pages + 15) / 16 || !mean || !basis || !rep_ops ||
+                 (((uintptr_t)mean | (uintptr_t)basis | (uintptr_t)rep_ops) & 15)))
     return (int)hipErrorInvalidValue;
   // a K/V row is 128 elements; page byte offsets of the window fit 32 bits
   if (kv_token_stride < kHeadDim || kv_head_stride < 0 || 128.0 * (double)kv_token_stride * pages >= 4294967296.0)
@@ -658,7 +902,9 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   p.k = (const uint16_t*)k;
   p.v = (const uint16_t*)v;
   p.rk = (const uint16_t*)keys;
-  p.rv = (const uint16_t*)rep_values;
+  p.mean = (const uint16_t*)mean;
+  p.basis = (const uint16_t*)basis;
+  p.rops = (const uint16_t*)rep_ops;
   p.ids = ids;
   p.out = (uint16_t*)out;
   p.kv_tok = kv_token_stride;
@@ -669,14 +915,15 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   p.T = n_tokens / 64;
   p.P = pages;
   p.HP = head_pages;
-  p.HPV = rep_head_pages;
+  p.RT = rep_tiles;
   p.C = count;
   p.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
   // a call whose caller states that every LUT row lists each page once
   // (flags bit 1: a dense call) runs, with an even number of blocks, two
-  // blocks per workgroup on one shared K/V stream of pages 0..P-1; ids are
-  // then not read.  Without the flag the LUT is walked as given.
-  if ((flags & 2) && count == pages && p.T % 2 == 0) {
+  // blocks per workgroup on one shared K/V stream of pages 0..P-1; ids,
+  // page means, basis and operand tiles are then not read.  Without the
+  // flag the LUT is walked as given.
+  if (dense) {
     const dim3 grid(heads * p.T / 2);
     if (flags & 1)
       hipLaunchKernelGGL((attn_kernel<true, 2>), grid, dim3(2 * kThreads), 0, stream, p);

@@ -100,22 +100,35 @@ __device__ __forceinline__ void dma_rows(const void* base, const uint32_t (&off)
   }
 }
 
-// The 4 rep value rows of one page at dimension d: row r = mean[d] +
-// sum_k (sum_a HAAR[a,r] detail[a,k]) basis[d,k] in fp32 (rounded to bf16 by
-// the caller); the compensation's value rows.  Shared by every kernel that
-// writes them, so they agree bit for bit.
-__device__ __forceinline__ void rep_value_rows(float mu, const float (&det)[24], const float (&b)[8], float (&out)[4]) {
-  const float haar[3][4] = {{1, 1, -1, -1}, {1, -1, 1, -1}, {1, -1, -1, 1}};
+// Detail operand tiles of the compensation.  A rep tile covers pages
+// 16 rt .. 16 rt + 15 of the window; its operand tile (kRepOpBytes) holds, for
+// each (pair, hh, rank) = the matrix-pipe A rows of one lane, the rank-`rank`
+// element of detail[page][a] for the 12 (page, contrast) pairs that lane half
+// hh of key pair `pair` weighs: v = 3 jp + a, page 16 rt + 8 pair + 2 jp + hh
+// (jp = 0..3, a = 0..2).  16-byte chunk c = ((pair * 2 + hh) * 8 + rank) * 3
+// + m is the A operand of contrast product m: elements j -> v = 4 m + (j & 3)
+// (the hi and lo halves of k share a detail value).  Pages >= P read zero.
+constexpr int kRepOpBytes = 1536;
+constexpr int kRepOpChunks = kRepOpBytes / 16;
+
+// Chunk c of operand tile rt from one head's detail rows [HP, 3, 8] bf16.
+// Shared by every kernel that writes the tiles, so they agree bit for bit.
+__device__ __forceinline__ u32x4 rep_operand_chunk(const uint16_t* det, int P, int rt, int c) {
+  const int m = c % 3, rank = (c / 3) & 7, hh = (c / 24) & 1, pair = c / 48;
+  uint32_t w[2];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    float acc = mu;
+  for (int x = 0; x < 2; ++x) {
+    uint32_t packed = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float code = haar[0][rr] * det[k] + haar[1][rr] * det[8 + k] + haar[2][rr] * det[16 + k];
-      acc += code * b[k];
+    for (int y = 0; y < 2; ++y) {
+      const int v = 4 * m + 2 * x + y, jp = v / 3, a = v % 3;
+      const int pg = 16 * rt + 8 * pair + 2 * jp + hh;
+      const uint32_t val = pg < P ? (uint32_t)det[pg * 24 + a * 8 + rank] : 0u;
+      packed |= val << (16 * y);
     }
-    out[rr] = acc;
+    w[x] = packed;
   }
+  return u32x4{w[0], w[1], w[0], w[1]};
 }
 
 }  // namespace ssa

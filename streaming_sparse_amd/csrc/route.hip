@@ -53,12 +53,11 @@ struct RouteParams {
   uint8_t* mask;               // [H, T, P] or null
   float* lse;                  // [H, T, 16] LSE of each probe over all reps (natural log), or null
   int H, T, P, HP, C, mode, total;
-  // rep value rows of the window's pages, written on the side (rvals null:
-  // not asked for): mean [H,HP,128], detail [H,HP,3,8], basis [H,128,8] bf16
-  // -> rvals [H,HPV,4,128] bf16
-  const uint16_t *rmean, *rdetail, *rbasis;
-  uint16_t* rvals;
-  int HPV;
+  // detail operand tiles of the window, written on the side (rops null: not
+  // asked for): detail [H,HP,3,8] bf16 -> rops [H,RT,kRepOpBytes/2] bf16
+  const uint16_t* rdetail;
+  uint16_t* rops;
+  int RT;
 };
 
 constexpr int kSlotBytes = 9 * 1024;   // a rep tile: 32 rows x 256 B (swizzled) + its pages' stats (768 B)
@@ -191,69 +190,17 @@ __device__ __forceinline__ void sort512_desc(unsigned long long (&key)[4], int b
   }
 }
 
-// Rep value rows written on the side by workgroups of their own, appended
-// to the router's grid: they take the slots of the CUs that hold one router
-// workgroup.  Block r writes pages [r*kRvPages, (r+1)*kRvPages) of the flat
-// (head, page) range; item = (page, 8 dims), two per thread at a time.
-constexpr int kRvPages = 64;
-
-struct RvIn {
-  u32x4 mean, det[3], basis[8];
-};
-
-__device__ __forceinline__ void rv_load(const RouteParams& p, int h, int pg, int c, RvIn& in) {
-  const long long row = (long long)h * p.HP + pg;
-  in.mean = ldg16(p.rmean + row * kHeadDim + 8 * c);
-#pragma unroll
-  for (int a = 0; a < 3; ++a) in.det[a] = ldg16(p.rdetail + row * 24 + 8 * a);
-#pragma unroll
-  for (int dd = 0; dd < 8; ++dd) in.basis[dd] = ldg16(p.rbasis + ((long long)h * kHeadDim + 8 * c + dd) * 8);
-}
-
-__device__ __forceinline__ void rv_store(const RouteParams& p, int h, int pg, int c, const RvIn& in) {
-  float dv[24];
-#pragma unroll
-  for (int a = 0; a < 3; ++a)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      dv[8 * a + 2 * w] = bf16_lo(in.det[a][w]);
-      dv[8 * a + 2 * w + 1] = bf16_hi(in.det[a][w]);
-    }
-  u32x4 outw[4];
-#pragma unroll
-  for (int dd = 0; dd < 8; ++dd) {
-    float b[8], o[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      b[2 * w] = bf16_lo(in.basis[dd][w]);
-      b[2 * w + 1] = bf16_hi(in.basis[dd][w]);
-    }
-    const float mu = (dd & 1) ? bf16_hi(in.mean[dd >> 1]) : bf16_lo(in.mean[dd >> 1]);
-    rep_value_rows(mu, dv, b, o);
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const uint32_t v = to_bf16(o[rr]);
-      if (dd & 1) outw[rr][dd >> 1] |= v << 16;
-      else outw[rr][dd >> 1] = v;
-    }
-  }
-  uint16_t* dst = p.rvals + ((long long)h * p.HPV + pg) * 4 * kHeadDim + 8 * c;
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) *reinterpret_cast<u32x4*>(dst + rr * kHeadDim) = outw[rr];
-}
-
-__device__ void rep_value_block(const RouteParams& p, int r) {
-  const int beg = r * kRvPages, n = min(p.H * p.P - beg, kRvPages) * 16;
-  for (int it = threadIdx.x; it < n; it += 2 * kThreads) {
-    const int it2 = it + kThreads;
-    const int f0 = beg + (it >> 4), f1 = beg + (it2 >> 4);
-    const int h0 = f0 / p.P, h1 = f1 / p.P;
-    RvIn a, b;
-    rv_load(p, h0, f0 - h0 * p.P, it & 15, a);
-    if (it2 < n) rv_load(p, h1, f1 - h1 * p.P, it2 & 15, b);
-    rv_store(p, h0, f0 - h0 * p.P, it & 15, a);
-    if (it2 < n) rv_store(p, h1, f1 - h1 * p.P, it2 & 15, b);
-  }
+// Detail operand tiles written on the side by workgroups of their own,
+// appended to the router's grid: they take the slots of the CUs that hold
+// one router workgroup.  Thread c of block r writes chunk r * kThreads + c
+// of the flat (head, tile, chunk) range.
+__device__ void rep_operand_block(const RouteParams& p, int r) {
+  const int tiles = (p.P + 15) >> 4;
+  const int f = r * kThreads + threadIdx.x;
+  if (f >= p.H * tiles * kRepOpChunks) return;
+  const int c = f % kRepOpChunks, ht = f / kRepOpChunks, h = ht / tiles, rt = ht % tiles;
+  const u32x4 w = rep_operand_chunk(p.rdetail + (long long)h * p.HP * 24, p.P, rt, c);
+  *reinterpret_cast<u32x4*>(p.rops + ((long long)h * p.RT + rt) * (kRepOpBytes / 2) + 8 * c) = w;
 }
 
 __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
@@ -261,7 +208,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int NP = (p.T + 1) >> 1;
   if ((int)blockIdx.x >= p.H * NP) {
-    rep_value_block(p, blockIdx.x - p.H * NP);
+    rep_operand_block(p, blockIdx.x - p.H * NP);
     return;
   }
   const int work = xcd_remap(blockIdx.x, p.H * NP);
@@ -751,14 +698,13 @@ extern "C" {
 int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
-              int pages, int head_pages, int count, int mode, int total, const void* mean, const void* detail,
-              const void* basis, void* rep_values, int rep_head_pages, hipStream_t stream) {
+              int pages, int head_pages, int count, int mode, int total, const void* detail, void* rep_ops,
+              int rep_tiles, hipStream_t stream) {
   if (heads <= 0 || blocks <= 0 || pages <= 0 || pages > kMaxPages || head_pages < pages || mode < -1 ||
       mode > 2)
     return (int)hipErrorInvalidValue;
-  if (rep_values && (!mean || !detail || !basis || rep_head_pages < pages)) return (int)hipErrorInvalidValue;
-  // the rep value rows move in 16-byte loads and stores
-  if (rep_values && (((uintptr_t)mean | (uintptr_t)detail | (uintptr_t)basis | (uintptr_t)rep_values) & 15))
+  // the operand tiles move in 16-byte stores
+  if (rep_ops && (!detail || rep_tiles < (pages + 15) / 16 || ((uintptr_t)rep_ops & 15)))
     return (int)hipErrorInvalidValue;
   if (mode >= 0 && (count < 1 || count > pages)) return (int)hipErrorInvalidValue;
   if (mode == 0 && (count < 1 + kAnchors || pages < kAnchors + kCurrent)) return (int)hipErrorInvalidValue;
@@ -789,13 +735,11 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
   p.C = count;
   p.mode = mode;
   p.total = total;
-  p.rmean = (const uint16_t*)mean;
   p.rdetail = (const uint16_t*)detail;
-  p.rbasis = (const uint16_t*)basis;
-  p.rvals = (uint16_t*)rep_values;
-  p.HPV = rep_head_pages;
+  p.rops = (uint16_t*)rep_ops;
+  p.RT = rep_tiles;
   const int np = (blocks + 1) / 2;
-  const int nrv = rep_values ? (heads * pages + kRvPages - 1) / kRvPages : 0;
+  const int nrv = rep_ops ? (heads * ((pages + 15) / 16) * kRepOpChunks + kThreads - 1) / kThreads : 0;
   hipLaunchKernelGGL(route_kernel, dim3(heads * np + nrv), dim3(kThreads), 0, stream, p);
   return (int)hipGetLastError();
 }

@@ -44,20 +44,31 @@ def kv_strides(k: torch.Tensor, v: torch.Tensor):
     raise ValueError("k/v must be contiguous [1,L,H,D] or head-major with equal strides")
 
 
+REP_OP_ELEMS = 768
+"""bf16 elements of one detail operand tile (16 pages, 1536 bytes)."""
+
+
+def rep_tiles(pages: int) -> int:
+    """Operand tiles a window of `pages` pages needs: ceil(pages / 16)."""
+    return (pages + 15) // 16
+
+
+def check_rep_ops(t: torch.Tensor, h: int, pages: int, name: str = "rep_ops"):
+    if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.dim() != 3 or t.shape[0] != h or \
+            t.shape[1] < rep_tiles(pages) or t.shape[2] != REP_OP_ELEMS:
+        raise ValueError(f"{name} must be a contiguous bf16 [H,>={rep_tiles(pages)},{REP_OP_ELEMS}] tensor")
+
+
 @torch.no_grad()
-def rep_values(s: Summary, basis: torch.Tensor, pages: int, out: torch.Tensor):
-    """Per-rep compensation values [H,P,4,D] (bf16) for the fused kernel."""
+def rep_operands(s: Summary, pages: int, out: torch.Tensor):
+    """The compensation's detail operand tiles [H,>=ceil(P/16),768] (bf16) of
+    the summary's detail rows, in the order the fused kernel reads them."""
     h = s.mean.shape[0]
     hp = _check_summary(s, h, pages)
-    b = basis if (basis.dtype == torch.bfloat16 and basis.is_contiguous()) else basis.to(torch.bfloat16).contiguous()
-    if b.shape != (h, HEAD_DIM, 8):
-        raise ValueError("basis must be [H,128,8]")
-    _lib.check(_lib.lib().ssa_rep_values(_lib.ptr(s.mean), _lib.ptr(s.detail), _lib.ptr(b), _lib.ptr(out), h, pages,
-                                         hp, out.shape[1], _lib.stream_handle(out.device)), "ssa_rep_values")
+    check_rep_ops(out, h, pages, "out")
+    _lib.check(_lib.lib().ssa_rep_operands(_lib.ptr(s.detail), _lib.ptr(out), h, pages, hp, out.shape[1],
+                                           _lib.stream_handle(out.device)), "ssa_rep_operands")
     return out
-
-
-rep_values_fn = rep_values   # attention() takes a `rep_values` keyword
 
 
 SINGLE_AV = False
@@ -69,7 +80,7 @@ the tail's _av at tuned_attention.py:16-18); True runs one bf16 product."""
 
 @torch.no_grad()
 def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None, all_pages=False,
-              rep_values=None):
+              rep_ops=None):
     """Exact attention over the LUT pages + summary compensation + merge.
 
     q [1,N,H,128] bf16 contiguous; k, v [1,64P,H,128] bf16 (resident cache);
@@ -78,17 +89,18 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None
     are not read).  Returns ``out`` [1,N,H,128] bf16, owned by `workspace`
     and overwritten by the next call.
 
-    Arithmetic: every probability multiplies V (and the rep value rows) as
-    the two-term bf16 product hi + lo, the reference's exact stage and its
-    ``bf16_av=True`` tail; ``bf16_av=False`` (the reference's tf32x3 tail) maps
-    to the same two-term product, the closest this kernel runs.
+    Arithmetic: every probability multiplies V as the two-term bf16 product
+    hi + lo, the reference's exact stage; the compensation weighs the page
+    means and the detail rows (through the bf16 basis) with two-term weights,
+    its ``bf16_av=True`` tail; ``bf16_av=False`` (the reference's tf32x3 tail)
+    maps to the same two-term products, the closest this kernel runs.
     ``single_av=True`` (default: the module's SINGLE_AV) opts into one bf16
-    product instead.  ``all_pages=True`` states that every row of ids lists
-    each page exactly once (a dense call): two query blocks then share each
-    K/V page load and ids are not read.  ``rep_values``: the [H,P,4,128] rep
-    value rows of `s` and `basis` when the caller already has them
-    (route(..., rep_out=...) writes them on the side); otherwise they are
-    computed here."""
+    product over the exact pages.  ``all_pages=True`` states that every row
+    of ids lists each page exactly once (a dense call): two query blocks then
+    share each K/V page load and ids are not read.  ``rep_ops``: the
+    [H,>=ceil(P/16),768] detail operand tiles of `s` when the caller already
+    has them (route(..., rep_out=...) writes them on the side); otherwise
+    they are computed here."""
     _, n, h, d = q.shape
     p = k.shape[1] // 64
     count = ids.shape[-1]
@@ -107,23 +119,24 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None
 
     if all_pages and count != p:
         raise ValueError("all_pages needs a table of exactly P pages per row")
-    if all_pages:
-        # every page exact: the kernel reads no rep rows (the rep keys stand
-        # in for the unused pointer)
-        vrep = s.keys
-    elif rep_values is not None:
-        if rep_values.dtype != torch.bfloat16 or not rep_values.is_contiguous() or rep_values.shape[0] != h or \
-                rep_values.shape[1] < p or tuple(rep_values.shape[2:]) != (4, d):
-            raise ValueError("rep_values must be a contiguous bf16 [H,>=P,4,128] tensor")
-        vrep = rep_values
+    b = basis if (basis.dtype == torch.bfloat16 and basis.is_contiguous()) else basis.to(torch.bfloat16).contiguous()
+    if b.shape != (h, HEAD_DIM, 8):
+        raise ValueError("basis must be [H,128,8]")
+    if all_pages and (n // 64) % 2 == 0:
+        # the two-block dense kernel reads no operand tiles
+        ops, ntiles = None, 0
+    elif rep_ops is not None:
+        check_rep_ops(rep_ops, h, p)
+        ops, ntiles = rep_ops, rep_ops.shape[1]
     else:
-        vrep = rep_values_fn(s, basis, p, buf('rep_values', (h, p, 4, d), torch.bfloat16))
+        ops = rep_operands(s, p, buf('rep_ops', (h, rep_tiles(p), REP_OP_ELEMS), torch.bfloat16))
+        ntiles = ops.shape[1]
     out = buf('out', q.shape, q.dtype)
     single = SINGLE_AV if single_av is None else bool(single_av)
     flags = (0 if single else 1) | (2 if all_pages else 0)
-    _lib.check(_lib.lib().ssa_attention(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(s.keys), _lib.ptr(vrep),
-                                        _lib.ptr(ids), _lib.ptr(out), n, h, p, hp, vrep.shape[1], count, tok, head,
-                                        flags, _lib.stream_handle(q.device)), "ssa_attention")
+    _lib.check(_lib.lib().ssa_attention(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(s.keys), _lib.ptr(s.mean),
+                                        _lib.ptr(b), _lib.ptr(ops), _lib.ptr(ids), _lib.ptr(out), n, h, p, hp, ntiles,
+                                        count, tok, head, flags, _lib.stream_handle(q.device)), "ssa_attention")
     return out
 
 
@@ -156,6 +169,6 @@ def risk(probes, z, summary, theta, *, z_tol=1e-4):
     out = torch.empty(h, t, p, device=probes.device, dtype=torch.float32)
     _lib.check(_lib.lib().ssa_route(_lib.ptr(pr), t * m * d, m * d, d, 1, _lib.ptr(summary.keys),
                                     _lib.ptr(summary.stats), _lib.ptr(th), None, None, _lib.ptr(out), None, None,
-                                    None, h, t, p, hp, 0, -1, 0, None, None, None, None, 0,
+                                    None, h, t, p, hp, 0, -1, 0, None, None, 0,
                                     _lib.stream_handle(probes.device)), "ssa_route")
     return out

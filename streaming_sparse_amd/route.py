@@ -29,7 +29,7 @@ import math
 import torch
 
 from . import _lib
-from .legacy_components import HEAD_DIM, _check_summary
+from .legacy_components import HEAD_DIM, _check_summary, check_rep_ops
 
 ANCHORS = 24
 CURRENT = 72
@@ -48,8 +48,7 @@ def tier_count(tier: str, pages: int, n: int | None = None) -> int:
 
 @torch.no_grad()
 def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=None, workspace=None,
-          want_mask=True, full_pset=None, encoding=None, reader=None, lse_out=None, rep_basis=None,
-          rep_out=None):
+          want_mask=True, full_pset=None, encoding=None, reader=None, lse_out=None, rep_out=None):
     """q [1,N,H,128] bf16 queries of the current chunk; summary over the P
     window pages; theta [H,4]; own [H,T] (default: page P-T+t).  For the
     intersection tier pass n = A+B (<= P - 24) and, unless P == 72,
@@ -57,9 +56,10 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
     full_pset: head ids to correct with `encoding` (pset.Encoding over the
     window) and `reader` (pset.Reader).  lse_out: optional [H,T,16] fp32
     tensor that receives each probe's log-sum-exp over all reps.
-    rep_basis [H,128,8] with rep_out [H,>=P,4,128] bf16: the router also
-    writes the attention's rep value rows (as legacy_components.rep_values)
-    into rep_out, so attention(..., rep_values=rep_out) skips that launch."""
+    rep_out [H,>=ceil(P/16),768] bf16: the router also writes the
+    attention's detail operand tiles of `summary` (as
+    legacy_components.rep_operands) into rep_out, so attention(...,
+    rep_ops=rep_out) skips that launch."""
     _, nq, h, d = q.shape
     if d != HEAD_DIM or q.dtype != torch.bfloat16 or not q.is_contiguous():
         raise ValueError("q must be contiguous [1,N,H,128] bf16")
@@ -108,22 +108,12 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
         lse = buf('lse', (h, t, 16), torch.float32)
     if lse is not None and (lse.shape != (h, t, 16) or lse.dtype != torch.float32 or not lse.is_contiguous()):
         raise ValueError("lse_out must be a contiguous [H,T,16] float32 tensor")
-    rb = None
     if rep_out is not None:
-        if rep_basis is None:
-            raise ValueError("rep_out needs rep_basis")
-        rb = rep_basis if (rep_basis.dtype == torch.bfloat16 and rep_basis.is_contiguous()) else \
-            rep_basis.to(torch.bfloat16).contiguous()
-        if rb.shape != (h, HEAD_DIM, 8):
-            raise ValueError("rep_basis must be [H,128,8]")
-        if rep_out.dtype != torch.bfloat16 or not rep_out.is_contiguous() or rep_out.shape[0] != h or \
-                rep_out.shape[1] < p or tuple(rep_out.shape[2:]) != (4, HEAD_DIM):
-            raise ValueError("rep_out must be a contiguous bf16 [H,>=P,4,128] tensor")
+        check_rep_ops(rep_out, h, p, "rep_out")
     _lib.check(_lib.lib().ssa_route(_lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys),
                                     _lib.ptr(summary.stats), _lib.ptr(th), _lib.ptr(cur), _lib.ptr(ow),
                                     _lib.ptr(risk), _lib.ptr(ids), _lib.ptr(mask), _lib.ptr(lse), h, t, p, hp, count,
-                                    mode, total, _lib.ptr(summary.mean) if rb is not None else None,
-                                    _lib.ptr(summary.detail) if rb is not None else None, _lib.ptr(rb),
+                                    mode, total, _lib.ptr(summary.detail) if rep_out is not None else None,
                                     _lib.ptr(rep_out), rep_out.shape[1] if rep_out is not None else 0,
                                     _lib.stream_handle(dev)), "ssa_route")
     if correcting:

@@ -49,7 +49,7 @@ import torch
 
 from . import _lib, group, pset, summary, workload
 from .attention import Workspace
-from .legacy_components import HEAD_DIM, attention, kv_strides
+from .legacy_components import HEAD_DIM, REP_OP_ELEMS, attention, kv_strides, rep_tiles
 from .ops import Summary
 from .route import route
 
@@ -316,15 +316,15 @@ class StreamRuntime:
         a_tab, n_tab = self.quota(self.chunk)
         a = a_tab[step, layer - 1]
         n = int(n_tab[step][layer - 1])
-        vrep = self.ws.tensor('rt_rep_values', (self.H, P, 4, HEAD_DIM), q.device, torch.bfloat16)
+        ops = self.ws.tensor('rt_rep_ops', (self.H, rep_tiles(P), REP_OP_ELEMS), q.device, torch.bfloat16)
         ids, _, _, _ = route(q, s, self.theta, tier='intersection', current_slots=a, n=n, workspace=self.ws,
                              want_mask=correct, lse_out=self.lse if correct else None,
                              full_pset=cfg.pset_heads if correct else None, encoding=L.encoding,
-                             reader=self.reader, rep_basis=L.basis, rep_out=vrep)
+                             reader=self.reader, rep_out=ops)
         self.calls['sparse'] += 1
         self.calls['full_pset'] += int(correct)
         self.last_ids = ids
-        return attention(q, kw, vw, s, L.basis, ids, self.ws, rep_values=vrep)
+        return attention(q, kw, vw, s, L.basis, ids, self.ws, rep_ops=ops)
 
     def commit_chunk(self, inputs):
         """The clean step's commit of every layer: one batched grouping of the

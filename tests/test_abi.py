@@ -21,7 +21,7 @@ def declared():
 
 
 def test_header_declares_entry_points():
-    assert set(declared()) == {"ssa_rep_values", "ssa_attention", "ssa_route", "ssa_select", "ssa_encode", "ssa_pset",
+    assert set(declared()) == {"ssa_rep_operands", "ssa_attention", "ssa_route", "ssa_select", "ssa_encode", "ssa_pset",
                                "ssa_summary", "ssa_pset_noalloc", "ssa_anchor_rebase", "ssa_commit_pages",
                                "ssa_group_order"}
 

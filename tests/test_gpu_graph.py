@@ -21,12 +21,11 @@ def test_call_replays_in_a_graph(device):
     P, H, D = g.pages, 12, 128
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()
-    vrep = ws.tensor('graph_rep_values', (H, P, 4, D), device, torch.bfloat16)
+    ops = ws.tensor('graph_rep_ops', (H, (P + 15) // 16, 768), device, torch.bfloat16)
 
     def call():
-        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_basis=basis,
-                             rep_out=vrep)
-        return ids, attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep)
+        ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_out=ops)
+        return ids, attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_ops=ops)
 
     ids, out = call()                      # eager: also creates every workspace buffer
     torch.cuda.synchronize()

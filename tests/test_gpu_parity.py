@@ -196,24 +196,49 @@ def test_route_intersection_matches_oracle(device):
     assert (mask.cpu()[..., :24]).all() and (got_mask[..., P - 72:].sum(-1) == a[:, None]).all()
 
 
+def operand_tiles(detail, pages):
+    """The detail operand tiles [H, ceil(P/16), 768] that ssa_rep_operands
+    documents, restated with index arithmetic on the CPU: element j of chunk
+    ((pair*2 + hh)*8 + rank)*3 + m of tile rt is detail[page, a, rank] with
+    v = 4m + j % 4, page = 16 rt + 8 pair + 2 (v // 3) + hh, a = v % 3, and 0
+    for pages >= P."""
+    h = detail.shape[0]
+    tiles = (pages + 15) // 16
+    out = torch.zeros(h, tiles, 2, 2, 8, 3, 8, dtype=torch.bfloat16)
+    for rt in range(tiles):
+        for pair in range(2):
+            for hh in range(2):
+                for m in range(3):
+                    for j in range(8):
+                        v = 4 * m + j % 4
+                        pg = 16 * rt + 8 * pair + 2 * (v // 3) + hh
+                        if pg < pages:
+                            out[:, rt, pair, hh, :, m, j] = detail[:, pg, v % 3, :]
+    return out.reshape(h, tiles, 768)
+
+
 @pytest.mark.parametrize("cfg,frames", [(0, 9), (1, 18)])
-def test_route_writes_rep_values(device, cfg, frames):
-    """The router's side output of rep value rows equals the standalone
-    rep-value kernel bit for bit (into a slab wider than the window), and the
-    attention call that reads them equals the one that computes its own."""
-    from streaming_sparse_amd.legacy_components import rep_values
+def test_route_writes_rep_operands(device, cfg, frames):
+    """The router's side output of detail operand tiles equals the standalone
+    kernel bit for bit (into a slab wider than the window), both equal the
+    documented layout restated on the CPU, and the attention call that reads
+    them equals the one that computes its own."""
+    from streaming_sparse_amd.legacy_components import rep_operands
     x = call_inputs(cfg, frames)
     g = x.to(device)
     P = x.pages
+    T = (P + 15) // 16
     basis = g.basis.to(torch.bfloat16).contiguous()
-    want = rep_values(g.summary, basis, P, torch.empty(12, P, 4, 128, device=device, dtype=torch.bfloat16))
-    slab = torch.full((12, P + 5, 4, 128), float("nan"), device=device, dtype=torch.bfloat16)
-    ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, rep_basis=basis, rep_out=slab)
-    assert torch.equal(slab[:, :P].view(torch.int16), want.view(torch.int16))
-    assert bool(slab[:, P:].isnan().all())           # rows past the window untouched
+    want = rep_operands(g.summary, P, torch.empty(12, T, 768, device=device, dtype=torch.bfloat16))
+    slab = torch.full((12, T + 2, 768), float("nan"), device=device, dtype=torch.bfloat16)
+    ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, rep_out=slab)
+    assert torch.equal(slab[:, :T].view(torch.int16), want.view(torch.int16))
+    assert bool(slab[:, T:].isnan().all())           # tiles past the window untouched
+    layout = operand_tiles(x.summary.detail[:, :P], P)
+    assert torch.equal(want.cpu().view(torch.int16), layout.view(torch.int16))
     ws = Workspace()
     a = attention(g.q, g.k, g.v, g.summary, basis, ids, ws).clone()
-    b = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=slab)
+    b = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_ops=slab)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
@@ -283,10 +308,11 @@ def test_attention_config2_intersection_tiles(device, single):
 def test_full_call_properties(device, single):
     """Size-independent properties of the whole base call at its full size
     (432 pages, 12 heads, 4608 queries), where the oracle would take minutes:
-    - two calls on the same inputs give bit-identical risk, page tables, rep
-      value rows and outputs (no atomics or order-dependent reductions);
-    - scaling V, the page V means and the V details by 2 scales every rep
-      value and every output by exactly 2 (the compensated and exact parts are
+    - two calls on the same inputs give bit-identical risk, page tables,
+      detail operand tiles and outputs (no atomics or order-dependent
+      reductions);
+    - scaling V, the page V means and the V details by 2 scales every operand
+      tile and every output by exactly 2 (the compensated and exact parts are
       linear in V, and a power of two commutes with every rounding);
     - reversing the order of each row's pages after its own page changes the
       output only by the online softmax's rounding, well inside the parity bar."""
@@ -296,9 +322,9 @@ def test_full_call_properties(device, single):
     ws = Workspace()
 
     def call(v, s):
-        vrep = torch.empty(12, x.pages, 4, 128, device=device, dtype=torch.bfloat16)
-        ids, _, risk, _ = route(g.q, s, g.theta, tier='base', own=g.own, workspace=ws, rep_basis=basis, rep_out=vrep)
-        out = attention(g.q, g.k, v, s, basis, ids, ws, rep_values=vrep, single_av=single).clone()
+        vrep = torch.empty(12, (x.pages + 15) // 16, 768, device=device, dtype=torch.bfloat16)
+        ids, _, risk, _ = route(g.q, s, g.theta, tier='base', own=g.own, workspace=ws, rep_out=vrep)
+        out = attention(g.q, g.k, v, s, basis, ids, ws, rep_ops=vrep, single_av=single).clone()
         return ids.clone(), risk.clone(), vrep, out
 
     ids, risk, vrep, out = call(g.v, g.summary)
@@ -315,7 +341,7 @@ def test_full_call_properties(device, single):
     assert torch.equal(vrep3, vrep * 2) and torch.equal(out3, out * 2)
 
     rev = torch.cat([ids[..., :1], ids[..., 1:].flip(-1)], -1).contiguous()
-    out4 = attention(g.q, g.k, g.v, g.summary, basis, rev, ws, rep_values=vrep, single_av=single).clone()
+    out4 = attention(g.q, g.k, g.v, g.summary, basis, rev, ws, rep_ops=vrep, single_av=single).clone()
     torch.cuda.synchronize()
     check_out(out4, out.cpu(), "reversed page order")
 
@@ -332,10 +358,9 @@ def test_route_and_attention_largest_window(device):
     count = P * 15 // 100
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()
-    vrep = torch.empty(12, P, 4, 128, device=device, dtype=torch.bfloat16)
-    ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, rep_basis=basis,
-                               rep_out=vrep)
-    out = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_values=vrep)
+    vrep = torch.empty(12, (P + 15) // 16, 768, device=device, dtype=torch.bfloat16)
+    ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, rep_out=vrep)
+    out = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_ops=vrep)
     torch.cuda.synchronize()
     r64 = ref.risk(ref.probes(x.q), ref.route_logits(ref.probes(x.q), x.summary.keys, torch.float64),
                    x.summary.stats, x.theta, dtype=torch.float64)
@@ -352,8 +377,8 @@ def test_route_and_attention_largest_window(device):
     same_set = (got.sort(-1).values == want_ids.sort(-1).values).all(-1)
     print(f"P={P}: {int(same.sum())}/{same.numel()} rows identical, {int(ties.sum())} near-tie rows", flush=True)
     assert bool((same | ties | (order_ties & same_set)).all())
-    from streaming_sparse_amd.legacy_components import rep_values
-    want_rv = rep_values(g.summary, basis, P, torch.empty_like(vrep))
+    from streaming_sparse_amd.legacy_components import rep_operands
+    want_rv = rep_operands(g.summary, P, torch.empty_like(vrep))
     assert torch.equal(vrep.view(torch.int16), want_rv.view(torch.int16))
     tiles = [0, 17, 40, 71]
     want = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, got, tiles=tiles).bfloat16()

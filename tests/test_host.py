@@ -63,7 +63,7 @@ def test_route_rejects_bad_arguments():
     with pytest.raises(ValueError):
         route(q, summary_slab(72), theta, tier='base')                # base tier needs a history window
     with pytest.raises(ValueError):
-        route(q, s, theta, rep_out=torch.zeros(H, 216, 4, D, dtype=torch.bfloat16))   # rep_out needs rep_basis
+        route(q, s, theta, rep_out=torch.zeros(H, 13, 768, dtype=torch.bfloat16))    # rep_out: ceil(216/16) tiles
     with pytest.raises(ValueError):
         route(q, s, theta, full_pset=[0])                             # Full_Pset only on the intersection tier
     with pytest.raises(ValueError):
@@ -125,18 +125,23 @@ def test_quota_tables_keep_totals():
 def test_c_abi_rejects_bad_shapes():
     L = _lib.lib()
     N = None
-    # ssa_attention: queries a multiple of 64, pages <= 512, count <= pages, K/V rows of 128 elements
-    att = lambda n, pages, count, tok: L.ssa_attention(N, N, N, N, N, N, N, n, 12, pages, pages, pages, count, tok,
-                                                       128, 0, N)
+    # ssa_attention: queries a multiple of 64, pages <= 512, count <= pages, K/V rows of 128 elements; the
+    # general call needs page means, basis and ceil(pages/16) operand tiles, 16-byte aligned
+    att = lambda n, pages, count, tok, mean=16, ops=16, tiles=27, flags=0: L.ssa_attention(
+        N, N, N, N, mean, 16, ops, N, N, n, 12, pages, pages, tiles, count, tok, 128, flags, N)
     assert att(65, 432, 64, 1536) == INVALID
     assert att(4608, 513, 64, 1536) == INVALID
     assert att(4608, 432, 433, 1536) == INVALID
     assert att(4608, 432, 64, 64) == INVALID
+    assert att(4608, 432, 64, 1536, mean=None) == INVALID
+    assert att(4608, 432, 64, 1536, ops=None) == INVALID
+    assert att(4608, 432, 64, 1536, ops=24) == INVALID                # misaligned
+    assert att(4608, 432, 64, 1536, tiles=26) == INVALID              # 432 pages need 27 tiles
     # ssa_route: pages in (0, 512], modes -1..2, base count >= 25, quota count = 24 + total,
-    # rep-value pointers 16-byte aligned
-    rt = lambda pages, count, mode, total, cur=None, rv=None, mean=None: L.ssa_route(
+    # operand tiles (when asked for) 16-byte aligned, ceil(pages/16) of them, with the detail rows
+    rt = lambda pages, count, mode, total, cur=None, ops=None, det=None, tiles=32: L.ssa_route(
         N, 128, 64 * 12 * 128, 12 * 128, 0, N, N, N, cur, N, N, N, N, N, 12, 72, pages, pages, count, mode, total,
-        mean, mean, mean, rv, pages, N)
+        det, ops, tiles, N)
     assert rt(0, 64, 0, 0) == INVALID
     assert rt(513, 64, 0, 0) == INVALID
     assert rt(432, 64, 3, 0) == INVALID
@@ -148,8 +153,9 @@ def test_c_abi_rejects_bad_shapes():
     assert rt(216, 24 + 193, 1, 193, cur=8) == INVALID                # total > P - 24
     assert rt(432, 20, 1, -4, cur=8) == INVALID                       # negative total
     assert rt(80, 44, 1, 20, cur=8) == INVALID                        # 72 < P < 96: no such window
-    assert rt(432, 64, 0, 0, rv=16, mean=None) == INVALID            # rep values without mean/detail/basis
-    assert rt(432, 64, 0, 0, rv=16, mean=8) == INVALID               # misaligned
+    assert rt(432, 64, 0, 0, ops=16, det=None) == INVALID             # operand tiles without detail rows
+    assert rt(432, 64, 0, 0, ops=8, det=16) == INVALID                # misaligned
+    assert rt(432, 64, 0, 0, ops=16, det=16, tiles=26) == INVALID     # 432 pages need 27 tiles
     # ssa_select: 0 < pages <= 512, 1 <= cap <= min(id_capacity, pages), density count <= id_capacity,
     # scores / own / outputs present (valid may be NULL)
     sel = lambda rows, pages, thr, fixed, cap, idcap, sc=8: L.ssa_select(sc, 8, N, rows, pages, 0.0, thr, fixed, cap,
@@ -178,7 +184,13 @@ def test_c_abi_rejects_bad_shapes():
                                          N, N, N, 3, N, N, N, N, N, N, N, 12, 72, pages, count, N)
     assert ps(96, 40) == INVALID
     assert ps(432, 400) == INVALID
-    assert L.ssa_rep_values(N, N, N, N, 0, 432, 432, 432, N) == INVALID
+    # ssa_rep_operands: heads >= 1, pages in (0, 512], ceil(pages/16) tiles, aligned output
+    ro = lambda heads, pages, tiles, out=16: L.ssa_rep_operands(16, out, heads, pages, 512, tiles, N)
+    assert ro(0, 432, 27) == INVALID
+    assert ro(12, 513, 33) == INVALID
+    assert ro(12, 432, 26) == INVALID
+    assert ro(12, 432, 27, out=8) == INVALID
+    assert ro(12, 432, 27, out=None) == INVALID
 
 
 def test_select_rejects_bad_config():
