@@ -529,7 +529,12 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     const lds_u8* kb = kslot(cur ^ 1);
     const lds_u8* vb = vslot(cur);
     uint32_t kl = klane, vl = vlane;
-    asm volatile("" : "+v"(kl), "+v"(vl));
+    // the two-term kernel has the registers to keep its 8 K read addresses
+    // across units; the single-term one re-forms them each step
+    if (PRECISE)
+      asm volatile("" : "+v"(vl));
+    else
+      asm volatile("" : "+v"(kl), "+v"(vl));
     if (PRECISE) {
       // Two-term P.V in three stages of 8 matrix products, each carrying a
       // similar share of the vector work, so that the matrix and vector
