@@ -43,11 +43,11 @@ extern "C" {
 #endif
 
 /* Detail operand tiles of the compensation: for each head and each tile of
- * 16 pages (rt < ceil(pages/16)), 1536 bytes holding the detail rows
+ * 16 pages (rt < ceil(pages/16)), 1024 bytes holding the detail rows
  * detail[h,p,a,:] (a = 0..2 Haar contrasts, rank 8) of the tile's pages in
  * the order the attention kernel's matrix products read them; pages >=
  * `pages` hold zeros.  detail [H,head_pages,3,8] bf16; rep_ops
- * [H,rep_tiles,768] bf16 (16-byte aligned), rep_tiles >= ceil(pages/16).
+ * [H,rep_tiles,512] bf16 (16-byte aligned), rep_tiles >= ceil(pages/16).
  * Recompute when the detail rows change. */
 int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, int head_pages, int rep_tiles,
                      hipStream_t stream);
@@ -58,7 +58,7 @@ int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, in
  * q, out [1,n_tokens,H,128] bf16 contiguous; k, v: page p, token j, head h at
  * element (64p+j)*kv_token_stride + h*kv_head_stride (+ dim); keys
  * [H,head_pages,4,128] bf16 (rep keys); mean [H,head_pages,128] bf16 (page V
- * means); basis [H,128,8] bf16; rep_ops [H,rep_tiles,768] from
+ * means); basis [H,128,8] bf16; rep_ops [H,rep_tiles,512] from
  * ssa_rep_operands (mean, basis and rep_ops 16-byte aligned; not read by a
  * dense call, flags bit 1);
  * ids [H,n_tokens/64,count] int32: page ids, own page first; entries
@@ -101,7 +101,7 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
  * ids [H,blocks,count] int32 and mask [H,blocks,pages] uint8 may be NULL; lse
  * [H,blocks,16] fp32 (NULL to skip) receives each probe's log-sum-exp over
  * all reps of the window (natural log), the input ssa_pset needs.
- * rep_ops [H,rep_tiles,768] bf16 (NULL to skip; 16-byte aligned, rep_tiles >=
+ * rep_ops [H,rep_tiles,512] bf16 (NULL to skip; 16-byte aligned, rep_tiles >=
  * ceil(pages/16)) receives, on the side, exactly what ssa_rep_operands
  * writes from detail [H,head_pages,3,8], so a call that routes needs no
  * separate operand launch. */

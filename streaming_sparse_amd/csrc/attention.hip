@@ -17,7 +17,7 @@
 // are never formed: with w_pr its rep weights, its share of the numerator is
 //   sum_p a_p mean_p + (sum_{p,a} b_pa detail_pa) . basis^T,
 // a_p = sum_r w_pr, b_pa = sum_r HAAR[a,r] w_pr, so the tile costs one
-// 8-page product against the page means and three rank-8 products into a
+// 8-page product against the page means and two rank-8 products into a
 // per-query code accumulator, which meets the basis once at the end.
 //
 // Workgroup: 4 waves, 64 queries of one head.  Wave w: pair w/2 takes keys
@@ -179,11 +179,8 @@ __device__ __forceinline__ void issue_rows(const AttnParams& p, const UnitSource
     const int rt = rep_tile(e);
     const int w = __builtin_amdgcn_readfirstlane(wave);
     if (w == 1) {
-      // 96 chunks of 16 bytes: lanes 0..63, then lanes 0..31 for the rest
-      const uint8_t* base = src.rops + (uint32_t)rt * kRepOpBytes;
-      const uint32_t off = 16u * (uint32_t)lane;
-      dma16(base, off, l);
-      if (lane < 32) dma16(base + 1024, off, l + 1024);
+      // 64 chunks of 16 bytes, one per lane
+      dma16(src.rops + (uint32_t)rt * kRepOpBytes, 16u * (uint32_t)lane, l);
     } else if (w != 3) {
       // rows rho and rho + 4 hold page pg, rows rho + 8 and rho + 12 page
       // pg + 1; pages >= P re-read page P - 1 (their weights are zero)
@@ -503,7 +500,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const UnitSources src = unit_sources(p, h);
   // this lane's detail operand rows (rank r % 8 of its half's 12 pairs) in a
   // rep tile's V slot
-  const uint32_t det_off = kDetailOff + ((pair * 2 + hh) * 8 + (r & 7)) * 48;
+  const uint32_t det_off = kDetailOff + ((pair * 2 + hh) * 8 + (r & 7)) * 32;
   const uint32_t klane = k_base(pair, lane), vlane = v_base(pair, lane);
   auto unit = [&](int i) { return __builtin_amdgcn_readfirstlane(units[i]); };
   // prologue: K0, V0, K1 in flight; S of unit 0 and its max
@@ -647,26 +644,33 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     }
   };
 
-  // The compensation of rep tile i (probabilities of Sc), with two-term
-  // (hi, lo) weights in the two-term path and one bf16 term (lo = 0) in the
-  // single-term path; with NEXT also S(i+1) from K slot kb and its max.  Lane (query r, half hh) holds the 4 reps of
-  // pair-local page 2 jp + hh in Sc[4 jp .. 4 jp + 3] (jp = 0..3).
-  //  * contrasts: C += D^T B^T in 3 products; product mm takes, in k =
-  //    8 hh + j, the weights v = 4 mm + (j & 3) of lane half hh's 12
-  //    (page, contrast) pairs v = 3 jp + a as hi parts (j < 4) and lo parts
-  //    (j >= 4), against A rows = detail[page][a][rank] (the operand tile);
+  // The compensation of rep tile i (probabilities of Sc); with NEXT also
+  // S(i+1) from the other K slot and its max.  Lane (query r, half hh) holds
+  // the 4 reps of pair-local page 2 jp + hh in Sc[4 jp .. 4 jp + 3] (jp =
+  // 0..3).
+  //  * contrasts: C += D^T B^T in 2 products; product mm takes, in k =
+  //    8 hh + j, the bf16 weight v = 8 mm + j of lane half hh's 12 (page,
+  //    contrast) pairs v = 3 jp + a (v >= 12: zero) against A rows =
+  //    detail[page][a][rank] (the operand tile);
   //  * means: O^T += M^T A^T, one product per dim tile over the pair's 8
   //    pages, k = 8 hh + e holding page e < 4 ? 2 e : 2 e - 7, the lo parts
-  //    of its mean weight in half 0 and the hi parts in half 1; M^T is read
-  //    as the V operand of k step 0 from the mean rows the loads placed.
+  //    of its mean weight in half 0 and the hi parts in half 1 (two-term
+  //    path; one bf16 term, lo = 0, in the single-term path); M^T is read as
+  //    the V operand of k step 0 from the mean rows the loads placed.
+  // The contrast weights take one bf16 term in both paths: the detail term is
+  // a small share of a rep's value, which the reference's tail rounds to
+  // bf16 as a whole.
   auto rep_body = [&](auto next_c, auto kind, int cur, const f32x16& Sc, f32x16& Sn, float nb) {
     constexpr bool NEXT = decltype(next_c)::value;
     constexpr int K = decltype(kind)::value;
     const lds_u8* kb = kslot(cur ^ 1);
     const lds_u8* vb = vslot(cur);
     uint32_t kl = klane, vl = vlane, dl = det_off;
-    asm volatile("" : "+v"(kl), "+v"(vl), "+v"(dl));
-    u32x4 ka[8], va[4], dop[3];
+    if (PRECISE)
+      asm volatile("" : "+v"(vl), "+v"(dl));
+    else
+      asm volatile("" : "+v"(kl), "+v"(vl), "+v"(dl));
+    u32x4 ka[8], va[4], dop[2];
     float hw[16];   // probabilities, then at 4 jp the Haar view of page jp
     if constexpr (NEXT) {
 #pragma unroll
@@ -682,24 +686,29 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
         Sn = mfma32(ka[st], qop[st], Sn);
         if (st < 4) ka[st + 4] = k_read(kb, kl, st + 4);
       }
-      if (st >= 4 && st < 7) dop[st - 4] = *(lds_u32x4*)(vb + dl + 16 * (st - 4));
+      if (st >= 4 && st < 6) dop[st - 4] = *(lds_u32x4*)(vb + dl + 16 * (st - 4));
       hw[2 * st] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st], p.scale_log2, nb));
       hw[2 * st + 1] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st + 1], p.scale_log2, nb));
       if (st & 1) haar4(hw + 4 * (st >> 1), hw + 4 * (st >> 1));
       __builtin_amdgcn_sched_barrier(0);
     }
-    // the contrast products, each with the splits of its 4 weights and the
-    // read of one mean operand
+    // the two contrast products, each with its weights' packing and the reads
+    // of two mean operands
     auto bw = [&](int v) { return hw[4 * (v / 3) + 1 + v % 3]; };
     auto wsplit = [&](float a, float b) { return PRECISE ? split_pair(a, b) : u32x2{pack_bf16(a, b), 0u}; };
-#pragma unroll
-    for (int mm = 0; mm < 3; ++mm) {
-      const u32x2 s0 = wsplit(bw(4 * mm), bw(4 * mm + 1)), s1 = wsplit(bw(4 * mm + 2), bw(4 * mm + 3));
-      C = mfma32(dop[mm], u32x4{s0[0], s1[0], s0[1], s1[1]}, C);
-      va[mm] = v_read(vb, vl, 0, mm);
+    {
+      const u32x4 b0 = {pack_bf16(bw(0), bw(1)), pack_bf16(bw(2), bw(3)), pack_bf16(bw(4), bw(5)),
+                        pack_bf16(bw(6), bw(7))};
+      C = mfma32(dop[0], b0, C);
+      va[0] = v_read(vb, vl, 0, 0);
+      va[1] = v_read(vb, vl, 0, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 b1 = {pack_bf16(bw(8), bw(9)), pack_bf16(bw(10), bw(11)), 0u, 0u};
+      C = mfma32(dop[1], b1, C);
+      va[2] = v_read(vb, vl, 0, 2);
+      va[3] = v_read(vb, vl, 0, 3);
       __builtin_amdgcn_sched_barrier(0);
     }
-    va[3] = v_read(vb, vl, 0, 3);
     const u32x2 a01 = wsplit(hw[0], hw[4]), a23 = wsplit(hw[8], hw[12]);
     const u32x2 x0 = halves(a01[1], a01[0]), x1 = halves(a23[1], a23[0]);
     const u32x4 am = {x0[0], x1[0], x0[1], x1[1]};

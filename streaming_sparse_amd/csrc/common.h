@@ -105,30 +105,30 @@ __device__ __forceinline__ void dma_rows(const void* base, const uint32_t (&off)
 // each (pair, hh, rank) = the matrix-pipe A rows of one lane, the rank-`rank`
 // element of detail[page][a] for the 12 (page, contrast) pairs that lane half
 // hh of key pair `pair` weighs: v = 3 jp + a, page 16 rt + 8 pair + 2 jp + hh
-// (jp = 0..3, a = 0..2).  16-byte chunk c = ((pair * 2 + hh) * 8 + rank) * 3
-// + m is the A operand of contrast product m: elements j -> v = 4 m + (j & 3)
-// (the hi and lo halves of k share a detail value).  Pages >= P read zero.
-constexpr int kRepOpBytes = 1536;
+// (jp = 0..3, a = 0..2), as two 16-byte chunks c = ((pair * 2 + hh) * 8 +
+// rank) * 2 + m, element j -> v = 8 m + j (v >= 12: zero), the A operands of
+// the two contrast products.  Pages >= P read zero.
+constexpr int kRepOpBytes = 1024;
 constexpr int kRepOpChunks = kRepOpBytes / 16;
 
 // Chunk c of operand tile rt from one head's detail rows [HP, 3, 8] bf16.
 // Shared by every kernel that writes the tiles, so they agree bit for bit.
 __device__ __forceinline__ u32x4 rep_operand_chunk(const uint16_t* det, int P, int rt, int c) {
-  const int m = c % 3, rank = (c / 3) & 7, hh = (c / 24) & 1, pair = c / 48;
-  uint32_t w[2];
+  const int m = c & 1, rank = (c >> 1) & 7, hh = (c >> 4) & 1, pair = c >> 5;
+  u32x4 out;
 #pragma unroll
-  for (int x = 0; x < 2; ++x) {
+  for (int x = 0; x < 4; ++x) {
     uint32_t packed = 0;
 #pragma unroll
     for (int y = 0; y < 2; ++y) {
-      const int v = 4 * m + 2 * x + y, jp = v / 3, a = v % 3;
+      const int v = 8 * m + 2 * x + y, jp = v / 3, a = v % 3;
       const int pg = 16 * rt + 8 * pair + 2 * jp + hh;
-      const uint32_t val = pg < P ? (uint32_t)det[pg * 24 + a * 8 + rank] : 0u;
+      const uint32_t val = (v < 12 && pg < P) ? (uint32_t)det[pg * 24 + a * 8 + rank] : 0u;
       packed |= val << (16 * y);
     }
-    w[x] = packed;
+    out[x] = packed;
   }
-  return u32x4{w[0], w[1], w[0], w[1]};
+  return out;
 }
 
 }  // namespace ssa

@@ -44,8 +44,8 @@ def kv_strides(k: torch.Tensor, v: torch.Tensor):
     raise ValueError("k/v must be contiguous [1,L,H,D] or head-major with equal strides")
 
 
-REP_OP_ELEMS = 768
-"""bf16 elements of one detail operand tile (16 pages, 1536 bytes)."""
+REP_OP_ELEMS = 512
+"""bf16 elements of one detail operand tile (16 pages, 1024 bytes)."""
 
 
 def rep_tiles(pages: int) -> int:
@@ -61,7 +61,7 @@ def check_rep_ops(t: torch.Tensor, h: int, pages: int, name: str = "rep_ops"):
 
 @torch.no_grad()
 def rep_operands(s: Summary, pages: int, out: torch.Tensor):
-    """The compensation's detail operand tiles [H,>=ceil(P/16),768] (bf16) of
+    """The compensation's detail operand tiles [H,>=ceil(P/16),512] (bf16) of
     the summary's detail rows, in the order the fused kernel reads them."""
     h = s.mean.shape[0]
     hp = _check_summary(s, h, pages)
@@ -98,7 +98,7 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None
     product over the exact pages.  ``all_pages=True`` states that every row
     of ids lists each page exactly once (a dense call): two query blocks then
     share each K/V page load and ids are not read.  ``rep_ops``: the
-    [H,>=ceil(P/16),768] detail operand tiles of `s` when the caller already
+    [H,>=ceil(P/16),512] detail operand tiles of `s` when the caller already
     has them (route(..., rep_out=...) writes them on the side); otherwise
     they are computed here."""
     _, n, h, d = q.shape

@@ -56,7 +56,7 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
     full_pset: head ids to correct with `encoding` (pset.Encoding over the
     window) and `reader` (pset.Reader).  lse_out: optional [H,T,16] fp32
     tensor that receives each probe's log-sum-exp over all reps.
-    rep_out [H,>=ceil(P/16),768] bf16: the router also writes the
+    rep_out [H,>=ceil(P/16),512] bf16: the router also writes the
     attention's detail operand tiles of `summary` (as
     legacy_components.rep_operands) into rep_out, so attention(...,
     rep_ops=rep_out) skips that launch."""

@@ -21,7 +21,7 @@ def test_call_replays_in_a_graph(device):
     P, H, D = g.pages, 12, 128
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()
-    ops = ws.tensor('graph_rep_ops', (H, (P + 15) // 16, 768), device, torch.bfloat16)
+    ops = ws.tensor('graph_rep_ops', (H, (P + 15) // 16, 512), device, torch.bfloat16)
 
     def call():
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_out=ops)

@@ -197,24 +197,24 @@ def test_route_intersection_matches_oracle(device):
 
 
 def operand_tiles(detail, pages):
-    """The detail operand tiles [H, ceil(P/16), 768] that ssa_rep_operands
+    """The detail operand tiles [H, ceil(P/16), 512] that ssa_rep_operands
     documents, restated with index arithmetic on the CPU: element j of chunk
-    ((pair*2 + hh)*8 + rank)*3 + m of tile rt is detail[page, a, rank] with
-    v = 4m + j % 4, page = 16 rt + 8 pair + 2 (v // 3) + hh, a = v % 3, and 0
-    for pages >= P."""
+    ((pair*2 + hh)*8 + rank)*2 + m of tile rt is detail[page, a, rank] with
+    v = 8m + j, page = 16 rt + 8 pair + 2 (v // 3) + hh, a = v % 3, and 0
+    for v >= 12 or pages >= P."""
     h = detail.shape[0]
     tiles = (pages + 15) // 16
-    out = torch.zeros(h, tiles, 2, 2, 8, 3, 8, dtype=torch.bfloat16)
+    out = torch.zeros(h, tiles, 2, 2, 8, 2, 8, dtype=torch.bfloat16)
     for rt in range(tiles):
         for pair in range(2):
             for hh in range(2):
-                for m in range(3):
+                for m in range(2):
                     for j in range(8):
-                        v = 4 * m + j % 4
+                        v = 8 * m + j
                         pg = 16 * rt + 8 * pair + 2 * (v // 3) + hh
-                        if pg < pages:
+                        if v < 12 and pg < pages:
                             out[:, rt, pair, hh, :, m, j] = detail[:, pg, v % 3, :]
-    return out.reshape(h, tiles, 768)
+    return out.reshape(h, tiles, 512)
 
 
 @pytest.mark.parametrize("cfg,frames", [(0, 9), (1, 18)])
@@ -229,8 +229,8 @@ def test_route_writes_rep_operands(device, cfg, frames):
     P = x.pages
     T = (P + 15) // 16
     basis = g.basis.to(torch.bfloat16).contiguous()
-    want = rep_operands(g.summary, P, torch.empty(12, T, 768, device=device, dtype=torch.bfloat16))
-    slab = torch.full((12, T + 2, 768), float("nan"), device=device, dtype=torch.bfloat16)
+    want = rep_operands(g.summary, P, torch.empty(12, T, 512, device=device, dtype=torch.bfloat16))
+    slab = torch.full((12, T + 2, 512), float("nan"), device=device, dtype=torch.bfloat16)
     ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, rep_out=slab)
     assert torch.equal(slab[:, :T].view(torch.int16), want.view(torch.int16))
     assert bool(slab[:, T:].isnan().all())           # tiles past the window untouched
@@ -322,7 +322,7 @@ def test_full_call_properties(device, single):
     ws = Workspace()
 
     def call(v, s):
-        vrep = torch.empty(12, (x.pages + 15) // 16, 768, device=device, dtype=torch.bfloat16)
+        vrep = torch.empty(12, (x.pages + 15) // 16, 512, device=device, dtype=torch.bfloat16)
         ids, _, risk, _ = route(g.q, s, g.theta, tier='base', own=g.own, workspace=ws, rep_out=vrep)
         out = attention(g.q, g.k, v, s, basis, ids, ws, rep_ops=vrep, single_av=single).clone()
         return ids.clone(), risk.clone(), vrep, out
@@ -358,7 +358,7 @@ def test_route_and_attention_largest_window(device):
     count = P * 15 // 100
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()
-    vrep = torch.empty(12, (P + 15) // 16, 768, device=device, dtype=torch.bfloat16)
+    vrep = torch.empty(12, (P + 15) // 16, 512, device=device, dtype=torch.bfloat16)
     ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws, rep_out=vrep)
     out = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, rep_ops=vrep)
     torch.cuda.synchronize()

@@ -63,7 +63,7 @@ def test_route_rejects_bad_arguments():
     with pytest.raises(ValueError):
         route(q, summary_slab(72), theta, tier='base')                # base tier needs a history window
     with pytest.raises(ValueError):
-        route(q, s, theta, rep_out=torch.zeros(H, 13, 768, dtype=torch.bfloat16))    # rep_out: ceil(216/16) tiles
+        route(q, s, theta, rep_out=torch.zeros(H, 13, 512, dtype=torch.bfloat16))    # rep_out: ceil(216/16) tiles
     with pytest.raises(ValueError):
         route(q, s, theta, full_pset=[0])                             # Full_Pset only on the intersection tier
     with pytest.raises(ValueError):
