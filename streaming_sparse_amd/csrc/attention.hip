@@ -406,16 +406,20 @@ __device__ __forceinline__ void pv(const u32x4 (&pb)[2], const u32x4 (&pl)[2], c
 // (the -1 padding of a shorter table) are not read: they add no exact unit
 // and select nothing.  A page listed twice is attended twice, as a LUT walk
 // does.  Called by every 4-wave workgroup's threads; wcount is 4 ints of LDS.
-__device__ void own_units(const AttnParams& p, int h, int t, int tid, int* units, uint32_t* maskw, int* wcount,
-                          int* nunits, int* nexact) {
+// first: this thread's entry of the table's first kThreads entries, read by
+// the caller (lut_entry) before its other loads.
+__device__ __forceinline__ int lut_entry(const AttnParams& p, int h, int t, int i) {
+  return i < p.C ? p.ids[((long long)h * p.T + t) * p.C + i] : -1;
+}
+
+__device__ void own_units(const AttnParams& p, int h, int t, int tid, int first, int* units, uint32_t* maskw,
+                          int* wcount, int* nunits, int* nexact) {
   const int lane = tid & 63, wave = tid >> 6;
   if (tid < 16) maskw[tid] = 0u;
   __syncthreads();
-  const int32_t* ids = p.ids + ((long long)h * p.T + t) * p.C;
   int base = 0;
   for (int i0 = 0; i0 < p.C; i0 += kThreads) {
-    const int i = i0 + tid;
-    const int pg = i < p.C ? ids[i] : -1;
+    const int pg = i0 == 0 ? first : lut_entry(p, h, t, i0 + tid);
     const bool ok = pg >= 0 && pg < p.P;
     const unsigned long long bal = __ballot(ok);
     if (lane == 0) wcount[wave] = __popcll(bal);
@@ -468,8 +472,11 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const int TB = p.T / NB;
   const int work = xcd_remap(blockIdx.x, p.H * TB);
   const int h = work / TB, t = (work % TB) * NB + grp;
-  // query operand: lane's query row, dims 16*st + 8*hh + [0,8); requested
-  // first so its latency overlaps the unit list
+  // the table entries first: the unit list waits for them alone, not for
+  // the query rows requested after them
+  const int first = NB == 1 ? lut_entry(p, h, t, tid) : -1;
+  // query operand: lane's query row, dims 16*st + 8*hh + [0,8); its latency
+  // overlaps the unit list
   const int r = lane & 31, hh = lane >> 5;
   const long long qrow = (long long)(t * 64 + qw * 32 + r);
   u32x4 qop[8];
@@ -477,7 +484,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
   for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st);
   if (NB == 1) {
-    own_units(p, h, t, tid, units, maskw, wcount, &nunits_s, &nexact_s);
+    own_units(p, h, t, tid, first, units, maskw, wcount, &nunits_s, &nexact_s);
   } else {
     // every page exact, no rep tiles: units are the pages in order
     for (int i = tid; i < p.P; i += kThreads * NB) units[i] = i;
