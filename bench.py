@@ -172,7 +172,8 @@ def main():
     import torch
     from streaming_sparse_amd import _lib, workload
     from streaming_sparse_amd.attention import Workspace
-    from streaming_sparse_amd.legacy_components import REP_OP_ELEMS, attention, kv_strides, rep_operands, rep_tiles
+    from streaming_sparse_amd.legacy_components import (REP_OP_ELEMS, attention, kv_strides, rep_operands, rep_tiles,
+                                                        split_workspace)
     from streaming_sparse_amd.route import route
 
     dev = torch.device("cuda:0")
@@ -206,10 +207,12 @@ def main():
     L = _lib.lib()
 
     def attn_only(flags):
+        split = split_workspace(ws, N, H, flags, dev)
         _lib.check(L.ssa_attention(_lib.ptr(g.q), _lib.ptr(g.k), _lib.ptr(g.v), _lib.ptr(g.summary.keys),
                                    _lib.ptr(g.summary.mean), _lib.ptr(basis), _lib.ptr(ops), _lib.ptr(ids),
                                    _lib.ptr(out), N, H, P, g.summary.head_pages, ops.shape[1], C, tok, head, flags,
-                                   _lib.stream_handle(dev)), "ssa_attention")
+                                   _lib.ptr(split), 0 if split is None else split.numel(), _lib.stream_handle(dev)),
+                   "ssa_attention")
 
     iters = max(10, args.steps)
     attn_ms = {name: time_loop(lambda f=f: attn_only(f), iters, stream) for name, f in (("two_term", 1),

@@ -71,11 +71,27 @@ int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, in
  * detail rows in the same arithmetic (two-term or one-term bf16 weights).
  * flags bit 1: the caller guarantees every row of ids lists each page of the
  * window exactly once (count == pages, a dense call); ids are then not read
- * and two query blocks share each K/V page load. */
+ * and two query blocks share each K/V page load.
+ * workspace: device memory of workspace_bytes >= ssa_attention_workspace_bytes
+ * (16-byte aligned; its contents on entry do not matter), the stand-in for
+ * the reference's Workspace (VR/attention.py:7-13).  With it, the (query
+ * block, head) tiles past the last multiple of the device's compute-unit
+ * count run as two pieces each, so the last round of tiles spreads over
+ * every CU, and a second kernel merges the pieces' states into out; NULL
+ * (or too small): every tile in one piece.  Results agree within the
+ * call's tolerance, not bit for bit, between the two; each is
+ * deterministic.  Calls that share a workspace must not overlap (one
+ * stream, or ordered). */
 int ssa_attention(const void* q, const void* k, const void* v, const void* keys, const void* mean, const void* basis,
                   const void* rep_ops, const int32_t* ids, void* out, int n_tokens, int heads, int pages,
                   int head_pages, int rep_tiles, int count, long long kv_token_stride, long long kv_head_stride,
-                  int flags, hipStream_t stream);
+                  int flags, void* workspace, long long workspace_bytes, hipStream_t stream);
+
+/* Bytes of the ssa_attention workspace for a call of n_tokens queries and
+ * heads heads with these flags on the current device (0: the call runs no
+ * split; -1: invalid shape or no device).  No counterpart in the reference:
+ * its Workspace allocates per call shape (VR/attention.py:7-13). */
+long long ssa_attention_workspace_bytes(int n_tokens, int heads, int flags);
 
 /* Router: risk [H,blocks,pages] fp32 and, unless mode == -1, the page table.
  * Probe rows: gathered=1 -> q is probes [H,blocks,16,128] addressed

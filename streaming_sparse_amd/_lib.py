@@ -14,9 +14,13 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssattn.s
 _lib = None
 
 _vp, _i, _ll, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float
+# return type of the entry points that do not return a status
+RESTYPES = {"ssa_attention_workspace_bytes": _ll}
 SIGNATURES = {
     "ssa_rep_operands": [_vp, _vp, _i, _i, _i, _i, _vp],
-    "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp],
+    "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp, _ll,
+                      _vp],
+    "ssa_attention_workspace_bytes": [_i, _i, _i],
     "ssa_route": [_vp, _ll, _ll, _ll, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
                   _vp, _vp, _i, _vp],
     "ssa_select": [_vp, _vp, _vp, _i, _i, _f, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
@@ -42,7 +46,7 @@ def lib():
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         _lib = handle
     return _lib
 

@@ -33,6 +33,8 @@
 // The two key halves are merged through LDS at the end.
 #include "common.h"
 
+#include <atomic>
+
 #include <type_traits>
 
 using namespace ssa;
@@ -63,7 +65,17 @@ struct AttnParams {
   long long q_tok, q_head;     // element strides of q / out
   int H, T, P, HP, RT, C;
   float scale_log2;            // log2(e) / sqrt(D)
+  // Tiles >= split_from (grid order) run as split_k pieces of their unit
+  // list, one workgroup each; a piece leaves its unnormalised state in
+  // part[(tile - split_from) * split_k + piece] for merge_kernel.
+  // split_from = H * T: no split.
+  float* part;
+  int split_from, split_k;
 };
+
+// Per piece of a split tile: O [qw][dt * 4 + j][64 lanes][4] fp32 (the
+// epilogue's lane layout), then m [qw][32] and l [qw][32].
+constexpr int kPieceFloats = 2 * 16 * 64 * 4 + 2 * 64;
 
 // K tile: 16-byte chunk c of row r at chunk c ^ (r & 15).
 __device__ __forceinline__ int k_off(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
@@ -470,7 +482,16 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave >> 2, pair = (wave >> 1) & 1, qw = wave & 1;
   const int TB = p.T / NB;
-  const int work = xcd_remap(blockIdx.x, p.H * TB);
+  // whole tiles first (XCD-grouped), then the pieces of the split tiles
+  int work, piece = 0, nparts = 1;
+  if (NB == 2 || (int)blockIdx.x < p.split_from) {
+    work = xcd_remap(blockIdx.x, NB == 2 ? p.H * TB : p.split_from);
+  } else {
+    const int b = blockIdx.x - p.split_from;
+    work = p.split_from + b / p.split_k;
+    piece = b % p.split_k;
+    nparts = p.split_k;
+  }
   const int h = work / TB, t = (work % TB) * NB + grp;
   // the table entries first: the unit list waits for them alone, not for
   // the query rows requested after them
@@ -491,7 +512,16 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     if (tid == 0) nunits_s = nexact_s = p.P;
   }
   __syncthreads();
-  const int nunits = nunits_s;
+  const int nunits = __builtin_amdgcn_readfirstlane(nunits_s);
+  // this workgroup's units [ibeg, iend): a piece of the list when split,
+  // starting at an even unit (so the slot of every step stays known at
+  // compile time).  A piece left empty (a list shorter than the pieces)
+  // walks unit ibeg and hands on an empty state instead (m = -inf, l = 0,
+  // O = 0).
+  const int ibeg = 2 * (nunits * piece / (2 * nparts));
+  const int inext = piece + 1 == nparts ? nunits : 2 * (nunits * (piece + 1) / (2 * nparts));
+  const bool empty = inext <= ibeg;
+  const int iend = empty ? ibeg + 1 : inext;
   lds_u8* const kbase = (lds_u8*)ring;
   lds_u8* const vbase = (lds_u8*)ring + 2 * kBuf;
   auto kslot = [&](int slot) { return kbase + slot * kBuf; };
@@ -510,21 +540,22 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const uint32_t det_off = kDetailOff + ((pair * 2 + hh) * 8 + (r & 7)) * 32;
   const uint32_t klane = k_base(pair, lane), vlane = v_base(pair, lane);
   auto unit = [&](int i) { return __builtin_amdgcn_readfirstlane(units[i]); };
-  // prologue: K0, V0, K1 in flight; S of unit 0 and its max
-  issue_rows<NB>(p, src, unit(0), 0, wave, lane, page_off, rep_off, kslot(0));
-  issue_rows<NB>(p, src, unit(0), 1, wave, lane, page_off, rep_off, vslot(0));
-  issue_rows<NB>(p, src, unit(min(1, nunits - 1)), 0, wave, lane, page_off, rep_off, kslot(1));
+  // prologue: K and V of unit ibeg, K of unit ibeg+1 in flight (unit i in
+  // slots i & 1); S of unit ibeg and its max
+  issue_rows<NB>(p, src, unit(ibeg), 0, wave, lane, page_off, rep_off, kslot(ibeg & 1));
+  issue_rows<NB>(p, src, unit(ibeg), 1, wave, lane, page_off, rep_off, vslot(ibeg & 1));
+  issue_rows<NB>(p, src, unit(min(ibeg + 1, iend - 1)), 0, wave, lane, page_off, rep_off, kslot((ibeg + 1) & 1));
   wait_loads();
   __syncthreads();
-  f32x16 S0 = s_tile(kslot(0), pair, lane, qop), S1;
+  f32x16 S0 = s_tile(kslot(ibeg & 1), pair, lane, qop), S1;
   float mloc;
-  float bias = unit_max(S0, unit(0), pair, lane, p.scale_log2, mloc);
+  float bias = unit_max(S0, unit(ibeg), pair, lane, p.scale_log2, mloc);
   update_max(mloc, m, L, ls, O, C);
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
   // Unit ids run ahead in registers (u0 = unit i); the id of unit i+3 is
   // read from LDS in step i-1, so the read completes at its barrier.
-  int u0 = unit(0), u1 = unit(min(1, nunits - 1)), u2 = unit(min(2, nunits - 1));
-  int u3raw = units[min(3, nunits - 1)];
+  int u0 = unit(ibeg), u1 = unit(min(ibeg + 1, iend - 1)), u2 = unit(min(ibeg + 2, iend - 1));
+  int u3raw = units[min(ibeg + 3, iend - 1)];
 
   // P.V of exact page i (probabilities of Sc, V slot cur), with S(i+1) from
   // the other K slot and its max.  K: the kind of units i+1 and i+2.
@@ -759,7 +790,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     u0 = u1;
     u1 = u2;
     u2 = u3;
-    u3raw = units[min(i + 4, nunits - 1)];
+    u3raw = units[min(i + 4, iend - 1)];
     wait_loads();
     __syncthreads();
   };
@@ -770,28 +801,28 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   using RepUnits = std::integral_constant<int, 1>;
   using AnyUnits = std::integral_constant<int, 2>;
   const int npages = nexact_s;
-  int i = 0;
-  for (; i + 2 < nunits && i + 3 < npages; i += 2) {
+  int i = ibeg;
+  for (; i + 2 < iend && i + 3 < npages; i += 2) {
     step(PageUnits{}, PageUnits{}, i, S0, S1);
     step(PageUnits{}, PageUnits{}, i + 1, S1, S0);
   }
-  for (; i + 2 < nunits && i + 1 < npages; i += 2) {
+  for (; i + 2 < iend && i + 1 < npages; i += 2) {
     step(PageUnits{}, AnyUnits{}, i, S0, S1);
     step(PageUnits{}, AnyUnits{}, i + 1, S1, S0);
   }
   if constexpr (NB == 1) {
     // here unit i+1 is a rep tile; unit i is the last page when npages is odd
-    if (i + 2 < nunits && i < npages) {
+    if (i + 2 < iend && i < npages) {
       step(PageUnits{}, RepUnits{}, i, S0, S1);
       step(RepUnits{}, RepUnits{}, i + 1, S1, S0);
       i += 2;
     }
-    for (; i + 2 < nunits; i += 2) {
+    for (; i + 2 < iend; i += 2) {
       step(RepUnits{}, RepUnits{}, i, S0, S1);
       step(RepUnits{}, RepUnits{}, i + 1, S1, S0);
     }
   }
-  // one unit with a successor left (units i and i+1 = nunits - 1): the same
+  // one unit with a successor left (units i and i+1 = iend - 1): the same
   // work without the interleaving, each kind chosen at run time
   auto unit_pv = [&](int cur, const f32x16& Sc, float nb) {
     bool rep = false;
@@ -805,7 +836,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       pv<PRECISE>(pb, pl, vslot(cur), pair, lane, L, O);
     }
   };
-  if (i + 1 < nunits) {
+  if (i + 1 < iend) {
     issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot((i + 1) & 1));
     S1 = s_tile(kslot((i + 1) & 1), pair, lane, qop);
     unit_pv(i & 1, S0, bias - (m == -INFINITY ? 0.0f : m));
@@ -863,9 +894,34 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const float mt = fmaxf(m, m1);
   const float mu = mt == -INFINITY ? 0.0f : mt;
   const float a0 = __builtin_amdgcn_exp2f(m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
-  const float inv = 1.0f / (l * a0 + l1 * a1);
+  const float lt = l * a0 + l1 * a1;
   const float* d = xo + qw * 4096 + lane;
-  uint16_t* op = p.out + qrow * p.q_tok + (long long)h * p.q_head + 4 * hh;
+  // the lane's query, dim half and query half, re-formed here so that no
+  // register holds them across the unit loop
+  int lq = tid;
+  asm volatile("" : "+v"(lq));
+  const int rq = lq & 31, hq = (lq >> 5) & 1, qq = (lq >> 6) & 1;
+  if (nparts > 1) {
+    // a piece: its unnormalised state (the two key halves merged) for
+    // merge_kernel, in this epilogue's lane layout
+    float* slot = p.part + (long long)((work - p.split_from) * nparts + piece) * kPieceFloats;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x4 po;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) po[c] = empty ? 0.0f : O[dt][4 * j + c] * a0 + d[(16 * dt + 4 * j + c) * 64] * a1;
+        *reinterpret_cast<f32x4*>(slot + ((qq * 16 + dt * 4 + j) * 64 + lq % 64) * 4) = po;
+      }
+    if (hq == 0) {
+      slot[8192 + qq * 32 + rq] = empty ? -INFINITY : mu;
+      slot[8256 + qq * 32 + rq] = empty ? 0.0f : lt;
+    }
+    return;
+  }
+  const float inv = 1.0f / lt;
+  uint16_t* op = p.out + (long long)(t * 64 + qq * 32 + rq) * p.q_tok + (long long)h * p.q_head + 4 * hq;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
@@ -879,6 +935,60 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   }
 }
 
+// The split tiles' output: block (s, qw, dh) merges the K pieces of tile
+// split_from + s for queries 32 qw .. 32 qw + 31 and dims 64 dh .. 64 dh + 63
+// (O = sum_j O_j 2^(m_j - M), l likewise, M = max_j m_j, in piece order) and
+// writes out = O / l.  Lane l holds the epilogue's lane layout; every load
+// is issued before the first use.
+template <int K>
+__global__ __launch_bounds__(64) void merge_kernel(const float* part, uint16_t* out, int split_from, int T,
+                                                   long long q_tok, long long q_head) {
+  const int lane = threadIdx.x, s = blockIdx.x >> 2, qw = (blockIdx.x >> 1) & 1, dh = blockIdx.x & 1;
+  const int r = lane & 31, hh = lane >> 5;
+  const int work = split_from + s;
+  const int h = work / T, t = work % T;
+  const float* slots = part + (long long)s * K * kPieceFloats;
+  float mj[K], lj[K];
+  f32x4 v[K][2][4];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const float* sj = slots + j * kPieceFloats;
+    mj[j] = sj[8192 + qw * 32 + r];
+    lj[j] = sj[8256 + qw * 32 + r];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        v[j][x][jj] = *reinterpret_cast<const f32x4*>(sj + ((qw * 16 + (2 * dh + x) * 4 + jj) * 64 + lane) * 4);
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < K; ++j) M = fmaxf(M, mj[j]);
+  f32x4 acc[2][4] = {};
+  float L = 0.0f;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const float a = __builtin_amdgcn_exp2f(mj[j] - M);
+    L += lj[j] * a;
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[x][jj][c] += v[j][x][jj][c] * a;
+  }
+  const float inv = 1.0f / L;
+  uint16_t* op = out + (long long)(t * 64 + qw * 32 + r) * q_tok + (long long)h * q_head + 4 * hh;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const u32x2 w = {pack_bf16(acc[x][jj][0] * inv, acc[x][jj][1] * inv),
+                       pack_bf16(acc[x][jj][2] * inv, acc[x][jj][3] * inv)};
+      *reinterpret_cast<u32x2*>(op + 32 * (2 * dh + x) + 8 * jj) = w;
+    }
+}
+
 // Detail operand tiles of one head per block row: rops[h, rt] for the
 // ceil(P/16) tiles of the window (96 chunks of 16 bytes each).
 __global__ __launch_bounds__(kRepOpChunks) void rep_operands_kernel(const uint16_t* detail, uint16_t* rops, int P,
@@ -888,9 +998,51 @@ __global__ __launch_bounds__(kRepOpChunks) void rep_operands_kernel(const uint16
   *reinterpret_cast<u32x4*>(rops + ((long long)h * RT + rt) * (kRepOpBytes / 2) + 8 * c) = w;
 }
 
+// Compute units of the current device (cached per device).
+int device_cus(int* out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cus[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return (int)e;
+    n = n > 0 ? n : 1;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  *out = n;
+  return (int)hipSuccess;
+}
+
+// The split a general call runs: the tiles past the last multiple of the
+// CU count (two per CU make the whole rounds) run as two pieces each, so
+// the last round spreads over every CU.  Returns the number of split tiles
+// (0: none) and the workspace bytes they need.
+int split_plan(int tiles, int* split_tiles, long long* bytes) {
+  int cus = 0;
+  const int e = device_cus(&cus);
+  if (e != (int)hipSuccess) return e;
+  const int r = tiles % cus;
+  *split_tiles = r;
+  *bytes = (long long)r * 2 * kPieceFloats * 4;
+  return (int)hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
+
+long long ssa_attention_workspace_bytes(int n_tokens, int heads, int flags) {
+  if (n_tokens <= 0 || n_tokens % 64 || heads <= 0) return -1;
+  if ((flags & 2) && (n_tokens / 64) % 2 == 0) return 0;
+  int r = 0;
+  long long bytes = 0;
+  if (split_plan(heads * (n_tokens / 64), &r, &bytes) != (int)hipSuccess) return -1;
+  return bytes;
+}
 
 int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, int head_pages, int rep_tiles,
                      hipStream_t stream) {
@@ -905,7 +1057,7 @@ int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, in
 int ssa_attention(const void* q, const void* k, const void* v, const void* keys, const void* mean, const void* basis,
                   const void* rep_ops, const int32_t* ids, void* out, int n_tokens, int heads, int pages,
                   int head_pages, int rep_tiles, int count, long long kv_token_stride, long long kv_head_stride,
-                  int flags, hipStream_t stream) {
+                  int flags, void* workspace, long long workspace_bytes, hipStream_t stream) {
   if (n_tokens <= 0 || n_tokens % 64 || heads <= 0 || pages <= 0 || pages > 512 || count <= 0 ||
       count > kMaxCount || count > pages || head_pages < pages)
     return (int)hipErrorInvalidValue;
@@ -939,6 +1091,9 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   p.RT = rep_tiles;
   p.C = count;
   p.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
+  p.part = nullptr;
+  p.split_from = heads * p.T;
+  p.split_k = 1;
   // a call whose caller states that every LUT row lists each page once
   // (flags bit 1: a dense call) runs, with an even number of blocks, two
   // blocks per workgroup on one shared K/V stream of pages 0..P-1; ids,
@@ -951,11 +1106,25 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
     else
       hipLaunchKernelGGL((attn_kernel<false, 2>), grid, dim3(2 * kThreads), 0, stream, p);
   } else {
-    const dim3 grid(heads * p.T);
+    // with a workspace of ssa_attention_workspace_bytes, the last tiles run
+    // as two pieces each
+    int r = 0;
+    long long need = 0;
+    const int e = split_plan(heads * p.T, &r, &need);
+    if (e != (int)hipSuccess) return e;
+    if (r > 0 && workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0) {
+      p.part = (float*)workspace;
+      p.split_from = heads * p.T - r;
+      p.split_k = 2;
+    }
+    const dim3 grid(p.split_from + (heads * p.T - p.split_from) * p.split_k);
     if (flags & 1)
       hipLaunchKernelGGL((attn_kernel<true, 1>), grid, dim3(kThreads), 0, stream, p);
     else
       hipLaunchKernelGGL((attn_kernel<false, 1>), grid, dim3(kThreads), 0, stream, p);
+    if (p.split_k > 1)
+      hipLaunchKernelGGL(merge_kernel<2>, dim3(4 * (heads * p.T - p.split_from)), dim3(64), 0, stream, p.part,
+                         p.out, p.split_from, p.T, p.q_tok, p.q_head);
   }
   return (int)hipGetLastError();
 }

@@ -79,8 +79,19 @@ the tail's _av at tuned_attention.py:16-18); True runs one bf16 product."""
 
 
 @torch.no_grad()
+def split_workspace(workspace, n_tokens, heads, flags, device):
+    """The attention call's split workspace from `workspace`, or None when
+    the call's tiles need no split: the tiles past the last multiple of the
+    device's CU count run as two pieces each, whose states a second kernel
+    merges."""
+    need = _lib.lib().ssa_attention_workspace_bytes(n_tokens, heads, flags)
+    if need < 0:
+        raise RuntimeError("ssa_attention_workspace_bytes failed")
+    return workspace.tensor('ssa_split', (need,), device, torch.uint8) if need > 0 else None
+
+
 def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None, all_pages=False,
-              rep_ops=None):
+              rep_ops=None, split=True):
     """Exact attention over the LUT pages + summary compensation + merge.
 
     q [1,N,H,128] bf16 contiguous; k, v [1,64P,H,128] bf16 (resident cache);
@@ -100,7 +111,9 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None
     share each K/V page load and ids are not read.  ``rep_ops``: the
     [H,>=ceil(P/16),512] detail operand tiles of `s` when the caller already
     has them (route(..., rep_out=...) writes them on the side); otherwise
-    they are computed here."""
+    they are computed here.  ``split=False`` runs every tile in one piece
+    (no split workspace; the tiles past the last multiple of the CU count
+    otherwise run as two pieces each)."""
     _, n, h, d = q.shape
     p = k.shape[1] // 64
     count = ids.shape[-1]
@@ -134,9 +147,12 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None
     out = buf('out', q.shape, q.dtype)
     single = SINGLE_AV if single_av is None else bool(single_av)
     flags = (0 if single else 1) | (2 if all_pages else 0)
+    split = split_workspace(workspace, n, h, flags, q.device) if split else None
     _lib.check(_lib.lib().ssa_attention(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(s.keys), _lib.ptr(s.mean),
                                         _lib.ptr(b), _lib.ptr(ops), _lib.ptr(ids), _lib.ptr(out), n, h, p, hp, ntiles,
-                                        count, tok, head, flags, _lib.stream_handle(q.device)), "ssa_attention")
+                                        count, tok, head, flags, _lib.ptr(split),
+                                        0 if split is None else split.numel(), _lib.stream_handle(q.device)),
+               "ssa_attention")
     return out
 
 

@@ -15,13 +15,13 @@ def declared():
     text = open(os.path.join(ROOT, "include", "ssattn.h")).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     out = {}
-    for m in re.finditer(r"\bint\s+(ssa_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int|long long)\s+(ssa_\w+)\s*\(([^)]*)\)\s*;", text):
         out[m.group(1)] = len([a for a in m.group(2).split(",") if a.strip()])
     return out
 
 
 def test_header_declares_entry_points():
-    assert set(declared()) == {"ssa_rep_operands", "ssa_attention", "ssa_route", "ssa_select", "ssa_encode", "ssa_pset",
+    assert set(declared()) == {"ssa_rep_operands", "ssa_attention", "ssa_attention_workspace_bytes", "ssa_route", "ssa_select", "ssa_encode", "ssa_pset",
                                "ssa_summary", "ssa_pset_noalloc", "ssa_anchor_rebase", "ssa_commit_pages",
                                "ssa_group_order"}
 

@@ -568,3 +568,50 @@ def test_attention_odd_window_and_slab(device, n):
         torch.cuda.synchronize()
         want = ref.selected_attention(q, k4.contiguous(), v4.contiguous(), sd, basis, ids).bfloat16()
         check_out(out, want, f"odd window n={n} count={count}")
+
+
+@pytest.mark.parametrize("single", [False, True])
+def test_attention_split_pieces(device, single):
+    """The last round of tiles as two pieces each (the 96 tiles past the
+    last multiple of the CU count at 12 x 72 tiles on a 256-CU device,
+    heads 10-11) merged by the second kernel: within the bar of the oracle
+    on blocks of split and whole tiles, within 1e-3 rel-L2 of the same call
+    run whole, and bit-identical over repeated calls."""
+    x = call_inputs(1, 18)
+    g = x.to(device)
+    ws = Workspace()
+    ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws)
+    a = attention(g.q, g.k, g.v, g.summary, g.basis, ids, ws, single_av=single).clone()
+    b = attention(g.q, g.k, g.v, g.summary, g.basis, ids, ws, single_av=single).clone()
+    whole = attention(g.q, g.k, g.v, g.summary, g.basis, ids, ws, single_av=single, split=False).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    err = ref.rel_l2(a.float().cpu(), whole.float().cpu())
+    print(f"split vs whole rel-L2 {err:.3e}", flush=True)
+    assert err <= 1e-3, err
+    tiles = [3, 50, 71]
+    want = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, ids.cpu(), tiles=tiles).bfloat16()
+    rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in tiles])
+    check_out(a[:, rows], want[:, rows], f"split pieces single={single}")
+
+
+def test_attention_split_short_lists(device):
+    """Unit lists shorter than two pieces: a 16-page window with one query
+    block per head, so every tile is split; a table of padding only (one rep
+    tile, no exact page: the first piece is empty) and a one-page table (one
+    exact page and one rep tile)."""
+    h, p = 2, 16
+    gen = torch.Generator().manual_seed(91)
+    q = torch.randn(1, 64, h, 128, generator=gen).bfloat16()
+    k = torch.randn(1, 64 * p, h, 128, generator=gen).bfloat16()
+    v = torch.randn(1, 64 * p, h, 128, generator=gen).bfloat16()
+    vp = v[0].transpose(0, 1).reshape(h, p, 64, 128)
+    basis = workload.pca_basis(vp.float())
+    s = workload.kmeans_summaries(k[0].transpose(0, 1).reshape(h, p, 64, 128), vp, basis,
+                                  torch.Generator().manual_seed(6))
+    gd = Summary(*(getattr(s, f).to(device) for f in Summary.FIELDS))
+    for table in (torch.full((h, 1, 1), -1, dtype=torch.int32), torch.tensor([[[5]], [[11]]], dtype=torch.int32)):
+        out = attention(q.to(device), k.to(device), v.to(device), gd, basis.to(device), table.to(device), Workspace())
+        torch.cuda.synchronize()
+        want = ref.selected_attention(q, k, v, s, basis, table).bfloat16()
+        check_out(out, want, f"short list {table.flatten().tolist()}")

@@ -128,7 +128,7 @@ def test_c_abi_rejects_bad_shapes():
     # ssa_attention: queries a multiple of 64, pages <= 512, count <= pages, K/V rows of 128 elements; the
     # general call needs page means, basis and ceil(pages/16) operand tiles, 16-byte aligned
     att = lambda n, pages, count, tok, mean=16, ops=16, tiles=27, flags=0: L.ssa_attention(
-        N, N, N, N, mean, 16, ops, N, N, n, 12, pages, pages, tiles, count, tok, 128, flags, N)
+        N, N, N, N, mean, 16, ops, N, N, n, 12, pages, pages, tiles, count, tok, 128, flags, N, 0, N)
     assert att(65, 432, 64, 1536) == INVALID
     assert att(4608, 513, 64, 1536) == INVALID
     assert att(4608, 432, 433, 1536) == INVALID
