@@ -74,11 +74,12 @@ int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, in
  * and two query blocks share each K/V page load.
  * workspace: device memory of workspace_bytes >= ssa_attention_workspace_bytes
  * (16-byte aligned; its contents on entry do not matter), the stand-in for
- * the reference's Workspace (VR/attention.py:7-13).  With it, the (query
- * block, head) tiles past the last multiple of the device's compute-unit
- * count run as two pieces each, so the last round of tiles spreads over
- * every CU, and a second kernel merges the pieces' states into out; NULL
- * (or too small): every tile in one piece.  Results agree within the
+ * the reference's Workspace (VR/attention.py:7-13).  With it, the
+ * workgroups past the last multiple of the device's compute-unit count run
+ * as pieces of their unit lists (two per (query block, head) tile in a
+ * general call, four per two-block workgroup in a dense one), so the last
+ * round spreads over every CU, and a second kernel merges the pieces'
+ * states into out; NULL (or too small): every workgroup in one piece.  Results agree within the
  * call's tolerance, not bit for bit, between the two; each is
  * deterministic.  Calls that share a workspace must not overlap (one
  * stream, or ordered). */

@@ -65,10 +65,11 @@ struct AttnParams {
   long long q_tok, q_head;     // element strides of q / out
   int H, T, P, HP, RT, C;
   float scale_log2;            // log2(e) / sqrt(D)
-  // Tiles >= split_from (grid order) run as split_k pieces of their unit
-  // list, one workgroup each; a piece leaves its unnormalised state in
-  // part[(tile - split_from) * split_k + piece] for merge_kernel.
-  // split_from = H * T: no split.
+  // Workgroups >= split_from (grid order; a workgroup holds NB tiles) run
+  // as split_k pieces of their unit list, one workgroup each; a piece leaves
+  // the unnormalised state of its tile g in
+  // part[((wg - split_from) * split_k + piece) * NB + g] for merge_kernel.
+  // split_from = H * T / NB: no split.
   float* part;
   int split_from, split_k;
 };
@@ -484,8 +485,8 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const int TB = p.T / NB;
   // whole tiles first (XCD-grouped), then the pieces of the split tiles
   int work, piece = 0, nparts = 1;
-  if (NB == 2 || (int)blockIdx.x < p.split_from) {
-    work = xcd_remap(blockIdx.x, NB == 2 ? p.H * TB : p.split_from);
+  if ((int)blockIdx.x < p.split_from) {
+    work = xcd_remap(blockIdx.x, p.split_from);
   } else {
     const int b = blockIdx.x - p.split_from;
     work = p.split_from + b / p.split_k;
@@ -904,7 +905,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   if (nparts > 1) {
     // a piece: its unnormalised state (the two key halves merged) for
     // merge_kernel, in this epilogue's lane layout
-    float* slot = p.part + (long long)((work - p.split_from) * nparts + piece) * kPieceFloats;
+    float* slot = p.part + (long long)(((work - p.split_from) * nparts + piece) * NB + grp) * kPieceFloats;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -935,24 +936,25 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   }
 }
 
-// The split tiles' output: block (s, qw, dh) merges the K pieces of tile
-// split_from + s for queries 32 qw .. 32 qw + 31 and dims 64 dh .. 64 dh + 63
-// (O = sum_j O_j 2^(m_j - M), l likewise, M = max_j m_j, in piece order) and
-// writes out = O / l.  Lane l holds the epilogue's lane layout; every load
-// is issued before the first use.
-template <int K>
+// The split tiles' output: block (s, qw, dh) merges the K pieces of split
+// tile s (tile g = s % NB of workgroup split_from + s / NB) for queries
+// 32 qw .. 32 qw + 31 and dims 64 dh .. 64 dh + 63 (O = sum_j O_j
+// 2^(m_j - M), l likewise, M = max_j m_j, in piece order) and writes
+// out = O / l.  Lane l holds the epilogue's lane layout; every load is
+// issued before the first use.
+template <int K, int NB>
 __global__ __launch_bounds__(64) void merge_kernel(const float* part, uint16_t* out, int split_from, int T,
                                                    long long q_tok, long long q_head) {
   const int lane = threadIdx.x, s = blockIdx.x >> 2, qw = (blockIdx.x >> 1) & 1, dh = blockIdx.x & 1;
   const int r = lane & 31, hh = lane >> 5;
-  const int work = split_from + s;
-  const int h = work / T, t = work % T;
-  const float* slots = part + (long long)s * K * kPieceFloats;
+  const int TB = T / NB, g = s % NB;
+  const int work = split_from + s / NB;
+  const int h = work / TB, t = (work % TB) * NB + g;
   float mj[K], lj[K];
   f32x4 v[K][2][4];
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    const float* sj = slots + j * kPieceFloats;
+    const float* sj = part + (long long)(((s / NB) * K + j) * NB + g) * kPieceFloats;
     mj[j] = sj[8192 + qw * 32 + r];
     lj[j] = sj[8256 + qw * 32 + r];
 #pragma unroll
@@ -1017,17 +1019,19 @@ int device_cus(int* out) {
   return (int)hipSuccess;
 }
 
-// The split a general call runs: the tiles past the last multiple of the
-// CU count (two per CU make the whole rounds) run as two pieces each, so
-// the last round spreads over every CU.  Returns the number of split tiles
-// (0: none) and the workspace bytes they need.
-int split_plan(int tiles, int* split_tiles, long long* bytes) {
+// The split a call runs: the workgroups past the last multiple of the CU
+// count run as pieces, so the last round spreads over every CU.  The
+// general call (NB = 1, two workgroups per CU) splits them in 2; the
+// two-block call (NB = 2, one per CU) in 4.  Returns the number of split
+// workgroups (0: none), the pieces per workgroup and the workspace bytes.
+int split_plan(int wgs, int nb, int* split_wgs, int* k, long long* bytes) {
   int cus = 0;
   const int e = device_cus(&cus);
   if (e != (int)hipSuccess) return e;
-  const int r = tiles % cus;
-  *split_tiles = r;
-  *bytes = (long long)r * 2 * kPieceFloats * 4;
+  const int r = wgs % cus;
+  *split_wgs = r;
+  *k = nb == 1 ? 2 : 4;
+  *bytes = (long long)r * *k * nb * kPieceFloats * 4;
   return (int)hipSuccess;
 }
 
@@ -1037,10 +1041,10 @@ extern "C" {
 
 long long ssa_attention_workspace_bytes(int n_tokens, int heads, int flags) {
   if (n_tokens <= 0 || n_tokens % 64 || heads <= 0) return -1;
-  if ((flags & 2) && (n_tokens / 64) % 2 == 0) return 0;
-  int r = 0;
+  const int nb = (flags & 2) && (n_tokens / 64) % 2 == 0 ? 2 : 1;
+  int r = 0, k = 1;
   long long bytes = 0;
-  if (split_plan(heads * (n_tokens / 64), &r, &bytes) != (int)hipSuccess) return -1;
+  if (split_plan(heads * (n_tokens / 64) / nb, nb, &r, &k, &bytes) != (int)hipSuccess) return -1;
   return bytes;
 }
 
@@ -1091,39 +1095,43 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   p.RT = rep_tiles;
   p.C = count;
   p.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
-  p.part = nullptr;
-  p.split_from = heads * p.T;
-  p.split_k = 1;
   // a call whose caller states that every LUT row lists each page once
   // (flags bit 1: a dense call) runs, with an even number of blocks, two
   // blocks per workgroup on one shared K/V stream of pages 0..P-1; ids,
   // page means, basis and operand tiles are then not read.  Without the
   // flag the LUT is walked as given.
+  const int nb = dense ? 2 : 1;
+  const int wgs = heads * p.T / nb;
+  p.part = nullptr;
+  p.split_from = wgs;
+  p.split_k = 1;
+  // with a workspace of ssa_attention_workspace_bytes, the workgroups past
+  // the last multiple of the CU count run as pieces, merged by merge_kernel
+  int r = 0, pieces = 1;
+  long long need = 0;
+  const int e = split_plan(wgs, nb, &r, &pieces, &need);
+  if (e != (int)hipSuccess) return e;
+  if (r > 0 && workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0) {
+    p.part = (float*)workspace;
+    p.split_from = wgs - r;
+    p.split_k = pieces;
+  }
+  const dim3 grid(p.split_from + (wgs - p.split_from) * p.split_k);
   if (dense) {
-    const dim3 grid(heads * p.T / 2);
     if (flags & 1)
       hipLaunchKernelGGL((attn_kernel<true, 2>), grid, dim3(2 * kThreads), 0, stream, p);
     else
       hipLaunchKernelGGL((attn_kernel<false, 2>), grid, dim3(2 * kThreads), 0, stream, p);
+    if (p.split_k > 1)
+      hipLaunchKernelGGL((merge_kernel<4, 2>), dim3(4 * 2 * (wgs - p.split_from)), dim3(64), 0, stream, p.part,
+                         p.out, p.split_from, p.T, p.q_tok, p.q_head);
   } else {
-    // with a workspace of ssa_attention_workspace_bytes, the last tiles run
-    // as two pieces each
-    int r = 0;
-    long long need = 0;
-    const int e = split_plan(heads * p.T, &r, &need);
-    if (e != (int)hipSuccess) return e;
-    if (r > 0 && workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0) {
-      p.part = (float*)workspace;
-      p.split_from = heads * p.T - r;
-      p.split_k = 2;
-    }
-    const dim3 grid(p.split_from + (heads * p.T - p.split_from) * p.split_k);
     if (flags & 1)
       hipLaunchKernelGGL((attn_kernel<true, 1>), grid, dim3(kThreads), 0, stream, p);
     else
       hipLaunchKernelGGL((attn_kernel<false, 1>), grid, dim3(kThreads), 0, stream, p);
     if (p.split_k > 1)
-      hipLaunchKernelGGL(merge_kernel<2>, dim3(4 * (heads * p.T - p.split_from)), dim3(64), 0, stream, p.part,
+      hipLaunchKernelGGL((merge_kernel<2, 1>), dim3(4 * (wgs - p.split_from)), dim3(64), 0, stream, p.part,
                          p.out, p.split_from, p.T, p.q_tok, p.q_head);
   }
   return (int)hipGetLastError();
