@@ -39,7 +39,7 @@ sys.path.insert(0, ROOT)
 # HBM bytes per attn_kernel launch of the base-tier call, keyed by (pages, exact pages, single-term P.V),
 # measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this bench (profiles/attn_kernel_base432_traffic.md):
 # 116.5 MB read + 14.2 MB written in either P.V arithmetic
-MEASURED_TRAFFIC = {(432, 64, False): 123.1e6, (432, 64, True): 123.1e6}
+MEASURED_TRAFFIC = {(432, 64, False): 158.7e6, (432, 64, True): 158.7e6}
 METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
