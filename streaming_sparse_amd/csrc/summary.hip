@@ -53,10 +53,32 @@ struct SumSmem {
 
 __device__ __forceinline__ int word(int t, int w) { return t * 64 + (w ^ ((t & 15) << 2)); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+// Butterfly reductions over the wave without the LDS crossbar.  Step o
+// (32, 16, 8, 4, 2, 1 in turn) combines lane l with lane l ^ o: the lane-half
+// swap and the row-pair swap return both operands of the pair, and for
+// o <= 8 a rotation of the 16-lane row by o reaches a lane that, after the
+// steps with the larger offsets, holds the value of lane l ^ o.  Each step
+// adds (or takes the max of) the same two values as a step over
+// __shfl_xor(v, o), so the results agree bit for bit.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(s[0]), __uint_as_float(s[1]));
+  }
+  {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(s[0]), __uint_as_float(s[1]));
+  }
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));   // row_ror:8
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));   // row_ror:4
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false)));   // row_ror:2
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false)));   // row_ror:1
   return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
 // Word `lane` of up to 4 member tokens of m (removed from m), 0 for absent
@@ -146,8 +168,7 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p) {
   }
   if (wave == 1) {
     vmax = sqrtf(((s.u.vnp[0][lane] + s.u.vnp[1][lane]) + s.u.vnp[2][lane]) + s.u.vnp[3][lane]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o));
+    vmax = wave_reduce(vmax, [](float a, float b) { return fmaxf(a, b); });
   }
   __syncthreads();
 
@@ -307,8 +328,11 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p) {
   e9 = wave_sum(e9);
   // [r, 0:8]: mean of the key variance over each 16-dim group (lanes 8g..8g+7)
   float gv = var0 + var1;
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) gv += __shfl_xor(gv, o);
+  // lanes l ^ 1, l ^ 2 (quad permutations), then l ^ 4 by the half-row mirror
+  // (lane l ^ 7, which holds the value of l ^ 4 after the first two steps)
+  gv += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(gv), 0xB1, 0xF, 0xF, false));
+  gv += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(gv), 0x4E, 0xF, 0xF, false));
+  gv += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(gv), 0x141, 0xF, 0xF, false));
   uint16_t* st = p.stats + (pg * 4 + r) * 12;
   if ((lane & 7) == 0) st[lane >> 3] = to_bf16(gv / 16.f);
   // [0, 11] = |mean v - bf16(mean v)|, [1, 11] = max token |v|, [2..3, 11] = 0
