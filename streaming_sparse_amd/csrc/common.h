@@ -100,6 +100,86 @@ __device__ __forceinline__ void dma_rows(const void* base, const uint32_t (&off)
   }
 }
 
+// Lane l's partner l ^ O (O = 32, 16, 8, 4, 2, 1) without the LDS
+// crossbar: the lane-half and row-pair swaps return both lanes of a pair, a
+// row rotation by 8 and the quad permutations are exact partners, and the
+// swizzle's xor mode covers 4.  Same values as __shfl_xor(v, O).
+__device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+template <int O>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  if constexpr (O == 32) {
+    const auto s = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane_id() & 32) ? s[0] : s[1];
+  } else if constexpr (O == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane_id() & 16) ? s[0] : s[1];
+  } else if constexpr (O == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);   // row_ror:8
+  } else if constexpr (O == 4) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x101F);                       // xor 4 in 32 lanes
+  } else if constexpr (O == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);    // quad_perm 2,3,0,1
+  } else {
+    static_assert(O == 1, "xor offsets 32, 16, 8, 4, 2, 1");
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);    // quad_perm 1,0,3,2
+  }
+}
+
+template <int O>
+__device__ __forceinline__ float xor_lane(float v) {
+  return __uint_as_float(xor_lane<O>(__float_as_uint(v)));
+}
+
+template <int O>
+__device__ __forceinline__ int xor_lane(int v) {
+  return (int)xor_lane<O>((uint32_t)v);
+}
+
+template <int O>
+__device__ __forceinline__ double xor_lane(double v) {
+  const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+  const uint32_t lo = xor_lane<O>((uint32_t)u), hi = xor_lane<O>((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// Butterfly over the wave (steps 32, 16, 8, 4, 2, 1) with a commutative op:
+// every lane ends with the reduction, bit for bit as over __shfl_xor.  The
+// swaps hand both lanes of a pair to op; for steps 8 .. 1 a rotation of the
+// 16-lane row reaches a lane that, after the larger steps, holds the value
+// of lane l ^ o (the values agree across the offsets already combined).
+template <int CTRL, typename T>
+__device__ __forceinline__ T rotate_row(T v) {
+  if constexpr (sizeof(T) == 8) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+  } else {
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  }
+}
+
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+  if constexpr (sizeof(T) == 8) {
+    v = op(v, xor_lane<32>(v));
+    v = op(v, xor_lane<16>(v));
+  } else {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = op(__builtin_bit_cast(T, (uint32_t)s32[0]), __builtin_bit_cast(T, (uint32_t)s32[1]));
+    const uint32_t w = __builtin_bit_cast(uint32_t, v);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    v = op(__builtin_bit_cast(T, (uint32_t)s16[0]), __builtin_bit_cast(T, (uint32_t)s16[1]));
+  }
+  v = op(v, rotate_row<0x128>(v));   // row_ror:8
+  v = op(v, rotate_row<0x124>(v));   // row_ror:4
+  v = op(v, rotate_row<0x122>(v));   // row_ror:2
+  v = op(v, rotate_row<0x121>(v));   // row_ror:1
+  return v;
+}
+
 // Detail operand tiles of the compensation.  A rep tile covers pages
 // 16 rt .. 16 rt + 15 of the window; its operand tile (kRepOpBytes) holds, for
 // each (pair, hh, rank) = the matrix-pipe A rows of one lane, the rank-`rank`

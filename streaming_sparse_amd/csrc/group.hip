@@ -225,9 +225,9 @@ __device__ __forceinline__ unsigned long long order_key(double s) {
 
 // Sum over the 8 lanes of a lane group (lanes 8q..8q+7).
 __device__ __forceinline__ double sum8(double x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
+  x += xor_lane<1>(x);
+  x += xor_lane<2>(x);
+  x += xor_lane<4>(x);
   return x;
 }
 

@@ -53,30 +53,6 @@ struct SumSmem {
 
 __device__ __forceinline__ int word(int t, int w) { return t * 64 + (w ^ ((t & 15) << 2)); }
 
-// Butterfly reductions over the wave without the LDS crossbar.  Step o
-// (32, 16, 8, 4, 2, 1 in turn) combines lane l with lane l ^ o: the lane-half
-// swap and the row-pair swap return both operands of the pair, and for
-// o <= 8 a rotation of the 16-lane row by o reaches a lane that, after the
-// steps with the larger offsets, holds the value of lane l ^ o.  Each step
-// adds (or takes the max of) the same two values as a step over
-// __shfl_xor(v, o), so the results agree bit for bit.
-template <typename Op>
-__device__ __forceinline__ float wave_reduce(float v, Op op) {
-  {
-    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = op(__uint_as_float(s[0]), __uint_as_float(s[1]));
-  }
-  {
-    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = op(__uint_as_float(s[0]), __uint_as_float(s[1]));
-  }
-  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));   // row_ror:8
-  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));   // row_ror:4
-  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false)));   // row_ror:2
-  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false)));   // row_ror:1
-  return v;
-}
-
 __device__ __forceinline__ float wave_sum(float v) {
   return wave_reduce(v, [](float a, float b) { return a + b; });
 }
