@@ -615,3 +615,28 @@ def test_attention_split_short_lists(device):
         torch.cuda.synchronize()
         want = ref.selected_attention(q, k, v, s, basis, table).bfloat16()
         check_out(out, want, f"short list {table.flatten().tolist()}")
+
+
+@pytest.mark.parametrize("blocks", [256, 257])
+def test_attention_split_boundary(device, blocks):
+    """Tile counts at the CU-count boundary (256 CUs): 256 tiles run whole,
+    257 split only the last tile into two pieces; both match the oracle on
+    the first, a middle and the last tiles."""
+    h, p = 1, 100
+    gen = torch.Generator().manual_seed(blocks)
+    n = 64 * blocks
+    q = torch.randn(1, n, h, 128, generator=gen).bfloat16()
+    k = torch.randn(1, 64 * p, h, 128, generator=gen).bfloat16()
+    v = torch.randn(1, 64 * p, h, 128, generator=gen).bfloat16()
+    vp = v[0].transpose(0, 1).reshape(h, p, 64, 128)
+    basis = workload.pca_basis(vp.float())
+    s = workload.kmeans_summaries(k[0].transpose(0, 1).reshape(h, p, 64, 128), vp, basis,
+                                  torch.Generator().manual_seed(8))
+    gd = Summary(*(getattr(s, f).to(device) for f in Summary.FIELDS))
+    ids = torch.stack([torch.randperm(p, generator=gen)[:15] for _ in range(blocks)]).reshape(h, blocks, 15).int()
+    out = attention(q.to(device), k.to(device), v.to(device), gd, basis.to(device), ids.to(device), Workspace())
+    torch.cuda.synchronize()
+    tiles = [0, blocks // 2, blocks - 1]
+    want = ref.selected_attention(q, k, v, s, basis, ids, tiles=tiles).bfloat16()
+    rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in tiles])
+    check_out(out[:, rows], want[:, rows], f"{blocks} tiles")
