@@ -160,7 +160,7 @@ def attn_flop(N, H, D, C, P):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; heads shard across GPUs without "
+        print(json.dumps({"error": "bench.py measures one GPU only; heads shard across GPUs without "
                                    "exchange, so run --gpus 1"}))
         sys.exit(2)
     if args.calibrate_copy:
