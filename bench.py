@@ -38,8 +38,9 @@ sys.path.insert(0, ROOT)
 
 # HBM bytes per attn_kernel launch of the base-tier call, keyed by (pages, exact pages, single-term P.V),
 # measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this bench (profiles/attn_kernel_base432_traffic.md):
-# 116.5 MB read + 14.2 MB written in either P.V arithmetic
-MEASURED_TRAFFIC = {(432, 64, False): 158.7e6, (432, 64, True): 158.7e6}
+# 139.8 MB read + 19.0 MB written by attn_kernel<true, 1> (the two-term headline; the figure leaves out
+# merge_kernel's 6.4 MB read and 1.5 MB written).  The single-term kernel was not measured: traffic null.
+MEASURED_TRAFFIC = {(432, 64, False): 158.7e6}
 METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
@@ -63,6 +64,9 @@ def parse():
     ap.add_argument("--cpu-sample-blocks", type=int, default=4)
     ap.add_argument("--headline-only", action="store_true",
                     help="only the headline call (for a profiler run whose kernel averages are the headline's)")
+    ap.add_argument("--staged", action="store_true",
+                    help="with --headline-only: the call's attention as two launches (exact pages, then the "
+                         "compensation) and a merge, so a profiler shows the stages apart")
     ap.add_argument("--chunk-only", action="store_true",
                     help="only the streaming chunk line (for a profiler run of the 30-layer chunk)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -101,11 +105,12 @@ def time_loop(fn, iters, stream):
     return a.elapsed_time(b) / iters
 
 
-def call_timings(g, P, C, single, steps, warmup, stream):
+def call_timings(g, P, C, single, steps, warmup, stream, staged=False):
     """One base-tier call (route + attention) timed over `steps` calls after
     `warmup`, then the kernels' average durations inside a call from HIP events
     recorded around each launch on its stream (a second pass of the same
-    calls, kept out of the timed region whose calls they would space out)."""
+    calls, kept out of the timed region whose calls they would space out).
+    Also returns the host's enqueue time per call over the timed calls."""
     import torch
     from streaming_sparse_amd.attention import Workspace
     from streaming_sparse_amd.legacy_components import REP_OP_ELEMS, attention, rep_tiles
@@ -124,7 +129,7 @@ def call_timings(g, P, C, single, steps, warmup, stream):
         ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False, rep_out=ops)
         if marks:
             marks[1].record(stream)
-        o = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, single_av=single, rep_ops=ops)
+        o = attention(g.q, g.k, g.v, g.summary, basis, ids, ws, single_av=single, rep_ops=ops, staged=staged)
         if marks:
             marks[2].record(stream)
         return o
@@ -135,8 +140,10 @@ def call_timings(g, P, C, single, steps, warmup, stream):
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
+    t0 = time.perf_counter()
     for _ in range(steps):
         step()
+    host_ms = (time.perf_counter() - t0) * 1e3 / steps
     end.record(stream)
     torch.cuda.synchronize()
     ms_call = start.elapsed_time(end) / steps
@@ -146,7 +153,7 @@ def call_timings(g, P, C, single, steps, warmup, stream):
     torch.cuda.synchronize()
     route_in = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
     attn_in = sum(m[1].elapsed_time(m[2]) for m in marks) / steps
-    return ms_call, route_in, attn_in
+    return ms_call, route_in, attn_in, host_ms
 
 
 def attn_flop(N, H, D, C, P):
@@ -187,16 +194,22 @@ def main():
     C = P * 15 // 100
     stream = torch.cuda.current_stream(dev)
     single = bool(args.single_av)
-    print(f"# headline: base tier P={P} C={C} single_av={single}", file=sys.stderr, flush=True)
-    ms_call, route_in_ms, attn_in_ms = call_timings(g, P, C, single, args.steps, args.warmup, stream)
-    log(f"headline call {ms_call:.4f} ms (attention kernel {attn_in_ms:.4f} ms)")
+    print(f"# headline: base tier P={P} C={C} single_av={single} staged={bool(args.staged)}", file=sys.stderr,
+          flush=True)
     if args.headline_only:
+        ms_call, route_in_ms, attn_in_ms, host_ms = call_timings(g, P, C, single, args.steps, args.warmup, stream,
+                                                                 staged=args.staged)
+        log(f"headline call {ms_call:.4f} ms (attention kernel {attn_in_ms:.4f} ms)")
         print(json.dumps({"metric": METRIC, "value": round(ms_call, 4), "unit": "ms", "headline_only": True,
                           "attention_kernel_ms": round(attn_in_ms, 4), "route_ms": round(route_in_ms, 4),
-                          "single_av": single}), flush=True)
+                          "host_enqueue_ms_per_call": round(host_ms, 4), "single_av": single,
+                          "staged": bool(args.staged)}), flush=True)
         return
 
-    # per-kernel timings back to back (same stream, same inputs), straight through the C ABI
+    # Per-kernel timings back to back (same stream, same inputs), straight through the C ABI, and the dense
+    # lines, before the headline: the GPU then runs the headline at its loaded clock.  Timed first in a
+    # fresh process, 5 warm-up and 20 timed calls of the headline read ~0.29 ms against ~0.25 ms once the
+    # GPU has been busy for a few hundred ms (its clocks ramp from idle); the host enqueues a call in ~0.055 ms.
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()
     ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
@@ -207,7 +220,7 @@ def main():
     L = _lib.lib()
 
     def attn_only(flags):
-        split = split_workspace(ws, N, H, flags, dev)
+        split = split_workspace(ws, N, H, P, C, flags, dev)
         _lib.check(L.ssa_attention(_lib.ptr(g.q), _lib.ptr(g.k), _lib.ptr(g.v), _lib.ptr(g.summary.keys),
                                    _lib.ptr(g.summary.mean), _lib.ptr(basis), _lib.ptr(ops), _lib.ptr(ids),
                                    _lib.ptr(out), N, H, P, g.summary.head_pages, ops.shape[1], C, tok, head, flags,
@@ -254,17 +267,22 @@ def main():
                 fn()
             dense_own[name] = time_loop(fn, max(5, iters // 5), stream)
 
-    # the same call in the other arithmetic, and the 216-page window (config 0)
-    other = not single
     log(f"dense: sdpa {dense_ms} ms, this kernel {dense_own}")
-    o_call, o_route_in, o_attn_in = call_timings(g, P, C, other, args.steps, args.warmup // 2, stream)
+    ms_call, route_in_ms, attn_in_ms, host_ms = call_timings(g, P, C, single, args.steps, args.warmup, stream)
+    log(f"headline call {ms_call:.4f} ms (attention kernel {attn_in_ms:.4f} ms, host enqueue {host_ms:.4f} ms)")
+
+    # the same call in the other arithmetic, staged, and the 216-page window (config 0)
+    other = not single
+    o_call, o_route_in, o_attn_in, _ = call_timings(g, P, C, other, args.steps, args.warmup // 2, stream)
+    st_call, st_route_in, st_attn_in, _ = call_timings(g, P, C, single, args.steps, args.warmup // 2, stream,
+                                                        staged=True)
     log(f"other arithmetic call {o_call:.4f} ms")
     x0 = workload.make_call(cfg=0, frames=9)
     g0 = x0.to(dev)
     P0, C0 = x0.pages, x0.pages * 15 // 100
     cfg0 = {}
     for name, sgl in (("two_term", False), ("single_term", True)):
-        c_ms, c_route, c_attn = call_timings(g0, P0, C0, sgl, args.steps, args.warmup // 2, stream)
+        c_ms, c_route, c_attn, _ = call_timings(g0, P0, C0, sgl, args.steps, args.warmup // 2, stream)
         e0, m0 = attn_flop(N, H, D, C0, P0)
         cfg0[name] = {"call_ms": round(c_ms, 4), "attention_kernel_ms": round(c_attn, 4),
                       "route_ms": round(c_route, 4),
@@ -273,6 +291,10 @@ def main():
 
     extra = {"other_arithmetic": {"single_av": other, "call_ms": round(o_call, 4),
                                   "attention_kernel_ms": round(o_attn_in, 4), "route_ms": round(o_route_in, 4)},
+             "staged": {"call_ms": round(st_call, 4), "attention_launches_ms": round(st_attn_in, 4),
+                        "note": "the headline call with its attention as exact-page launch + compensation "
+                                "launch + merge (the reference's kernel split); per-stage durations in a "
+                                "kernel trace"},
              "config0_p216_c32": cfg0}
     if not args.no_extra:
         extra.update(intersection_lines(args, dense_ms, iters))
@@ -316,6 +338,7 @@ def main():
                                f"{'single-term' if single else 'two-term (reference)'} bf16 P.V",
                    "tier": "base", "pages": P, "exact_pages": C, "heads": H, "queries": N, "head_dim": D,
                    "single_av": single},
+        "host_enqueue_ms_per_call": round(host_ms, 4),
         "breakdown_ms": {"route_and_rep_operands": round(route_in_ms, 4), "attention_kernel": round(attn_in_ms, 4),
                          "route_back_to_back": round(route_ms, 4),
                          "attention_back_to_back_two_term": round(attn_ms["two_term"], 4),

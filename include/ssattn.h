@@ -64,17 +64,29 @@ int ssa_rep_operands(const void* detail, void* rep_ops, int heads, int pages, in
  * ids [H,n_tokens/64,count] int32: page ids, own page first; entries
  * outside [0,pages) (the -1 padding of a shorter table, RV/ops.py:115) are
  * not read and select nothing; a page listed twice is attended twice.
- * flags bit 0: two-term bf16 P.V (hi + lo parts of each probability, the
- * reference's HIGH_PRECISION_AV / BF16_AV arithmetic,
- * LE/gap_exact_round_kernel.py:98-125, RV/tuned_attention.py:16-18);
- * clear: single-term bf16 P.V.  The compensation weighs the page means and
- * detail rows in the same arithmetic (two-term or one-term bf16 weights).
+ * flags bit 0: two-term bf16 products, the reference's HIGH_PRECISION_AV /
+ * bf16_av=True arithmetic: the exact pages' P.V as bf16(P) V + bf16(P -
+ * bf16(P)) V (LE/gap_exact_round_kernel.py:98-125), and in the compensation
+ * the page-mean weights and the Haar contrast weights each as hi + lo bf16
+ * parts against the bf16 mean and detail rows, as the tail's _av does
+ * (RV/tuned_attention.py:16-18,60-62); the rank-8 code then meets the bf16
+ * basis as a two-term bf16 product, where the reference's tail uses tf32x3
+ * (RV/tuned_attention.py:71).  Clear: one bf16 term for every one of these
+ * weights (single-term P.V).
  * flags bit 1: the caller guarantees every row of ids lists each page of the
  * window exactly once (count == pages, a dense call); ids are then not read
  * and two query blocks share each K/V page load.
+ * flags bit 2: staged call (not with bit 1): the exact pages of every tile
+ * in one launch, the compensation's rep tiles in a second, each leaving its
+ * unnormalised softmax state in the workspace, then the merge kernel -- the
+ * reference's split into an exact kernel, a tail and a merge
+ * (RV/tuned_attention.py:20-81); the stages then show as separate kernels in
+ * a profiler.  Needs the workspace (else hipErrorInvalidValue); results
+ * agree with the fused call within its tolerance, not bit for bit.
  * workspace: device memory of workspace_bytes >= ssa_attention_workspace_bytes
- * (16-byte aligned; its contents on entry do not matter), the stand-in for
- * the reference's Workspace (VR/attention.py:7-13).  With it, the
+ * of the same shape and flags (16-byte aligned; its contents on entry do
+ * not matter), the stand-in for the reference's Workspace
+ * (VR/attention.py:7-13).  With it, the
  * workgroups past the last multiple of the device's compute-unit count run
  * as pieces of their unit lists (two per (query block, head) tile in a
  * general call, four per two-block workgroup in a dense one), so the last
@@ -88,11 +100,14 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
                   int head_pages, int rep_tiles, int count, long long kv_token_stride, long long kv_head_stride,
                   int flags, void* workspace, long long workspace_bytes, hipStream_t stream);
 
-/* Bytes of the ssa_attention workspace for a call of n_tokens queries and
- * heads heads with these flags on the current device (0: the call runs no
- * split; -1: invalid shape or no device).  No counterpart in the reference:
- * its Workspace allocates per call shape (VR/attention.py:7-13). */
-long long ssa_attention_workspace_bytes(int n_tokens, int heads, int flags);
+/* Bytes of the ssa_attention workspace for a call of n_tokens queries,
+ * heads heads, a window of pages pages and count table entries per row, with
+ * these flags, on the current device (0: the call runs no split; -1:
+ * invalid shape or flags, or no device).  The call's path (two-block dense
+ * kernel, split, staged) follows from exactly these arguments, so the size
+ * and the call agree.  No counterpart in the reference: its Workspace
+ * allocates per call shape (VR/attention.py:7-13). */
+long long ssa_attention_workspace_bytes(int n_tokens, int heads, int pages, int count, int flags);
 
 /* Router: risk [H,blocks,pages] fp32 and, unless mode == -1, the page table.
  * Probe rows: gathered=1 -> q is probes [H,blocks,16,128] addressed
@@ -184,7 +199,14 @@ int ssa_encode(const void* keys, const void* mean, const void* detail, const voi
  * [n_heads,blocks,16,32] fp64 (illegal pairs -1e30) or NULL; stats [3]
  * int64 = (executed swaps, corrected rows, non-finite legal scores),
  * overwritten.
- * Requires 96 < pages <= 512 and pages - count >= 64. */
+ * Pools: per partition (history [24,pages-72), current [pages-72,pages)),
+ * up to 8 movable removes x 16 adds (VB/quota_pool.py:3-15,34-46); a
+ * 72-page window (the first chunk, VB/quota_pool.py:21-33): up to 8 movable
+ * removes (then the anchor pages other than own as stand-ins) x the first 16
+ * of 32 adds (the unselected pages by descending risk, then the selected
+ * pages in page order).
+ * Requires pages == 72 with 24 <= count <= 72, or 96 < pages <= 512 with
+ * pages - count >= 64. */
 int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
              int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
              const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,

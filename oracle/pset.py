@@ -11,7 +11,8 @@ Pipeline for the scoped heads of one call (VB/graph.py:169-210):
   readout    rp[16], beta per probe/page  (VR/page.py:17-21)
   log mass   lm = LSE_r z - LSE_{p,r} z   (VB/graph.py:181)
   center     approx - sum_p e^lm approx   (VB/graph.py:199-201)
-  pools      8 removes + 16 adds per partition, same-partition legality
+  pools      8 removes + 16 adds per partition, same-partition legality;
+             a 72-page window: 8 current removes x the top 16 adds
                                           (VB/quota_pool.py:3-46)
   scores     FP64 proxy gain per (remove, add), mean over probes
                                           (VR/scores.py:54-91)
@@ -111,10 +112,36 @@ def stratified_pool(risk, mask, own):
     return r, a, legal
 
 
+def first_chunk_pool(risk, mask, own):
+    """Pool of a 72-page window, where the anchor frame is the chunk's first
+    frame and every non-anchor page is current (VB/quota_pool.py:21-33).
+    Removes: the movable pages (selected, not an anchor, not own) by
+    ascending risk, at most 8, then the anchor pages other than own in page
+    order.  Adds: the unselected pages by descending risk, then the selected
+    pages in page order, 32 slots.  Legal: the movable removes x the first
+    16 add slots (whatever those hold).  Ties -> lower page."""
+    p = risk.shape[-1]
+    page = torch.arange(p)
+    movable = mask & (page >= ANCHORS) & (page != own[..., None])
+    by_risk = risk.masked_fill(~movable, torch.inf).sort(dim=-1, stable=True).indices
+    n_mov = movable.sum(-1, keepdim=True).clamp_max(8)
+    # anchor pages other than own, ascending (own, if an anchor, goes last)
+    stand_in = torch.where((page < ANCHORS) & (page != own[..., None]), page, p + page).sort(dim=-1).values
+    slot = torch.arange(16)
+    pad = stand_in.gather(-1, (slot - n_mov).clamp_min(0))
+    remove = torch.where(slot < n_mov, by_risk[..., :16], pad)
+    add = risk.masked_fill(mask, -torch.inf).sort(dim=-1, descending=True, stable=True).indices[..., :32]
+    legal = (slot < n_mov)[..., None] & (torch.arange(32) < 16)
+    return remove, add, legal
+
+
 def pool(risk, mask, own):
     """Stratified pool with slot padding (VB/quota_pool.py:32-46): invalid
     remove slot i -> anchor page i; invalid add slot j -> the j-th smallest page
-    that is neither selected nor a valid add.  Padded slots are never legal."""
+    that is neither selected nor a valid add.  Padded slots are never legal.
+    A 72-page window takes the first chunk's pool (first_chunk_pool)."""
+    if risk.shape[-1] == CURRENT:
+        return first_chunk_pool(risk, mask, own)
     r, a, legal = stratified_pool(risk, mask, own)
     valid_remove = mask.gather(-1, r) & (r != own[..., None])
     anchor = torch.arange(r.size(-1))

@@ -20,7 +20,7 @@ SIGNATURES = {
     "ssa_rep_operands": [_vp, _vp, _i, _i, _i, _i, _vp],
     "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp, _ll,
                       _vp],
-    "ssa_attention_workspace_bytes": [_i, _i, _i],
+    "ssa_attention_workspace_bytes": [_i, _i, _i, _i, _i],
     "ssa_route": [_vp, _ll, _ll, _ll, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
                   _vp, _vp, _i, _vp],
     "ssa_select": [_vp, _vp, _vp, _i, _i, _f, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],

@@ -17,8 +17,9 @@
 // are never formed: with w_pr its rep weights, its share of the numerator is
 //   sum_p a_p mean_p + (sum_{p,a} b_pa detail_pa) . basis^T,
 // a_p = sum_r w_pr, b_pa = sum_r HAAR[a,r] w_pr, so the tile costs one
-// 8-page product against the page means and two rank-8 products into a
-// per-query code accumulator, which meets the basis once at the end.
+// 8-page product against the page means and two (one bf16 term per weight)
+// or three (two terms) rank-8 products into a per-query code accumulator,
+// which meets the basis once at the end.
 //
 // Workgroup: 4 waves, 64 queries of one head.  Wave w: pair w/2 takes keys
 // 32*pair..32*pair+31 of every unit, queries 32*(w%2)..+31.  Per unit:
@@ -425,6 +426,9 @@ __device__ __forceinline__ int lut_entry(const AttnParams& p, int h, int t, int 
   return i < p.C ? p.ids[((long long)h * p.T + t) * p.C + i] : -1;
 }
 
+// STAGE 1 lists the exact pages only, STAGE 2 the rep tiles only (the two
+// launches of a staged call); STAGE 0 both.
+template <int STAGE>
 __device__ void own_units(const AttnParams& p, int h, int t, int tid, int first, int* units, uint32_t* maskw,
                           int* wcount, int* nunits, int* nexact) {
   const int lane = tid & 63, wave = tid >> 6;
@@ -440,7 +444,7 @@ __device__ void own_units(const AttnParams& p, int h, int t, int tid, int first,
     int off = base;
     for (int w = 0; w < wave; ++w) off += wcount[w];
     if (ok) {
-      units[off + __popcll(bal & ((1ull << lane) - 1ull))] = pg;
+      if (STAGE != 2) units[off + __popcll(bal & ((1ull << lane) - 1ull))] = pg;
       atomicOr(&maskw[pg >> 5], 1u << (pg & 31));
     }
     base += wcount[0] + wcount[1] + wcount[2] + wcount[3];
@@ -459,10 +463,11 @@ __device__ void own_units(const AttnParams& p, int h, int t, int tid, int first,
       live = drop != 0xffffu;
     }
     const unsigned long long bal = __ballot(live);
-    if (live) units[base + __popcll(bal & ((1ull << lane) - 1ull))] = rep_unit(lane, drop);
+    const int rbase = STAGE == 2 ? 0 : base;
+    if (STAGE != 1 && live) units[rbase + __popcll(bal & ((1ull << lane) - 1ull))] = rep_unit(lane, drop);
     if (lane == 0) {
-      *nunits = base + __popcll(bal);
-      *nexact = base;
+      *nunits = STAGE == 1 ? base : rbase + __popcll(bal);
+      *nexact = STAGE == 2 ? 0 : base;
     }
   }
 }
@@ -470,8 +475,14 @@ __device__ void own_units(const AttnParams& p, int h, int t, int tid, int first,
 // NB query blocks per workgroup (4 waves each).  NB = 1: the general call
 // (own page table, rep tiles).  NB = 2: a call that selects every page, so
 // both blocks walk the same units (pages 0..P-1) and share each K/V load.
-template <bool PRECISE, int NB>
+// STAGE (general call only): 0 walks every unit of a tile and writes out (or
+// a piece's state); 1 and 2 are the two launches of a staged call -- the
+// exact pages, then the compensation's rep tiles -- each leaving its state
+// in part[2 tile + STAGE - 1] for merge_kernel, the reference's split into
+// an exact kernel, a tail and a merge (RV/tuned_attention.py:20-81).
+template <bool PRECISE, int NB, int STAGE = 0>
 __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams p) {
+  static_assert(STAGE == 0 || NB == 1, "staged calls are general calls");
   // LDS ring: K rows of units i (slot i & 1) run two units ahead of use, V
   // rows one unit ahead.  Iteration i reads K slot (i+1)&1 and V slot i&1
   // while the loads of K unit i+2 and V unit i+1 land in the other slots.
@@ -485,7 +496,11 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   const int TB = p.T / NB;
   // whole tiles first (XCD-grouped), then the pieces of the split tiles
   int work, piece = 0, nparts = 1;
-  if ((int)blockIdx.x < p.split_from) {
+  if (STAGE != 0) {
+    work = xcd_remap(blockIdx.x, p.split_from);
+    piece = STAGE - 1;
+    nparts = 2;
+  } else if ((int)blockIdx.x < p.split_from) {
     work = xcd_remap(blockIdx.x, p.split_from);
   } else {
     const int b = blockIdx.x - p.split_from;
@@ -506,7 +521,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
   for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st);
   if (NB == 1) {
-    own_units(p, h, t, tid, first, units, maskw, wcount, &nunits_s, &nexact_s);
+    own_units<STAGE>(p, h, t, tid, first, units, maskw, wcount, &nunits_s, &nexact_s);
   } else {
     // every page exact, no rep tiles: units are the pages in order
     for (int i = tid; i < p.P; i += kThreads * NB) units[i] = i;
@@ -514,13 +529,22 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   }
   __syncthreads();
   const int nunits = __builtin_amdgcn_readfirstlane(nunits_s);
+  // the piece state's slot: tile (work - split_from) of the split ones, or
+  // every tile in a staged call
+  const long long pslot = (long long)(((work - (STAGE ? 0 : p.split_from)) * nparts + piece) * NB + grp) * kPieceFloats;
+  if (STAGE != 0 && nunits == 0) {
+    // no unit of this stage (a table that selects every page, or lists none
+    // in the window): the empty state m = -inf, l = 0, O = 0
+    for (int i = tid; i < kPieceFloats; i += kThreads) p.part[pslot + i] = i >= 8192 && i < 8256 ? -INFINITY : 0.0f;
+    return;
+  }
   // this workgroup's units [ibeg, iend): a piece of the list when split,
   // starting at an even unit (so the slot of every step stays known at
   // compile time).  A piece left empty (a list shorter than the pieces)
   // walks unit ibeg and hands on an empty state instead (m = -inf, l = 0,
   // O = 0).
-  const int ibeg = 2 * (nunits * piece / (2 * nparts));
-  const int inext = piece + 1 == nparts ? nunits : 2 * (nunits * (piece + 1) / (2 * nparts));
+  const int ibeg = STAGE ? 0 : 2 * (nunits * piece / (2 * nparts));
+  const int inext = (STAGE || piece + 1 == nparts) ? nunits : 2 * (nunits * (piece + 1) / (2 * nparts));
   const bool empty = inext <= ibeg;
   const int iend = empty ? ibeg + 1 : inext;
   lds_u8* const kbase = (lds_u8*)ring;
@@ -687,18 +711,18 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   // S(i+1) from the other K slot and its max.  Lane (query r, half hh) holds
   // the 4 reps of pair-local page 2 jp + hh in Sc[4 jp .. 4 jp + 3] (jp =
   // 0..3).
-  //  * contrasts: C += D^T B^T in 2 products; product mm takes, in k =
-  //    8 hh + j, the bf16 weight v = 8 mm + j of lane half hh's 12 (page,
-  //    contrast) pairs v = 3 jp + a (v >= 12: zero) against A rows =
-  //    detail[page][a][rank] (the operand tile);
+  //  * contrasts: C += D^T B^T; in k = 8 hh + j the products take bf16
+  //    weights of lane half hh's 12 (page, contrast) pairs v = 3 jp + a
+  //    against A rows = detail[page][a][rank] (the operand tile, whose two
+  //    chunks hold v = 0..7 and v = 8..11, 0..3).  Single-term path: 2
+  //    products, weights 0..7 and 8..11 (then zeros).  Two-term path (the
+  //    reference's _av(c_a, detail_a) on hi + lo parts): 3 products, hi
+  //    0..7; hi 8..11 with lo 0..3; lo 4..11 against the words of v = 4..11;
   //  * means: O^T += M^T A^T, one product per dim tile over the pair's 8
   //    pages, k = 8 hh + e holding page e < 4 ? 2 e : 2 e - 7, the lo parts
   //    of its mean weight in half 0 and the hi parts in half 1 (two-term
   //    path; one bf16 term, lo = 0, in the single-term path); M^T is read as
   //    the V operand of k step 0 from the mean rows the loads placed.
-  // The contrast weights take one bf16 term in both paths: the detail term is
-  // a small share of a rep's value, which the reference's tail rounds to
-  // bf16 as a whole.
   auto rep_body = [&](auto next_c, auto kind, int cur, const f32x16& Sc, f32x16& Sn, float nb) {
     constexpr bool NEXT = decltype(next_c)::value;
     constexpr int K = decltype(kind)::value;
@@ -731,11 +755,31 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       if (st & 1) haar4(hw + 4 * (st >> 1), hw + 4 * (st >> 1));
       __builtin_amdgcn_sched_barrier(0);
     }
-    // the two contrast products, each with its weights' packing and the reads
-    // of two mean operands
+    // the contrast products, each with its weights' packing and the reads of
+    // mean operands
     auto bw = [&](int v) { return hw[4 * (v / 3) + 1 + v % 3]; };
     auto wsplit = [&](float a, float b) { return PRECISE ? split_pair(a, b) : u32x2{pack_bf16(a, b), 0u}; };
-    {
+    if constexpr (PRECISE) {
+      u32x2 cw[6];   // hi | lo words of the weights v = 2k, 2k + 1
+#pragma unroll
+      for (int k = 0; k < 4; ++k) cw[k] = split_pair(bw(2 * k), bw(2 * k + 1));
+      const u32x4 b0 = {cw[0][0], cw[1][0], cw[2][0], cw[3][0]};
+      C = mfma32(dop[0], b0, C);
+      cw[4] = split_pair(bw(8), bw(9));
+      cw[5] = split_pair(bw(10), bw(11));
+      va[0] = v_read(vb, vl, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 b1 = {cw[4][0], cw[5][0], cw[0][1], cw[1][1]};
+      C = mfma32(dop[1], b1, C);
+      va[1] = v_read(vb, vl, 0, 1);
+      va[2] = v_read(vb, vl, 0, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 a2 = {dop[0][2], dop[0][3], dop[1][0], dop[1][1]};
+      const u32x4 b2 = {cw[2][1], cw[3][1], cw[4][1], cw[5][1]};
+      C = mfma32(a2, b2, C);
+      va[3] = v_read(vb, vl, 0, 3);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
       const u32x4 b0 = {pack_bf16(bw(0), bw(1)), pack_bf16(bw(2), bw(3)), pack_bf16(bw(4), bw(5)),
                         pack_bf16(bw(6), bw(7))};
       C = mfma32(dop[0], b0, C);
@@ -905,7 +949,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   if (nparts > 1) {
     // a piece: its unnormalised state (the two key halves merged) for
     // merge_kernel, in this epilogue's lane layout
-    float* slot = p.part + (long long)(((work - p.split_from) * nparts + piece) * NB + grp) * kPieceFloats;
+    float* slot = p.part + pslot;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -1035,13 +1079,27 @@ int split_plan(int wgs, int nb, int* split_wgs, int* k, long long* bytes) {
   return (int)hipSuccess;
 }
 
+// Flag bits of ssa_attention.
+constexpr int kTwoTerm = 1, kDense = 2, kStaged = 4;
+
+// Whether a call runs the two-block dense kernel: the caller's flag, a table
+// of every page and an even number of query blocks.
+bool dense_call(int flags, int count, int pages, int n_tokens) {
+  return (flags & kDense) && count == pages && (n_tokens / 64) % 2 == 0;
+}
+
+// Workspace bytes of a staged call: two piece states per tile.
+long long staged_bytes(int wgs) { return (long long)wgs * 2 * kPieceFloats * 4; }
+
 }  // namespace
 
 extern "C" {
 
-long long ssa_attention_workspace_bytes(int n_tokens, int heads, int flags) {
-  if (n_tokens <= 0 || n_tokens % 64 || heads <= 0) return -1;
-  const int nb = (flags & 2) && (n_tokens / 64) % 2 == 0 ? 2 : 1;
+long long ssa_attention_workspace_bytes(int n_tokens, int heads, int pages, int count, int flags) {
+  if (n_tokens <= 0 || n_tokens % 64 || heads <= 0 || pages <= 0 || count <= 0 || count > pages) return -1;
+  if ((flags & kStaged) && (flags & kDense)) return -1;
+  if (flags & kStaged) return staged_bytes(heads * (n_tokens / 64));
+  const int nb = dense_call(flags, count, pages, n_tokens) ? 2 : 1;
   int r = 0, k = 1;
   long long bytes = 0;
   if (split_plan(heads * (n_tokens / 64) / nb, nb, &r, &k, &bytes) != (int)hipSuccess) return -1;
@@ -1065,7 +1123,12 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   if (n_tokens <= 0 || n_tokens % 64 || heads <= 0 || pages <= 0 || pages > 512 || count <= 0 ||
       count > kMaxCount || count > pages || head_pages < pages)
     return (int)hipErrorInvalidValue;
-  const bool dense = (flags & 2) && count == pages && (n_tokens / 64) % 2 == 0;
+  const bool dense = dense_call(flags, count, pages, n_tokens);
+  const bool staged = (flags & kStaged) != 0;
+  // a staged call is a general call that needs the workspace for its states
+  if (staged && ((flags & kDense) || !workspace || workspace_bytes < staged_bytes(heads * (n_tokens / 64)) ||
+                 ((uintptr_t)workspace & 15)))
+    return (int)hipErrorInvalidValue;
   // the general call reads page means, the basis and the operand tiles (in
   // 16-byte rows)
   if (!dense && (rep_tiles < (pages + 15) / 16 || !mean || !basis || !rep_ops ||
@@ -1111,6 +1174,21 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   long long need = 0;
   const int e = split_plan(wgs, nb, &r, &pieces, &need);
   if (e != (int)hipSuccess) return e;
+  if (staged) {
+    // the exact pages of every tile, then the rep tiles of every tile, each
+    // launch leaving per-tile states; merge_kernel combines the two
+    p.part = (float*)workspace;
+    if (flags & kTwoTerm) {
+      hipLaunchKernelGGL((attn_kernel<true, 1, 1>), dim3(wgs), dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((attn_kernel<true, 1, 2>), dim3(wgs), dim3(kThreads), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((attn_kernel<false, 1, 1>), dim3(wgs), dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((attn_kernel<false, 1, 2>), dim3(wgs), dim3(kThreads), 0, stream, p);
+    }
+    hipLaunchKernelGGL((merge_kernel<2, 1>), dim3(4 * wgs), dim3(64), 0, stream, p.part, p.out, 0, p.T, p.q_tok,
+                       p.q_head);
+    return (int)hipGetLastError();
+  }
   if (r > 0 && workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0) {
     p.part = (float*)workspace;
     p.split_from = wgs - r;
@@ -1118,7 +1196,7 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
   }
   const dim3 grid(p.split_from + (wgs - p.split_from) * p.split_k);
   if (dense) {
-    if (flags & 1)
+    if (flags & kTwoTerm)
       hipLaunchKernelGGL((attn_kernel<true, 2>), grid, dim3(2 * kThreads), 0, stream, p);
     else
       hipLaunchKernelGGL((attn_kernel<false, 2>), grid, dim3(2 * kThreads), 0, stream, p);
@@ -1126,7 +1204,7 @@ int ssa_attention(const void* q, const void* k, const void* v, const void* keys,
       hipLaunchKernelGGL((merge_kernel<4, 2>), dim3(4 * 2 * (wgs - p.split_from)), dim3(64), 0, stream, p.part,
                          p.out, p.split_from, p.T, p.q_tok, p.q_head);
   } else {
-    if (flags & 1)
+    if (flags & kTwoTerm)
       hipLaunchKernelGGL((attn_kernel<true, 1>), grid, dim3(kThreads), 0, stream, p);
     else
       hipLaunchKernelGGL((attn_kernel<false, 1>), grid, dim3(kThreads), 0, stream, p);

@@ -186,8 +186,13 @@ __device__ __forceinline__ T wave_reduce(T v, Op op) {
 // element of detail[page][a] for the 12 (page, contrast) pairs that lane half
 // hh of key pair `pair` weighs: v = 3 jp + a, page 16 rt + 8 pair + 2 jp + hh
 // (jp = 0..3, a = 0..2), as two 16-byte chunks c = ((pair * 2 + hh) * 8 +
-// rank) * 2 + m, element j -> v = 8 m + j (v >= 12: zero), the A operands of
-// the two contrast products.  Pages >= P read zero.
+// rank) * 2 + m, element j -> v = (8 m + j) mod 12: chunk 0 holds v = 0..7,
+// chunk 1 v = 8..11 then 0..3.  These are the A operands of the contrast
+// products: with one bf16 term per weight, chunk 0 against weights 0..7 and
+// chunk 1 against weights 8..11 (zeros against its second half); with two
+// terms (hi + lo parts), chunk 0 against hi 0..7, chunk 1 against hi 8..11
+// and lo 0..3, and the words of v = 4..11 (second half of chunk 0, first half
+// of chunk 1) against lo 4..11.  Pages >= P read zero.
 constexpr int kRepOpBytes = 1024;
 constexpr int kRepOpChunks = kRepOpBytes / 16;
 
@@ -201,9 +206,9 @@ __device__ __forceinline__ u32x4 rep_operand_chunk(const uint16_t* det, int P, i
     uint32_t packed = 0;
 #pragma unroll
     for (int y = 0; y < 2; ++y) {
-      const int v = 8 * m + 2 * x + y, jp = v / 3, a = v % 3;
+      const int v = (8 * m + 2 * x + y) % 12, jp = v / 3, a = v % 3;
       const int pg = 16 * rt + 8 * pair + 2 * jp + hh;
-      const uint32_t val = (v < 12 && pg < P) ? (uint32_t)det[pg * 24 + a * 8 + rank] : 0u;
+      const uint32_t val = pg < P ? (uint32_t)det[pg * 24 + a * 8 + rank] : 0u;
       packed |= val << (16 * y);
     }
     out[x] = packed;

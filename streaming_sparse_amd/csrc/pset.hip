@@ -224,7 +224,12 @@ struct PoolSmem {
 // VB/quota_pool.py:3-46 from one descending bitonic sort of 512 keys whose
 // group field orders history removes > current removes > history adds >
 // current adds; removes rank by ascending risk, adds by descending risk,
-// ties -> lower page.
+// ties -> lower page.  A 72-page window (the anchor frame is the chunk's
+// first frame, every other page current: VB/quota_pool.py:21-33) has one
+// remove group and one add group: up to 8 movable removes, then the anchor
+// pages other than own; the unselected pages by descending risk, then the
+// selected pages in page order; the movable removes x the first 16 add
+// slots are legal.
 __global__ __launch_bounds__(256) void pset_pool_kernel(PsetParams p) {
   __shared__ PoolSmem s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -241,14 +246,19 @@ __global__ __launch_bounds__(256) void pset_pool_kernel(PsetParams p) {
   }
   if (tid < 4) s.cnt[tid] = 0;
   __syncthreads();
+  const bool first = P == kCurrent;
   for (int pg = tid; pg < kMaxPages; pg += 256) {
     unsigned long long key = 0ull;
-    if (pg >= kAnchors && pg < P) {
-      const int cur = pg >= P - kCurrent;
+    // a 72-page window counts every page in the history groups (4: removes,
+    // 2: adds), so its removes and adds each form one contiguous run; its
+    // adds range over all pages (an anchor page is selected in every mask
+    // the router writes)
+    if ((pg >= kAnchors || first) && pg < P) {
+      const int cur = first ? 0 : pg >= P - kCurrent;
       const uint32_t ord = orderable(s.risk[pg]);
       int group = 0;
       uint32_t kv = 0;
-      if (s.sel[pg] && pg != own) {
+      if (s.sel[pg] && pg != own && pg >= kAnchors) {
         group = cur ? 3 : 4;
         kv = ~ord;
       } else if (!s.sel[pg]) {
@@ -277,6 +287,37 @@ __global__ __launch_bounds__(256) void pset_pool_kernel(PsetParams p) {
   }
   const int nmh = s.cnt[0], nmc = s.cnt[1], nuh = s.cnt[2], nuc = s.cnt[3];
   auto page_at = [&](int i) -> int { return 1023 - (int)(s.key[i] & 1023ull); };
+  if (first) {
+    // the selected pages in page order fill the add slots past the unselected ones
+    if (wave == 0) {
+      int cnt = 0;
+      for (int base = 0; base < P; base += 64) {
+        const int pg = base + lane;
+        const bool on = pg < P && s.sel[pg];
+        const unsigned long long bal = __ballot(on);
+        const int r = cnt + __popcll(bal & ((1ull << lane) - 1ull));
+        if (on && r < 32) s.spare[r] = pg;
+        cnt += __popcll(bal);
+      }
+    }
+    __syncthreads();
+    if (tid < kCand) {
+      const int sl = tid, used = min(nmh, 8);
+      int page;
+      if (sl < 16) {
+        // the anchor pages other than own, in page order, stand in past the movable removes
+        const int a = sl - used;
+        page = sl < used ? page_at(sl) : a + (own < kAnchors && a >= own ? 1 : 0);
+      } else {
+        const int k = sl - 16;
+        page = k < nuh ? page_at(nmh + k) : s.spare[k - nuh];
+      }
+      int32_t* po = p.pool + ((long long)hs * p.T + t) * kPoolInts;
+      po[sl] = page;
+      if (sl < 16) po[kCand + sl] = sl < used ? 0xffff : 0;
+    }
+    return;
+  }
   // valid adds, then spare pages (neither selected nor a valid add), ascending
   if (tid < 32) {
     const int q = tid >> 4, k = tid & 15;
@@ -328,7 +369,8 @@ constexpr int kRowPart = 52;       // accH[16], accT[16], accB[16], sH, sT, sB, 
 
 struct RowsSmem {
   uint8_t sel[2][kMaxPages];
-  int8_t slot[2][kMaxPages];
+  int8_t slot[2][kMaxPages];       // remove slot (0..15) of a pool page, or -1
+  int8_t aslot[2][kMaxPages];      // add slot (16..47), or -1: a 72-page pool may list a page in both
   float u[32][8];
   float L[32];
   alignas(16) float coef[4][8][128];     // per-wave staging of a tile's 8 pages (fp32)
@@ -359,13 +401,14 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
     const int tb = min(t0 + b, p.T - 1);
     s.sel[b][pg] = p.mask[((long long)h * p.T + tb) * P + pg] ? 1 : 0;
     s.slot[b][pg] = -1;
+    s.aslot[b][pg] = -1;
   }
   __syncthreads();
   if (tid < 2 * kCand) {
     const int b = tid / kCand, sl = tid % kCand;
     const int tb = min(t0 + b, p.T - 1);
     const int page = p.pool[((long long)hs * p.T + tb) * kPoolInts + sl];
-    if (page >= 0 && page < P) s.slot[b][page] = (int8_t)sl;
+    if (page >= 0 && page < P) (sl < 16 ? s.slot : s.aslot)[b][page] = (int8_t)sl;
   }
   // reader query u = Wq . probe (fp32) and the probe LSE from the router
   {
@@ -501,7 +544,8 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
       }
       const double beta = (double)val[16];
       const bool sel = s.sel[blk][page];
-      const int sl = s.slot[blk][page];
+      const int sl = s.slot[blk][page], sa = s.aslot[blk][page];
+      const bool bg = sl < 0 && sa < 0;      // a background page: in no pool slot
       const double le = lm + beta;
       const double lg = sel ? le : lm;
       lmax = fmax(lmax, lg);
@@ -509,12 +553,17 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
       const double et = (double)__builtin_amdgcn_exp2f((float)le * kLog2e);
       sH += ex;
       sT += et;
-      if (sl < 0) sB += ex;
+      if (bg) sB += ex;
       const double* md = mw + pl * 64;
       double* cd = (sl >= 0 && blk < nrow) ? p.cand + (row_id * kCand + sl) * kCandVals : nullptr;
+      double* ca = (sa >= 0 && blk < nrow) ? p.cand + (row_id * kCand + sa) * kCandVals : nullptr;
       if (cd) {
         cd[0] = lm;
         cd[1] = beta;
+      }
+      if (ca) {
+        ca[0] = lm;
+        ca[1] = beta;
       }
       const double d0 = c0, d1 = c1, d2 = cc2;
 #pragma unroll
@@ -524,10 +573,14 @@ __global__ __launch_bounds__(256) void pset_rows_kernel(PsetParams p) {
         const double cur = sel ? ap + rp : ap;
         accH[e] += ex * cur;
         accT[e] += et * (ap + rp);
-        if (sl < 0) accB[e] += ex * cur;
+        if (bg) accB[e] += ex * cur;
         if (cd) {
           cd[2 + e] = ap;
           cd[18 + e] = rp;
+        }
+        if (ca) {
+          ca[2 + e] = ap;
+          ca[18 + e] = rp;
         }
       }
     }
@@ -893,8 +946,12 @@ int pset_launch(const void* q, long long q_head_stride, long long q_block_stride
                 uint8_t* mask, int32_t* ids, const int32_t* own, const int32_t* heads, int n_heads, double* cand,
                 double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
                 int total_heads, int blocks, int pages, int count, hipStream_t stream) {
-  if (n_heads <= 0 || n_heads > total_heads || blocks <= 0 || pages > kMaxPages || pages <= kAnchors + kCurrent ||
-      head_pages < pages || enc_pages < pages || count < 1 || count > pages || pages - count < 64 ||
+  // a 72-page window (the first chunk) or a window beyond the anchor frame
+  // and the current chunk with at least 64 unselected pages
+  const bool first = pages == kCurrent;
+  if (n_heads <= 0 || n_heads > total_heads || blocks <= 0 || pages > kMaxPages ||
+      (!first && (pages <= kAnchors + kCurrent || pages - count < 64)) || head_pages < pages ||
+      enc_pages < pages || count < (first ? kAnchors : 1) || count > pages ||
       heads == nullptr || probe_lse == nullptr || cand == nullptr || rows == nullptr || pool == nullptr ||
       gain == nullptr || info == nullptr || stats == nullptr)
     return (int)hipErrorInvalidValue;

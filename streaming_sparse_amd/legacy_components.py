@@ -17,16 +17,26 @@ from .ops import Summary
 HEAD_DIM = 128
 
 
+_SUMMARY_INNER = (('keys', (4, HEAD_DIM)), ('mean', (HEAD_DIM,)), ('detail', (3, 8)), ('stats', (4, 12)))
+
+
 def _check_summary(s: Summary, h: int, p: int):
+    """Head-page capacity of the summary slab after checking that each field
+    is a bf16 [H, >=p, ...] page slice of a contiguous [H, Pcap, ...] slab
+    (shape and stride arithmetic only: no tensor views are built)."""
     hp = s.head_pages
-    d = HEAD_DIM
-    for name, t, inner in (('keys', s.keys, 4 * d), ('mean', s.mean, d), ('detail', s.detail, 24),
-                           ('stats', s.stats, 48)):
+    for name, inner in _SUMMARY_INNER:
+        t = getattr(s, name)
         if t.dtype != torch.bfloat16:
             raise TypeError(f"summary.{name} must be bf16")
-        if t.shape[0] != h or t.shape[1] < p:
-            raise ValueError(f"summary.{name} shape {tuple(t.shape)} does not cover {h} heads x {p} pages")
-        if t.stride(0) != hp * inner or t[0, 0].numel() != inner or not t[0].is_contiguous():
+        shape, stride = t.shape, t.stride()
+        if shape[0] != h or shape[1] < p:
+            raise ValueError(f"summary.{name} shape {tuple(shape)} does not cover {h} heads x {p} pages")
+        want = [1] * len(inner)
+        for i in range(len(inner) - 2, -1, -1):
+            want[i] = want[i + 1] * inner[i + 1]
+        n = want[0] * inner[0]
+        if tuple(shape[2:]) != inner or list(stride[2:]) != want or stride[1] != n or stride[0] != hp * n:
             raise ValueError(f"summary.{name} must be a page slice of a contiguous [H,{hp},...] slab")
     return hp
 
@@ -78,20 +88,28 @@ each probability, HIGH_PRECISION_AV=not SINGLE_AV at legacy_components.py:49;
 the tail's _av at tuned_attention.py:16-18); True runs one bf16 product."""
 
 
+_WORKSPACE_BYTES = {}
+
+
 @torch.no_grad()
-def split_workspace(workspace, n_tokens, heads, flags, device):
-    """The attention call's split workspace from `workspace`, or None when
-    the call's tiles need no split: the tiles past the last multiple of the
-    device's CU count run as two pieces each, whose states a second kernel
-    merges."""
-    need = _lib.lib().ssa_attention_workspace_bytes(n_tokens, heads, flags)
-    if need < 0:
-        raise RuntimeError("ssa_attention_workspace_bytes failed")
+def split_workspace(workspace, n_tokens, heads, pages, count, flags, device):
+    """The attention call's workspace from `workspace`, or None when the call
+    needs none: the tiles past the last multiple of the device's CU count
+    run as pieces whose states a second kernel merges, and a staged call
+    (flags bit 2) keeps two states per tile.  The size is asked of the
+    library once per (shape, flags, device)."""
+    key = (n_tokens, heads, pages, count, flags, device)
+    need = _WORKSPACE_BYTES.get(key)
+    if need is None:
+        need = _lib.lib().ssa_attention_workspace_bytes(n_tokens, heads, pages, count, flags)
+        if need < 0:
+            raise RuntimeError("ssa_attention_workspace_bytes failed")
+        _WORKSPACE_BYTES[key] = need
     return workspace.tensor('ssa_split', (need,), device, torch.uint8) if need > 0 else None
 
 
 def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None, all_pages=False,
-              rep_ops=None, split=True):
+              rep_ops=None, split=True, staged=False):
     """Exact attention over the LUT pages + summary compensation + merge.
 
     q [1,N,H,128] bf16 contiguous; k, v [1,64P,H,128] bf16 (resident cache);
@@ -102,18 +120,24 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None
 
     Arithmetic: every probability multiplies V as the two-term bf16 product
     hi + lo, the reference's exact stage; the compensation weighs the page
-    means and the detail rows (through the bf16 basis) with two-term weights,
-    its ``bf16_av=True`` tail; ``bf16_av=False`` (the reference's tf32x3 tail)
+    means and the Haar contrasts of the detail rows with two-term (hi + lo)
+    bf16 weights, as the reference's ``bf16_av=True`` tail does
+    (tuned_attention.py:16-18,60-62), and applies the rank-8 code to the
+    bf16 basis as a two-term bf16 product (the reference: tf32x3,
+    tuned_attention.py:71).  ``bf16_av=False`` (the reference's tf32x3 tail)
     maps to the same two-term products, the closest this kernel runs.
     ``single_av=True`` (default: the module's SINGLE_AV) opts into one bf16
-    product over the exact pages.  ``all_pages=True`` states that every row
+    term for every probability and weight.  ``all_pages=True`` states that every row
     of ids lists each page exactly once (a dense call): two query blocks then
     share each K/V page load and ids are not read.  ``rep_ops``: the
     [H,>=ceil(P/16),512] detail operand tiles of `s` when the caller already
     has them (route(..., rep_out=...) writes them on the side); otherwise
     they are computed here.  ``split=False`` runs every tile in one piece
     (no split workspace; the tiles past the last multiple of the CU count
-    otherwise run as two pieces each)."""
+    otherwise run as two pieces each).  ``staged=True`` runs the exact pages
+    and the compensation as two launches whose states a merge kernel
+    combines (the reference's exact kernel + tail + merge), so a profiler
+    shows the two stages apart; not with ``all_pages``."""
     _, n, h, d = q.shape
     p = k.shape[1] // 64
     count = ids.shape[-1]
@@ -146,8 +170,10 @@ def attention(q, k, v, s, basis, ids, workspace, *, bf16_av=True, single_av=None
         ntiles = ops.shape[1]
     out = buf('out', q.shape, q.dtype)
     single = SINGLE_AV if single_av is None else bool(single_av)
-    flags = (0 if single else 1) | (2 if all_pages else 0)
-    split = split_workspace(workspace, n, h, flags, q.device) if split else None
+    if staged and all_pages:
+        raise ValueError("a staged call is a general call (not all_pages)")
+    flags = (0 if single else 1) | (2 if all_pages else 0) | (4 if staged else 0)
+    split = split_workspace(workspace, n, h, p, count, flags, q.device) if (split or staged) else None
     _lib.check(_lib.lib().ssa_attention(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(s.keys), _lib.ptr(s.mean),
                                         _lib.ptr(b), _lib.ptr(ops), _lib.ptr(ids), _lib.ptr(out), n, h, p, hp, ntiles,
                                         count, tok, head, flags, _lib.ptr(split),

@@ -235,11 +235,22 @@ class StreamRuntime:
         return out
 
     def quota(self, chunk: int):
+        """(A [steps, layers-1, H] int32 on the device, A+B per (step, layer)
+        as host ints) of a chunk.  Chunks 0 and 1 (windows of 72 and 144
+        pages, sparse only when listed in sparse_start_chunks) take the
+        reference's fixed quotas n = 4 / 12 with A = 4 / 7 for every call
+        (VB/queue_policy.py:25-28); later chunks a seeded table."""
         if chunk not in self.quotas:
             for done in [c for c in self.quotas if c < chunk - 1]:
                 del self.quotas[done]
-            tab = workload.quota_table(self.cfg.seed, layers=max(self.cfg.layers - 1, 1), steps=self.cfg.steps,
-                                       heads=self.H, mean_total=self.cfg.quota_mean, window=chunk)
+            if chunk < 2:
+                a, n = (4, 7)[chunk], (4, 12)[chunk]
+                tab = torch.empty(self.cfg.steps, max(self.cfg.layers - 1, 1), self.H, 2, dtype=torch.int64)
+                tab[..., 0] = a
+                tab[..., 1] = n - a
+            else:
+                tab = workload.quota_table(self.cfg.seed, layers=max(self.cfg.layers - 1, 1), steps=self.cfg.steps,
+                                           heads=self.H, mean_total=self.cfg.quota_mean, window=chunk)
             # pinned staging: the copy does not wait for the stream's earlier work
             cur = tab[..., 0].to(torch.int32).pin_memory().to(self.device, non_blocking=True)
             self.quotas[chunk] = (cur, tab[..., 0, :].sum(-1).tolist())

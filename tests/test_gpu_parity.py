@@ -200,8 +200,8 @@ def operand_tiles(detail, pages):
     """The detail operand tiles [H, ceil(P/16), 512] that ssa_rep_operands
     documents, restated with index arithmetic on the CPU: element j of chunk
     ((pair*2 + hh)*8 + rank)*2 + m of tile rt is detail[page, a, rank] with
-    v = 8m + j, page = 16 rt + 8 pair + 2 (v // 3) + hh, a = v % 3, and 0
-    for v >= 12 or pages >= P."""
+    v = (8m + j) mod 12, page = 16 rt + 8 pair + 2 (v // 3) + hh, a = v % 3,
+    and 0 for pages >= P."""
     h = detail.shape[0]
     tiles = (pages + 15) // 16
     out = torch.zeros(h, tiles, 2, 2, 8, 2, 8, dtype=torch.bfloat16)
@@ -210,9 +210,9 @@ def operand_tiles(detail, pages):
             for hh in range(2):
                 for m in range(2):
                     for j in range(8):
-                        v = 8 * m + j
+                        v = (8 * m + j) % 12
                         pg = 16 * rt + 8 * pair + 2 * (v // 3) + hh
-                        if v < 12 and pg < pages:
+                        if pg < pages:
                             out[:, rt, pair, hh, :, m, j] = detail[:, pg, v % 3, :]
     return out.reshape(h, tiles, 512)
 
@@ -640,3 +640,52 @@ def test_attention_split_boundary(device, blocks):
     want = ref.selected_attention(q, k, v, s, basis, ids, tiles=tiles).bfloat16()
     rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in tiles])
     check_out(out[:, rows], want[:, rows], f"{blocks} tiles")
+
+
+@pytest.mark.parametrize("single", [False, True])
+def test_attention_staged(device, single):
+    """A staged call (the exact pages of every tile in one launch, the
+    compensation's rep tiles in a second, then the merge): within the bar of
+    the oracle at 432 pages on 8 spread blocks, close to the fused call
+    (two-term: 1e-3 rel-L2; single-term 4e-3: each rounds its probabilities
+    to one bf16 term relative to its own running maximum, which differs
+    between the stages and the fused walk), and bit-identical over repeated
+    calls."""
+    x = call_inputs(1, 18)
+    g = x.to(device)
+    ws = Workspace()
+    ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', own=g.own, workspace=ws)
+    a = attention(g.q, g.k, g.v, g.summary, g.basis, ids, ws, single_av=single, staged=True).clone()
+    b = attention(g.q, g.k, g.v, g.summary, g.basis, ids, ws, single_av=single, staged=True).clone()
+    fused = attention(g.q, g.k, g.v, g.summary, g.basis, ids, ws, single_av=single).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    err = ref.rel_l2(a.float().cpu(), fused.float().cpu())
+    print(f"staged vs fused rel-L2 {err:.3e}", flush=True)
+    assert err <= (4e-3 if single else 1e-3), err
+    want = ref.selected_attention(x.q, x.k, x.v, x.summary, x.basis, ids.cpu(), tiles=TILES8).bfloat16()
+    rows = tile_rows(TILES8)
+    check_out(a[:, rows], want[:, rows], f"staged single={single}")
+
+
+def test_attention_staged_empty_stages(device):
+    """Staged calls whose one stage has no unit: a table of every page of a
+    16-page window (no rep tile: the compensation launch hands on an empty
+    state) and a table of padding only (no exact page)."""
+    h, p = 2, 16
+    gen = torch.Generator().manual_seed(93)
+    q = torch.randn(1, 128, h, 128, generator=gen).bfloat16()
+    k = torch.randn(1, 64 * p, h, 128, generator=gen).bfloat16()
+    v = torch.randn(1, 64 * p, h, 128, generator=gen).bfloat16()
+    vp = v[0].transpose(0, 1).reshape(h, p, 64, 128)
+    basis = workload.pca_basis(vp.float())
+    s = workload.kmeans_summaries(k[0].transpose(0, 1).reshape(h, p, 64, 128), vp, basis,
+                                  torch.Generator().manual_seed(7))
+    gd = Summary(*(getattr(s, f).to(device) for f in Summary.FIELDS))
+    every = torch.stack([torch.randperm(p, generator=gen) for _ in range(2 * h)]).reshape(h, 2, p).int()
+    for name, table in (("every page", every), ("padding only", torch.full((h, 2, 3), -1, dtype=torch.int32))):
+        out = attention(q.to(device), k.to(device), v.to(device), gd, basis.to(device), table.to(device),
+                        Workspace(), staged=True)
+        torch.cuda.synchronize()
+        want = ref.selected_attention(q, k, v, s, basis, table).bfloat16()
+        check_out(out, want, f"staged, {name}")

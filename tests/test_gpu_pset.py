@@ -158,3 +158,57 @@ def test_route_full_pset_end_to_end(device):
           f"executed {int(stats[0])}/{int(stats[1])}", flush=True)
     assert bool((same | ties).all())
     assert int(stats[1]) == len(HEADS) * 72 and int(stats[2]) == 0
+
+
+@pytest.mark.parametrize("n", [4, 20, 40])
+def test_pset_first_chunk_matches_oracle(device, n):
+    """Full_Pset on a 72-page window, the first chunk's (VB/quota_pool.py:
+    21-33): the anchor frame is the chunk's first frame, own page t of block
+    t.  n = 4 is the reference's first-chunk quota (VB/queue_policy.py:26);
+    n = 20 leaves 28 unselected pages, so add slots 28..31 hold selected
+    (anchor) pages, also listed as remove stand-ins; n = 40 leaves 8, so
+    legal adds hold selected pages too.  Pools equal, scores within 1e-4 of
+    the row scale, decisions and masks equal off near ties."""
+    x = workload.make_call(cfg=3, frames=3)
+    w = workload.reader_weights()
+    assert x.pages == 72
+    g, reader, enc = gpu_encoding(x, w, device)
+    ws = Workspace()
+    lse = torch.empty(12, 72, 16, device=device)
+    ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='intersection', own=g.own, n=n, workspace=ws,
+                               lse_out=lse)
+    mask0 = mask.clone()
+    stats, rows = pset.correct(g.q, g.summary, enc, reader, risk, lse, mask, ids, g.own, HEADS, want_scores=True)
+    torch.cuda.synchronize()
+    pr = ref.probes(x.q)
+    z = ref.route_logits(pr, x.summary.keys)
+    enc_o = dict(co=enc.co.cpu(), A=enc.A.cpu(), mean=enc.mean.cpu(), detail=enc.detail.cpu())
+    m0 = mask0.cpu()
+    assert (m0.sum(-1) == 24 + n).all()
+    want_mask, orow, ostats = opset.correct(pr.bfloat16().float(), z, risk.cpu(), m0, x.own, enc_o, w['wq'], HEADS)
+    pool = rows['pool'].cpu()
+    assert torch.equal(pool[..., :16].long(), orow['remove'])
+    assert torch.equal(pool[..., 16:48].long(), orow['add'])
+    legal = orow['legal'].reshape(len(HEADS), 72, 16, 32)
+    got_s = rows['scores'].cpu()
+    want_s = orow['scores']
+    scale = want_s.masked_fill(~legal, 0).abs().flatten(-2).amax(-1).clamp_min(1e-300)
+    err = ((got_s - want_s).abs().masked_fill(~legal, 0).flatten(-2).amax(-1) / scale)
+    print(f"n={n}: scores max err / row scale {float(err.max()):.2e}; gpu executed {int(stats[0])}, "
+          f"oracle executed {int(ostats[0])} of {int(ostats[1])}", flush=True)
+    assert float(err.max()) < 1e-4
+    assert (got_s.masked_fill(legal, 0) == -1e30).masked_fill(legal, True).all()
+    ties = _near_tie(want_s, legal)
+    ex_g = rows['executed'].cpu().bool()
+    same = (ex_g == orow['executed']) & (~ex_g | (rows['argmax'].cpu().long() == orow['argmax']))
+    print(f"decisions: {int(same.sum())}/{same.numel()} identical, {int(ties.sum())} near-tie rows", flush=True)
+    assert bool((same | ties).all())
+    got_mask = mask.cpu()
+    hs = torch.tensor(HEADS)
+    assert bool(((got_mask[hs] == want_mask[hs]).all(-1) | ties).all())
+    # the LUT of every row: own first, then the selection by descending risk, -1 past its end
+    got_ids = ids.cpu()
+    assert torch.equal(ref.mask_from_ids(got_ids, 72), got_mask)
+    assert (got_ids[..., 0] == x.own).all() and got_mask[..., :24].all()
+    want_ids = ref.lut(risk.cpu(), got_mask, x.own, 24 + n)
+    assert torch.equal(got_ids.sort(-1).values, want_ids.sort(-1).values)

@@ -118,3 +118,38 @@ def test_rolling_window(device):
             w = wsum[name].float()[ok]
             assert bool(((got - w).abs() <= w.abs() * 2.0 ** -7 + 1e-6).all()), (layer, name)
     assert rt.calls['full_pset'] >= 1
+
+
+def test_first_chunk_sparse(device):
+    """sparse_start_chunks=(0,): chunk 0 runs sparse on its 72-page window
+    (the reference's first-chunk quota n = 4, A = 4: VB/queue_policy.py:
+    25-28) with Full_Pset on layer 2, chunk 1 dense; the chunk-0 sparse and
+    corrected calls match SelectedAttention.fixed on their page tables."""
+    cfg = StreamConfig(layers=3, steps=1, history_pages=168, pset_layers=(2,), seed=9, sparse_start_chunks=(0,))
+    rt = StreamRuntime(cfg, device)
+    inputs = rt.chunk_inputs()
+    rt.begin_chunk()
+    rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in TILES])
+    for layer in range(3):
+        q, k, v = inputs[0][layer]
+        out = rt.layer_call(0, layer, q, k, v).clone()
+        torch.cuda.synchronize()
+        if layer == 0:
+            continue
+        L = rt.layers[layer]
+        ids = rt.last_ids.cpu()
+        assert ids.shape[-1] == 28 and (ids[..., 0] == torch.arange(72)).all()
+        kw, vw = L.k[:, :64 * 72].cpu(), L.v[:, :64 * 72].cpu()
+        s = Summary(*(getattr(L.slab, f)[:, :72].cpu() for f in Summary.FIELDS))
+        want = ref.selected_attention(q.cpu(), kw, vw, s, L.basis.cpu().float(), ids, tiles=TILES).bfloat16()
+        _check(out[:, rows], want[:, rows], f"first-chunk sparse layer {layer}")
+    assert rt.calls == dict(sparse=2, dense=1, full_pset=1)
+    # the rest of chunk 0 (clean step, commit) and chunk 1 (dense: 72 history pages)
+    for layer in range(3):
+        rt.layer_call(cfg.steps, layer, *inputs[cfg.steps][layer])
+    rt.commit_chunk(inputs)
+    rt.end_chunk()
+    rt.run_chunk(rt.chunk_inputs())
+    torch.cuda.synchronize()
+    assert rt.ring.n == 144 and rt.calls['sparse'] == 2 and rt.calls['full_pset'] == 1
+    assert bool(torch.isfinite(rt.last['out'].float()).all())

@@ -137,6 +137,16 @@ def test_c_abi_rejects_bad_shapes():
     assert att(4608, 432, 64, 1536, ops=None) == INVALID
     assert att(4608, 432, 64, 1536, ops=24) == INVALID                # misaligned
     assert att(4608, 432, 64, 1536, tiles=26) == INVALID              # 432 pages need 27 tiles
+    # a staged call (flags bit 2) is a general call and needs the workspace
+    assert att(4608, 432, 432, 1536, flags=6) == INVALID
+    assert att(4608, 432, 64, 1536, flags=5) == INVALID               # no workspace
+    # the workspace size query rejects what the call rejects; a staged call keeps two states of
+    # 33,280 bytes per tile
+    wb = L.ssa_attention_workspace_bytes
+    assert wb(65, 12, 432, 64, 1) == -1
+    assert wb(4608, 12, 432, 433, 1) == -1
+    assert wb(4608, 12, 432, 432, 6) == -1
+    assert wb(4608, 12, 432, 64, 5) == 864 * 2 * 33280
     # ssa_route: pages in (0, 512], modes -1..2, base count >= 25, quota count = 24 + total,
     # operand tiles (when asked for) 16-byte aligned, ceil(pages/16) of them, with the detail rows
     rt = lambda pages, count, mode, total, cur=None, ops=None, det=None, tiles=32: L.ssa_route(
@@ -179,10 +189,13 @@ def test_c_abi_rejects_bad_shapes():
                                             hidden, N)
     assert en(73, 256) == INVALID
     assert en(72, 257) == INVALID
-    # ssa_pset: 96 < pages <= 512 and at least 64 unselected pages
+    # ssa_pset: a 72-page window (the first chunk) or 96 < pages <= 512 with at least 64 unselected pages
     ps = lambda pages, count: L.ssa_pset(N, 128, 64 * 12 * 128, 12 * 128, 0, N, pages, N, N, N, pages, N, N, N, N,
                                          N, N, N, 3, N, N, N, N, N, N, N, 12, 72, pages, count, N)
     assert ps(96, 40) == INVALID
+    assert ps(80, 40) == INVALID
+    assert ps(72, 73) == INVALID
+    assert ps(72, 23) == INVALID                                      # fewer than the 24 anchors
     assert ps(432, 400) == INVALID
     # ssa_rep_operands: heads >= 1, pages in (0, 512], ceil(pages/16) tiles, aligned output
     ro = lambda heads, pages, tiles, out=16: L.ssa_rep_operands(16, out, heads, pages, 512, tiles, N)

@@ -129,6 +129,48 @@ def test_pool_rules(p):
             assert len(set(rm + ad)) == 48
 
 
+def _rule_pool72(risk, sel, own):
+    """The first chunk's pool from its rules, one row of a 72-page window,
+    plain Python: movable removes by (risk, page) up to 8, then the anchor
+    pages other than own; adds by (-risk, page) over the unselected pages,
+    then the selected pages by page; legal = movable x the first 16 adds."""
+    mov = sorted((i for i in range(24, 72) if sel[i] and i != own), key=lambda i: (float(risk[i]) + 0.0, i))
+    used = min(len(mov), 8)
+    stand = [i for i in range(24) if i != own]
+    rm = mov[:used] + stand[:16 - used]
+    uns = sorted((i for i in range(72) if not sel[i]), key=lambda i: (-float(risk[i]) + 0.0, i))
+    ad = (uns + [i for i in range(72) if sel[i]])[:32]
+    legal = [[x < used and y < 16 for y in range(32)] for x in range(16)]
+    return rm, ad, legal
+
+
+def test_pool_rules_first_chunk():
+    """72-page window (VB/quota_pool.py:21-33): rows with few and many
+    movable pages, own inside and outside the anchor frame, fewer than 16
+    and fewer than 32 unselected pages (the add slots then hold selected
+    pages), signed-zero and integer-binned risks."""
+    h, t, p = 2, 6, 72
+    risk = _adversarial(p, h * t, 5).reshape(h, t, p)
+    g = torch.Generator().manual_seed(11)
+    mask = torch.rand(h, t, p, generator=g) < 0.4
+    mask[..., :24] = True
+    own = torch.tensor([[3, 30, 50, 71, 24, 0], [23, 40, 60, 25, 10, 70]])
+    mask.scatter_(-1, own[..., None], True)
+    mask[0, 1, 24:] = False
+    mask[0, 1, 30] = True                       # only own beyond the anchors: no movable page
+    mask[1, 2, 24:60] = True                    # 12 unselected pages: add slots 12..31 hold selected pages
+    mask[1, 3, 24:] = True
+    mask[1, 3, 60:64] = False                   # 4 unselected pages
+    r, a, legal = pset.pool(risk, mask, own)
+    for hh in range(h):
+        for tt in range(t):
+            rm, ad, lg = _rule_pool72(risk[hh, tt], mask[hh, tt].tolist(), int(own[hh, tt]))
+            assert r[hh, tt].tolist() == rm
+            assert a[hh, tt].tolist() == ad
+            assert legal[hh, tt].tolist() == lg
+            assert len(set(rm)) == 16 and len(set(ad)) == 32
+
+
 def test_read_closed_forms():
     g = torch.Generator().manual_seed(4)
     h, t, m, p = 2, 2, 3, 5
