@@ -19,6 +19,11 @@ Also measured in the same run:
   and this library's kernel with every page exact;
 * a chunk of the 30-layer streaming workload (rolling window runtime).
 
+Before the first measured line, untimed headline calls run for
+--device-warmup-ms (300 ms): a GPU leaving its idle clocks would otherwise
+slow whatever is measured first.  Every line then does its own warm-up calls
+(the headline exactly --warmup) before its timed calls.
+
 Prints ONE JSON line; `value` is ms per call (lower is better).  The
 roofline object covers the dominant kernel (fused exact + compensation +
 merge): its average duration inside a call, from HIP events recorded around
@@ -62,6 +67,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip the intersection / Full_Pset lines")
     ap.add_argument("--no-chunk", action="store_true", help="skip the per-chunk 30-layer line")
     ap.add_argument("--cpu-sample-blocks", type=int, default=4)
+    ap.add_argument("--device-warmup-ms", type=float, default=300.0,
+                    help="untimed headline calls for at least this long before the first measured line")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the headline call (for a profiler run whose kernel averages are the headline's)")
     ap.add_argument("--staged", action="store_true",
@@ -105,18 +112,16 @@ def time_loop(fn, iters, stream):
     return a.elapsed_time(b) / iters
 
 
-def call_timings(g, P, C, single, steps, warmup, stream, staged=False):
-    """One base-tier call (route + attention) timed over `steps` calls after
-    `warmup`, then the kernels' average durations inside a call from HIP events
-    recorded around each launch on its stream (a second pass of the same
-    calls, kept out of the timed region whose calls they would space out).
-    Also returns the host's enqueue time per call over the timed calls."""
+def call_step(g, P, single, stream, staged=False):
+    """One base-tier call (route + attention) as a function of optional HIP
+    event marks recorded before the route, between the launches and after
+    the attention."""
     import torch
     from streaming_sparse_amd.attention import Workspace
     from streaming_sparse_amd.legacy_components import REP_OP_ELEMS, attention, rep_tiles
     from streaming_sparse_amd.route import route
     dev = g.q.device
-    H, D = 12, 128
+    H = 12
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()   # the caller keeps the basis bf16-rounded
     ops = ws.tensor('call_rep_ops', (H, rep_tiles(P), REP_OP_ELEMS), dev, torch.bfloat16)
@@ -134,6 +139,17 @@ def call_timings(g, P, C, single, steps, warmup, stream, staged=False):
             marks[2].record(stream)
         return o
 
+    return step
+
+
+def call_timings(g, P, C, single, steps, warmup, stream, staged=False):
+    """One base-tier call (route + attention) timed over `steps` calls after
+    `warmup`, then the kernels' average durations inside a call from HIP events
+    recorded around each launch on its stream (a second pass of the same
+    calls, kept out of the timed region whose calls they would space out).
+    Also returns the host's enqueue time per call over the timed calls."""
+    import torch
+    step = call_step(g, P, single, stream, staged)
     for _ in range(warmup):
         step()
     start = torch.cuda.Event(enable_timing=True)
@@ -154,6 +170,24 @@ def call_timings(g, P, C, single, steps, warmup, stream, staged=False):
     route_in = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
     attn_in = sum(m[1].elapsed_time(m[2]) for m in marks) / steps
     return ms_call, route_in, attn_in, host_ms
+
+
+def device_warmup(step, ms):
+    """Untimed headline calls (`step`) for at least `ms` milliseconds of wall
+    time, before anything is measured: the GPU leaves its idle clocks within
+    a few hundred ms of load.  Measured first in a fresh process, 5 warm-up
+    and 20 timed calls of the headline read ~0.29 ms against ~0.25 ms after
+    such a warm-up (the host enqueues a call in ~0.05 ms, so the loop is not
+    host-bound)."""
+    import torch
+    t0 = time.perf_counter()
+    calls = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(20):
+            step()
+        calls += 20
+        torch.cuda.synchronize()
+    return calls
 
 
 def attn_flop(N, H, D, C, P):
@@ -196,6 +230,9 @@ def main():
     single = bool(args.single_av)
     print(f"# headline: base tier P={P} C={C} single_av={single} staged={bool(args.staged)}", file=sys.stderr,
           flush=True)
+    warm_calls = device_warmup(call_step(g, P, single, stream, args.staged and args.headline_only),
+                               args.device_warmup_ms) if args.device_warmup_ms > 0 else 0
+    log(f"device warm-up: {warm_calls} untimed calls")
     if args.headline_only:
         ms_call, route_in_ms, attn_in_ms, host_ms = call_timings(g, P, C, single, args.steps, args.warmup, stream,
                                                                  staged=args.staged)
@@ -203,13 +240,11 @@ def main():
         print(json.dumps({"metric": METRIC, "value": round(ms_call, 4), "unit": "ms", "headline_only": True,
                           "attention_kernel_ms": round(attn_in_ms, 4), "route_ms": round(route_in_ms, 4),
                           "host_enqueue_ms_per_call": round(host_ms, 4), "single_av": single,
+                          "device_warmup": {"ms": args.device_warmup_ms, "untimed_calls": warm_calls},
                           "staged": bool(args.staged)}), flush=True)
         return
 
-    # Per-kernel timings back to back (same stream, same inputs), straight through the C ABI, and the dense
-    # lines, before the headline: the GPU then runs the headline at its loaded clock.  Timed first in a
-    # fresh process, 5 warm-up and 20 timed calls of the headline read ~0.29 ms against ~0.25 ms once the
-    # GPU has been busy for a few hundred ms (its clocks ramp from idle); the host enqueues a call in ~0.055 ms.
+    # per-kernel timings back to back (same stream, same inputs), straight through the C ABI
     ws = Workspace()
     basis = g.basis.to(torch.bfloat16).contiguous()
     ids, _, _, _ = route(g.q, g.summary, g.theta, tier='base', workspace=ws, want_mask=False)
@@ -238,7 +273,7 @@ def main():
         _lib.check(L.ssa_route(_lib.ptr(g.q), D, 64 * H * D, H * D, 0, _lib.ptr(g.summary.keys),
                                _lib.ptr(g.summary.stats), _lib.ptr(theta32), None, None, _lib.ptr(rrisk),
                                _lib.ptr(rids), None, None, H, N // 64, P, g.summary.head_pages, C, 0, 0,
-                               _lib.ptr(g.summary.detail), _lib.ptr(ops_call), ops_call.shape[1],
+                               _lib.ptr(g.summary.detail), _lib.ptr(ops_call), ops_call.shape[1], 0.0, None, None,
                                _lib.stream_handle(dev)), "ssa_route")
 
     route_ms = time_loop(route_only, iters, stream)
@@ -339,6 +374,7 @@ def main():
                    "tier": "base", "pages": P, "exact_pages": C, "heads": H, "queries": N, "head_dim": D,
                    "single_av": single},
         "host_enqueue_ms_per_call": round(host_ms, 4),
+        "device_warmup": {"ms": args.device_warmup_ms, "untimed_calls": warm_calls},
         "breakdown_ms": {"route_and_rep_operands": round(route_in_ms, 4), "attention_kernel": round(attn_in_ms, 4),
                          "route_back_to_back": round(route_ms, 4),
                          "attention_back_to_back_two_term": round(attn_ms["two_term"], 4),

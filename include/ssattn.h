@@ -136,12 +136,25 @@ long long ssa_attention_workspace_bytes(int n_tokens, int heads, int pages, int 
  * rep_ops [H,rep_tiles,512] bf16 (NULL to skip; 16-byte aligned, rep_tiles >=
  * ceil(pages/16)) receives, on the side, exactly what ssa_rep_operands
  * writes from detail [H,head_pages,3,8], so a call that routes needs no
- * separate operand launch. */
+ * separate operand launch.
+ * Near-tie report (tie_rows NULL to skip; mode >= 0, tie_eps >= 0): the
+ * rows h*blocks + t whose selection depends on a near tie are appended to
+ * tie_rows [H*blocks] int32 in no particular order, and *tie_count (int32,
+ * set to 0 by the call itself, graph-safe) receives their number -- the
+ * compacted list and count of the reference's select_close / mark_close
+ * (VR/csrc/risk_close.cu:35-79), which its recheck recomputes
+ * (VR/risk_recheck.py:86-123).  A row is listed when, in a sorted run of
+ * its selection (base: the pages >= 24 other than own, count-25 kept;
+ * quota: the current pages with own first, A kept, and the history pages,
+ * total-A kept, each clamped to the run; top-k: all pages with own first,
+ * count kept), the last kept and the first dropped risks a, c (own, ranked
+ * first by force, never counts) satisfy |a - c| <= tie_eps * max(|a|,
+ * |c|). */
 int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
               int pages, int head_pages, int count, int mode, int total, const void* detail, void* rep_ops,
-              int rep_tiles, hipStream_t stream);
+              int rep_tiles, float tie_eps, int32_t* tie_rows, int32_t* tie_count, hipStream_t stream);
 
 /* Page selection from given scores (RV/ops.py:113-138 RouteOps.select), one
  * row per (head, block): scores [rows,pages] fp32, own [rows] int32, valid

@@ -22,7 +22,7 @@ SIGNATURES = {
                       _vp],
     "ssa_attention_workspace_bytes": [_i, _i, _i, _i, _i],
     "ssa_route": [_vp, _ll, _ll, _ll, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
-                  _vp, _vp, _i, _vp],
+                  _vp, _vp, _i, _f, _vp, _vp, _vp],
     "ssa_select": [_vp, _vp, _vp, _i, _i, _f, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     "ssa_encode": [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                    _i, _vp],

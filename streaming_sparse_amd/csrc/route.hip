@@ -58,6 +58,12 @@ struct RouteParams {
   const uint16_t* rdetail;
   uint16_t* rops;
   int RT;
+  // near-tie report (tie_rows null: not asked for): rows h * T + t whose
+  // selection boundary holds two risks within tie_eps relative, appended
+  // to tie_rows through the counter *tie_count (zeroed by a launch before)
+  float tie_eps;
+  int32_t* tie_rows;
+  int32_t* tie_count;
 };
 
 constexpr int kSlotBytes = 9 * 1024;   // a rep tile: 32 rows x 256 B (swizzled) + its pages' stats (768 B)
@@ -202,6 +208,8 @@ __device__ void rep_operand_block(const RouteParams& p, int r) {
   const u32x4 w = rep_operand_chunk(p.rdetail + (long long)h * p.HP * 24, p.P, rt, c);
   *reinterpret_cast<u32x4*>(p.rops + ((long long)h * p.RT + rt) * (kRepOpBytes / 2) + 8 * c) = w;
 }
+
+__global__ __launch_bounds__(1) void zero_count_kernel(int32_t* count) { *count = 0; }
 
 __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   __shared__ Smem s;
@@ -521,6 +529,31 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   // sl.key[b] sorted descending; the page of entry i is 1023 - (key & 1023)
   auto page_at = [&](int i) -> int { return 1023 - (int)(sl.key[b][i] & 1023ull); };
   const bool row_ok = b < nrow;
+  if (p.tie_rows && bt == 0 && row_ok) {
+    // Near ties at the selection boundaries, in the sorted runs of the
+    // partitions: the last kept entry of a run against the first dropped
+    // one, when both are ranked by risk (not the forced own page); flagged
+    // iff |a - c| <= eps max(|a|, |c|).  Base: the candidates (pages >= 24
+    // other than own), C - 25 kept; quota: the current run (own first when
+    // inside it), A kept, and the history run after it, nh kept; top-k: all
+    // pages (own first), C kept.  The reference's recheck lists such rows
+    // (VR/csrc/risk_close.cu:35-79, VR/risk_recheck.py:86-123).
+    auto risk_at = [&](int i) { return s.risk[b][page_at(i)]; };
+    auto near = [&](int base, int len, int kept, bool forced_first) {
+      if (kept < 1 || kept >= len || (forced_first && kept == 1)) return false;
+      const float a = risk_at(base + kept - 1), c = risk_at(base + kept);
+      return fabsf(a - c) <= p.tie_eps * fmaxf(fabsf(a), fabsf(c));
+    };
+    bool tie;
+    if (p.mode == 0) {
+      tie = near(0, P - kAnchors - (own[b] >= kAnchors ? 1 : 0), p.C - 1 - kAnchors, false);
+    } else if (p.mode == 1) {
+      tie = near(0, ncur, A, own[b] >= cur_lo) || near(ncur, nhist, nh, false);
+    } else {
+      tie = near(0, P, p.C, true);
+    }
+    if (tie) p.tie_rows[atomicAdd(p.tie_count, 1)] = h * p.T + t0 + b;
+  }
   int32_t* idsrow = p.ids ? p.ids + ((long long)h * p.T + t0 + b) * p.C : nullptr;
   for (int pg = bt; pg < P; pg += 128) sl.sel[b][pg] = 0;
   __syncthreads();
@@ -699,10 +732,12 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
               int gathered, const void* keys, const void* stats, const float* theta, const int32_t* current,
               const int32_t* own, float* risk, int32_t* ids, uint8_t* mask, float* lse, int heads, int blocks,
               int pages, int head_pages, int count, int mode, int total, const void* detail, void* rep_ops,
-              int rep_tiles, hipStream_t stream) {
+              int rep_tiles, float tie_eps, int32_t* tie_rows, int32_t* tie_count, hipStream_t stream) {
   if (heads <= 0 || blocks <= 0 || pages <= 0 || pages > kMaxPages || head_pages < pages || mode < -1 ||
       mode > 2)
     return (int)hipErrorInvalidValue;
+  // the near-tie report needs a selection, its counter and a non-negative epsilon
+  if (tie_rows && (mode < 0 || !tie_count || !(tie_eps >= 0.0f))) return (int)hipErrorInvalidValue;
   // the operand tiles move in 16-byte stores
   if (rep_ops && (!detail || rep_tiles < (pages + 15) / 16 || ((uintptr_t)rep_ops & 15)))
     return (int)hipErrorInvalidValue;
@@ -738,6 +773,12 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
   p.rdetail = (const uint16_t*)detail;
   p.rops = (uint16_t*)rep_ops;
   p.RT = rep_tiles;
+  p.tie_eps = tie_eps;
+  p.tie_rows = tie_rows;
+  p.tie_count = tie_count;
+  // the counter starts at zero: a fill kernel rather than a memset node, so
+  // that a captured graph replays it
+  if (tie_rows) hipLaunchKernelGGL(zero_count_kernel, dim3(1), dim3(1), 0, stream, tie_count);
   const int np = (blocks + 1) / 2;
   const int nrv = rep_ops ? (heads * ((pages + 15) / 16) * kRepOpChunks + kThreads - 1) / kThreads : 0;
   hipLaunchKernelGGL(route_kernel, dim3(heads * np + nrv), dim3(kThreads), 0, stream, p);

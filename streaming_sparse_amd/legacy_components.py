@@ -211,6 +211,6 @@ def risk(probes, z, summary, theta, *, z_tol=1e-4):
     out = torch.empty(h, t, p, device=probes.device, dtype=torch.float32)
     _lib.check(_lib.lib().ssa_route(_lib.ptr(pr), t * m * d, m * d, d, 1, _lib.ptr(summary.keys),
                                     _lib.ptr(summary.stats), _lib.ptr(th), None, None, _lib.ptr(out), None, None,
-                                    None, h, t, p, hp, 0, -1, 0, None, None, 0,
+                                    None, h, t, p, hp, 0, -1, 0, None, None, 0, 0.0, None, None,
                                     _lib.stream_handle(probes.device)), "ssa_route")
     return out

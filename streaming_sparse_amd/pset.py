@@ -105,7 +105,7 @@ def encode(summary: Summary, basis: torch.Tensor, reader: Reader, out: Encoding 
 
 @torch.no_grad()
 def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, lse, mask, ids, own, heads,
-            workspace=None, want_scores=False, no_alloc=False):
+            workspace=None, want_scores=False, no_alloc=False, probe_layout=None):
     """Full_Pset correction of the scoped `heads` in place on `mask` (uint8 or
     bool storage, [H,T,P]) and `ids` [H,T,C] from the intersection router,
     whose `risk` and per-probe `lse` ([H,T,16], route(..., lse_out=...)) it
@@ -113,22 +113,35 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, lse, 
     no_alloc: run ssa_pset_noalloc, whose scratch is the library's own
     device array (at most 216 scoped (head, block) rows; concurrent calls on
     one device race), instead of workspace scratch.
+    probe_layout: (head, block, row strides in elements, gathered) of a q in
+    another layout, e.g. the reference's [H, T, n, D] blocks (gathered = 1:
+    q holds the 16 probe rows of each block); default: q is [1,N,H,128].
     Returns (stats int64 [3] = executed, rows, non-finite scores; per-row
     dict)."""
-    _, nq, h, d = q.shape
-    t = nq // 64
-    p = risk.shape[-1]
+    h, t, p = risk.shape
+    d = HEAD_DIM
     dev = q.device
-    head_list = [int(i) for i in heads]
-    if not head_list or len(set(head_list)) != len(head_list) or min(head_list) < 0 or max(head_list) >= h:
-        raise ValueError(f"full_pset heads must be distinct ids in [0,{h})")
-    key = ('pset_heads', tuple(head_list), torch.device(dev), torch.int32)
-    if workspace is not None and key in workspace.entries:
-        hs = workspace.entries[key]
+    if probe_layout is None:
+        if q.dim() != 4 or q.shape[2] != h or q.shape[1] != 64 * t:
+            raise ValueError("q must be [1,N,H,128] (or pass probe_layout)")
+        probe_layout = (d, 64 * h * d, h * d, 0)
+    if torch.is_tensor(heads) and heads.device == dev and heads.dtype == torch.int32 and heads.dim() == 1:
+        # a device list the caller has checked (distinct ids in [0, H)): read by the kernels as it is
+        # at launch, so a captured graph follows the caller's updates
+        hs = heads
+        if hs.numel() == 0:
+            raise ValueError("full_pset heads must not be empty")
     else:
-        hs = torch.tensor(head_list, dtype=torch.int32).to(dev)
-        if workspace is not None:
-            workspace.entries[key] = hs
+        head_list = [int(i) for i in heads]
+        if not head_list or len(set(head_list)) != len(head_list) or min(head_list) < 0 or max(head_list) >= h:
+            raise ValueError(f"full_pset heads must be distinct ids in [0,{h})")
+        key = ('pset_heads', tuple(head_list), torch.device(dev), torch.int32)
+        if workspace is not None and key in workspace.entries:
+            hs = workspace.entries[key]
+        else:
+            hs = torch.tensor(head_list, dtype=torch.int32).to(dev)
+            if workspace is not None:
+                workspace.entries[key] = hs
     n = hs.numel()
     hp = _summary_ok(summary)
     if encoding.coef.shape[1] < p:
@@ -147,7 +160,7 @@ def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, lse, 
     stats = buf('stats', (3,), torch.int64)
     mask_u8 = mask.view(torch.uint8) if mask.dtype == torch.bool else mask
     ow = None if own is None else own.to(device=dev, dtype=torch.int32).contiguous()
-    head = (_lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys), hp, _lib.ptr(encoding.coef),
+    head = (_lib.ptr(q), *probe_layout, _lib.ptr(summary.keys), hp, _lib.ptr(encoding.coef),
             _lib.ptr(encoding.mean), _lib.ptr(encoding.detail), encoding.coef.shape[1], _lib.ptr(reader.wq),
             _lib.ptr(risk), _lib.ptr(lse), _lib.ptr(mask_u8), _lib.ptr(ids), _lib.ptr(ow), _lib.ptr(hs), n)
     tail = (_lib.ptr(gain), _lib.ptr(info), _lib.ptr(scores), _lib.ptr(stats), h, t, p, ids.shape[-1],

@@ -48,7 +48,8 @@ def tier_count(tier: str, pages: int, n: int | None = None) -> int:
 
 @torch.no_grad()
 def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=None, workspace=None,
-          want_mask=True, full_pset=None, encoding=None, reader=None, lse_out=None, rep_out=None):
+          want_mask=True, full_pset=None, encoding=None, reader=None, lse_out=None, rep_out=None, ties=None,
+          tie_eps=1e-3):
     """q [1,N,H,128] bf16 queries of the current chunk; summary over the P
     window pages; theta [H,4]; own [H,T] (default: page P-T+t).  For the
     intersection tier pass n = A+B (<= P - 24) and, unless P == 72,
@@ -59,7 +60,13 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
     rep_out [H,>=ceil(P/16),512] bf16: the router also writes the
     attention's detail operand tiles of `summary` (as
     legacy_components.rep_operands) into rep_out, so attention(...,
-    rep_ops=rep_out) skips that launch."""
+    rep_ops=rep_out) skips that launch.
+    ties: optional (rows [H*T] int32, count [1] int32) device tensors that
+    receive the rows h*T + t whose selection boundary is a near tie (last
+    kept and first dropped risk within tie_eps relative; own never counts)
+    and their number, as the reference's select_close reports them for its
+    recheck; they describe the router's selection, before any Full_Pset
+    swap."""
     _, nq, h, d = q.shape
     if d != HEAD_DIM or q.dtype != torch.bfloat16 or not q.is_contiguous():
         raise ValueError("q must be contiguous [1,N,H,128] bf16")
@@ -110,11 +117,20 @@ def route(q, summary, theta, *, tier='base', own=None, current_slots=None, n=Non
         raise ValueError("lse_out must be a contiguous [H,T,16] float32 tensor")
     if rep_out is not None:
         check_rep_ops(rep_out, h, p, "rep_out")
+    tie_rows = tie_count = None
+    if ties is not None:
+        tie_rows, tie_count = ties
+        if tie_rows.dtype != torch.int32 or tie_rows.numel() < h * t or not tie_rows.is_contiguous() or \
+                tie_count.dtype != torch.int32 or tie_count.numel() < 1:
+            raise ValueError("ties must be (rows int32 [>=H*T], count int32 [1]) device tensors")
+        if not tie_eps >= 0:
+            raise ValueError("tie_eps must be >= 0")
     _lib.check(_lib.lib().ssa_route(_lib.ptr(q), d, 64 * h * d, h * d, 0, _lib.ptr(summary.keys),
                                     _lib.ptr(summary.stats), _lib.ptr(th), _lib.ptr(cur), _lib.ptr(ow),
                                     _lib.ptr(risk), _lib.ptr(ids), _lib.ptr(mask), _lib.ptr(lse), h, t, p, hp, count,
                                     mode, total, _lib.ptr(summary.detail) if rep_out is not None else None,
                                     _lib.ptr(rep_out), rep_out.shape[1] if rep_out is not None else 0,
+                                    float(tie_eps), _lib.ptr(tie_rows), _lib.ptr(tie_count),
                                     _lib.stream_handle(dev)), "ssa_route")
     if correcting:
         from . import pset

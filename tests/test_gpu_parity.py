@@ -689,3 +689,59 @@ def test_attention_staged_empty_stages(device):
         torch.cuda.synchronize()
         want = ref.selected_attention(q, k, v, s, basis, table).bfloat16()
         check_out(out, want, f"staged, {name}")
+
+
+def _expected_ties(r, x, tier, a=None, n=None, eps=1e-3):
+    """The rows a near-tie report lists, from the router's own fp32 risk with
+    the same arithmetic as the kernel (|a - c| <= eps max(|a|, |c|) in fp32)
+    at each selection boundary of the tier (oracle.reference.near_tie_rows on
+    the partition's candidates)."""
+    P = r.shape[-1]
+    own = x.own
+    if tier == 'base':
+        cand = r.clone()
+        cand[..., :24] = -math.inf
+        cand.scatter_(-1, own[..., None].long(), -math.inf)
+        return ref.near_tie_rows(cand, torch.full(own.shape, P * 15 // 100 - 25), rel=eps)
+    nh = (n - a).clamp(0, P - 96)[:, None].expand_as(own)
+    hist = r.clone()
+    hist[..., :24] = -math.inf
+    hist[..., P - 72:] = -math.inf
+    cur = r.clone()
+    cur[..., :P - 72] = -math.inf
+    cur.scatter_(-1, own[..., None].long(), math.inf)
+    ac = a[:, None].expand_as(own)
+    return (ref.near_tie_rows(hist, nh, rel=eps) & (nh >= 1)) | (ref.near_tie_rows(cur, ac, rel=eps) & (ac >= 2))
+
+
+@pytest.mark.parametrize("cfg,frames,tier", [(0, 9, 'base'), (2, 18, 'intersection')])
+def test_route_reports_near_ties(device, cfg, frames, tier):
+    """The router's near-tie report (the compacted row list + count of the
+    reference's select_close): exactly the rows whose selection boundary
+    holds two risks within 1e-3 relative, at the 216-page base call and the
+    432-page intersection call; the same rows (up to rounding of risks right
+    at the threshold) against the float64 oracle risk."""
+    x = call_inputs(cfg, frames)
+    g = x.to(device)
+    H, T = 12, 72
+    rows = torch.full((H * T,), -1, dtype=torch.int32, device=device)
+    cnt = torch.full((1,), 12345, dtype=torch.int32, device=device)
+    kw, a, n = {}, None, None
+    if tier == 'intersection':
+        tab = workload.quota_table(2)
+        a = tab[0, 3, :, 0]
+        n = int(tab[0, 3, 0].sum())
+        kw = dict(current_slots=a.to(device), n=n)
+    ids, _, risk, _ = route(g.q, g.summary, g.theta, tier=tier, own=g.own, ties=(rows, cnt), tie_eps=1e-3, **kw)
+    torch.cuda.synchronize()
+    k = int(cnt.item())
+    got = rows[:k].cpu().sort().values
+    assert k <= H * T and got.unique().numel() == k and bool((rows[k:] == -1).all())
+    want = _expected_ties(risk.cpu(), x, tier, a, n).flatten().nonzero()[:, 0].int()
+    r64 = oracle_risk(x).double()
+    want64 = _expected_ties(r64, x, tier, a, n).flatten()
+    print(f"{tier}: {k} near-tie rows of {H * T}; float64 oracle risk flags {int(want64.sum())}, "
+          f"{int((want64[got.long()]).sum())} of them listed", flush=True)
+    assert torch.equal(got, want)
+    assert int((want64 != torch.zeros(H * T, dtype=torch.bool).index_fill_(0, got.long(), True)).sum()) <= \
+        max(2, k // 10)

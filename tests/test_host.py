@@ -149,9 +149,9 @@ def test_c_abi_rejects_bad_shapes():
     assert wb(4608, 12, 432, 64, 5) == 864 * 2 * 33280
     # ssa_route: pages in (0, 512], modes -1..2, base count >= 25, quota count = 24 + total,
     # operand tiles (when asked for) 16-byte aligned, ceil(pages/16) of them, with the detail rows
-    rt = lambda pages, count, mode, total, cur=None, ops=None, det=None, tiles=32: L.ssa_route(
-        N, 128, 64 * 12 * 128, 12 * 128, 0, N, N, N, cur, N, N, N, N, N, 12, 72, pages, pages, count, mode, total,
-        det, ops, tiles, N)
+    rt = lambda pages, count, mode, total, cur=None, ops=None, det=None, tiles=32, eps=0.0, rows=None, cnt=None: \
+        L.ssa_route(N, 128, 64 * 12 * 128, 12 * 128, 0, N, N, N, cur, N, N, N, N, N, 12, 72, pages, pages, count, mode,
+                    total, det, ops, tiles, eps, rows, cnt, N)
     assert rt(0, 64, 0, 0) == INVALID
     assert rt(513, 64, 0, 0) == INVALID
     assert rt(432, 64, 3, 0) == INVALID
@@ -166,6 +166,9 @@ def test_c_abi_rejects_bad_shapes():
     assert rt(432, 64, 0, 0, ops=16, det=None) == INVALID             # operand tiles without detail rows
     assert rt(432, 64, 0, 0, ops=8, det=16) == INVALID                # misaligned
     assert rt(432, 64, 0, 0, ops=16, det=16, tiles=26) == INVALID     # 432 pages need 27 tiles
+    assert rt(432, 64, 0, 0, rows=16) == INVALID                      # near-tie rows without their counter
+    assert rt(432, 64, 0, 0, rows=16, cnt=16, eps=-1.0) == INVALID    # negative epsilon
+    assert rt(432, 64, -1, 0, rows=16, cnt=16, eps=1e-3) == INVALID   # risk only: no selection
     # ssa_select: 0 < pages <= 512, 1 <= cap <= min(id_capacity, pages), density count <= id_capacity,
     # scores / own / outputs present (valid may be NULL)
     sel = lambda rows, pages, thr, fixed, cap, idcap, sc=8: L.ssa_select(sc, 8, N, rows, pages, 0.0, thr, fixed, cap,
@@ -219,3 +222,24 @@ def test_select_rejects_bad_config():
     with pytest.raises(ValueError):
         select(torch.zeros(1, 1, 600), own, id_capacity=200)
 
+
+
+def test_batch_graphs_checks_call_shape():
+    """BatchGraphs rejects an unknown tier, a q outside the reference's
+    [H, T, 64 or 16, 128] block layout, and an intersection call without its
+    quota, before any device work."""
+    from streaming_sparse_amd.graph import BatchGraphs
+    with pytest.raises(ValueError):
+        BatchGraphs('nope')
+    p = 216
+    s = Summary(torch.zeros(H, p, 4, D, dtype=torch.bfloat16), torch.zeros(H, p, D, dtype=torch.bfloat16),
+                torch.zeros(H, p, 3, 8, dtype=torch.bfloat16), torch.zeros(H, p, 4, 12, dtype=torch.bfloat16))
+    bg = BatchGraphs('intersection')
+    with pytest.raises(ValueError):
+        bg.get(torch.zeros(H, 72, 32, D), s, None, torch.ones(H, 4), None, None, False)
+    with pytest.raises(ValueError):                                  # n and current_slots not set
+        bg.get(torch.zeros(H, 72, 64, D), s, None, torch.ones(H, 4), None, None, False)
+    bg.n = 40
+    bg.current_slots = torch.full((H,), 10)
+    with pytest.raises(ValueError):                                  # Full_Pset without reader / encoding
+        bg.get(torch.zeros(H, 72, 64, D), s, None, torch.ones(H, 4), None, None, True, [3])
