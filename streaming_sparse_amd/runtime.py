@@ -77,6 +77,10 @@ class StreamConfig:
     quota_mean: float = 40.8
     sparse_start_chunks: tuple = ()   # chunks with <= 72 history pages that still run sparse
     grouping: bool = True             # group the committed tokens into pages (False: token order)
+    # 'intersection': anchor/current/history quotas with Full_Pset (VB/queue_policy.py); 'base': the
+    # base tier, own + 24 anchors + the floor(0.15 P) - 25 highest-risk pages, no swap correction
+    # (VR/runtime.py:279-288; a window of at least 96 pages)
+    tier: str = 'intersection'
 
 
 class PageRing:
@@ -157,6 +161,8 @@ class StreamRuntime:
     """Resident per-layer state of a stream of 3-frame chunks."""
 
     def __init__(self, cfg: StreamConfig, device, reader_weights=None):
+        if cfg.tier not in ('intersection', 'base'):
+            raise ValueError(f"unknown tier {cfg.tier!r}")
         self.cfg = cfg
         dev = torch.device(device)
         self.device = dev
@@ -319,15 +325,20 @@ class StreamRuntime:
 
     def sparse_call(self, step, layer, q, kw, vw, P):
         cfg, L = self.cfg, self.layers[layer]
-        correct = L.encoding is not None and step in cfg.pset_steps
+        correct = cfg.tier == 'intersection' and L.encoding is not None and step in cfg.pset_steps
         summary.build(L.k, L.v, L.basis, self.init, L.slab, P - CURRENT, CURRENT)
         s = L.slab.slice(0, P)
+        ops = self.ws.tensor('rt_rep_ops', (self.H, rep_tiles(P), REP_OP_ELEMS), q.device, torch.bfloat16)
+        if cfg.tier == 'base':
+            ids, _, _, _ = route(q, s, self.theta, tier='base', workspace=self.ws, want_mask=False, rep_out=ops)
+            self.calls['sparse'] += 1
+            self.last_ids = ids
+            return attention(q, kw, vw, s, L.basis, ids, self.ws, rep_ops=ops)
         if correct:
             pset.encode(L.slab, L.basis, self.reader, out=L.encoding, first=P - CURRENT, pages=CURRENT)
         a_tab, n_tab = self.quota(self.chunk)
         a = a_tab[step, layer - 1]
         n = int(n_tab[step][layer - 1])
-        ops = self.ws.tensor('rt_rep_ops', (self.H, rep_tiles(P), REP_OP_ELEMS), q.device, torch.bfloat16)
         ids, _, _, _ = route(q, s, self.theta, tier='intersection', current_slots=a, n=n, workspace=self.ws,
                              want_mask=correct, lse_out=self.lse if correct else None,
                              full_pset=cfg.pset_heads if correct else None, encoding=L.encoding,
@@ -420,5 +431,5 @@ class StreamRuntime:
         dense_window = self.dense_window()
         sparse = 0 if dense_window else cfg.steps * (cfg.layers - 1)
         return dict(sparse=sparse, dense=cfg.steps * cfg.layers + cfg.layers - sparse,
-                    full_pset=0 if dense_window else
+                    full_pset=0 if dense_window or cfg.tier != 'intersection' else
                     len([l for l in cfg.pset_layers if 0 < l < cfg.layers]) * len(cfg.pset_steps))

@@ -153,3 +153,46 @@ def test_first_chunk_sparse(device):
     torch.cuda.synchronize()
     assert rt.ring.n == 144 and rt.calls['sparse'] == 2 and rt.calls['full_pset'] == 1
     assert bool(torch.isfinite(rt.last['out'].float()).all())
+
+
+def test_base_tier_stream(device):
+    """The base tier as a stream (the 116-call base workload of a chunk,
+    here 3 layers x 1 step): chunks 0-1 dense, chunk 2 sparse on a 216-page
+    window with the base table (own, 24 anchors, the 7 highest-risk other
+    pages: floor(0.15 P) = 32); the page tables equal the oracle's base
+    selection off near ties, and the calls match SelectedAttention.fixed on
+    their tables."""
+    cfg = StreamConfig(layers=3, steps=1, history_pages=168, pset_layers=(2,), seed=10, tier='base')
+    rt = StreamRuntime(cfg, device)
+    for c in range(2):
+        rt.run_chunk(rt.chunk_inputs())
+    assert rt.calls['sparse'] == 0
+    inputs = rt.chunk_inputs()
+    rt.begin_chunk()
+    P = rt.ring.n + CURRENT
+    assert P == 216
+    rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in TILES])
+    for layer in (1, 2):
+        q, k, v = inputs[0][layer]
+        out = rt.layer_call(0, layer, q, k, v).clone()
+        torch.cuda.synchronize()
+        L = rt.layers[layer]
+        ids = rt.last_ids.cpu()
+        assert ids.shape[-1] == 32
+        s = Summary(*(getattr(L.slab, f)[:, :P].cpu() for f in Summary.FIELDS))
+        own = (torch.arange(72) + P - 72)[None].expand(12, -1)
+        pr = ref.probes(q.cpu())
+        r64 = ref.risk(pr, ref.route_logits(pr, s.keys, torch.float64), s.stats, rt.theta.cpu(), dtype=torch.float64)
+        want = ref.select_base(r64, own, 32)
+        cand = r64.clone()
+        cand[..., :24] = -float("inf")
+        cand.scatter_(-1, own[..., None], -float("inf"))
+        ties = ref.near_tie_rows(cand, torch.full(own.shape, 7))
+        same_set = (ids.sort(-1).values == want.sort(-1).values).all(-1)
+        print(f"base stream layer {layer}: {int(same_set.sum())}/864 tables equal, {int(ties.sum())} near-tie rows",
+              flush=True)
+        assert bool((same_set | ties).all())
+        kw, vw = L.k[:, :64 * P].cpu(), L.v[:, :64 * P].cpu()
+        want_out = ref.selected_attention(q.cpu(), kw, vw, s, L.basis.cpu().float(), ids, tiles=TILES).bfloat16()
+        _check(out[:, rows], want_out[:, rows], f"base stream layer {layer}")
+    assert rt.calls['sparse'] == 2 and rt.calls['full_pset'] == 0
