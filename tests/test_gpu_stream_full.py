@@ -47,3 +47,75 @@ def test_full_stream_repeat_and_counts(device):
         assert torch.equal(la.k.view(torch.int16), lb.k.view(torch.int16))
         assert torch.equal(la.slab.keys.view(torch.int16), lb.slab.keys.view(torch.int16))
         assert torch.equal(la.slab.stats.view(torch.int16), lb.slab.stats.view(torch.int16))
+
+
+def test_full_stream_call_matches_oracle(device):
+    """One call of the full workload against the oracle: after chunks 0..6
+    of the 30-layer runtime, chunk 7 (anchor rebased by 6 frames) step 0 of
+    layer 4, an intersection call with Full_Pset on heads {3, 4, 9} over the
+    full 432-page window.  Its page table equals the oracle chain (float64
+    risk -> quota mask -> Full_Pset) on every row whose selection or swap
+    decision is not a near tie, and its output matches
+    SelectedAttention.fixed on its table (4 query blocks x 12 heads)."""
+    import math
+
+    from oracle import pset as opset
+    from oracle import reference as ref
+    from streaming_sparse_amd import workload
+    from streaming_sparse_amd.ops import Summary
+    from streaming_sparse_amd.runtime import CURRENT, PSET_HEADS
+
+    rt, _ = run(device)
+    inputs = rt.chunk_inputs()
+    rt.begin_chunk()
+    layer = 4
+    q, k, v = inputs[0][layer]
+    out = rt.layer_call(0, layer, q, k, v).clone()
+    torch.cuda.synchronize()
+    L = rt.layers[layer]
+    P = rt.ring.n + CURRENT
+    assert P == 432 and rt.calls['full_pset'] > 0
+    ids = rt.last_ids.cpu()
+    s = Summary(*(getattr(L.slab, f)[:, :P].cpu() for f in Summary.FIELDS))
+    tiles = [0, 30, 50, 71]
+    rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in tiles])
+    want = ref.selected_attention(q.cpu(), L.k[:, :64 * P].cpu(), L.v[:, :64 * P].cpu(), s, L.basis.cpu().float(),
+                                  ids, tiles=tiles).bfloat16()
+    g, w_ = out[:, rows].cpu().float(), want[:, rows].float()
+    err, mx = ref.rel_l2(g, w_), float((g - w_).abs().max())
+    print(f"full-size call: rel-L2 {err:.3e} max-abs {mx:.3e}", flush=True)
+    assert err <= 5e-3 and mx <= 2e-2
+    # the page table against the oracle chain
+    a_tab, n_tab = rt.quota(rt.chunk)
+    a = a_tab[0, layer - 1].cpu().long()
+    n = int(n_tab[0][layer - 1])
+    own = (torch.arange(72) + P - 72)[None].expand(12, -1)
+    pr = ref.probes(q.cpu())
+    z = ref.route_logits(pr, s.keys)
+    r64 = ref.risk(pr, ref.route_logits(pr, s.keys, torch.float64), s.stats, rt.theta.cpu(), dtype=torch.float64)
+    m0 = ref.quota_mask(r64, own, a, n)
+    enc = L.encoding
+    enc_o = dict(co=enc.co[:, :P].cpu(), A=enc.A[:, :P].cpu(), mean=enc.mean[:, :P].cpu(),
+                 detail=enc.detail[:, :P].cpu())
+    w = workload.reader_weights(rt.cfg.seed)
+    want_mask, orow, _ = opset.correct(pr.bfloat16().float(), z, r64.float(), m0, own, enc_o, w['wq'],
+                                       list(PSET_HEADS))
+    hist = r64.clone()
+    hist[..., :24] = -math.inf
+    hist[..., P - 72:] = -math.inf
+    cur = r64.clone()
+    cur[..., :P - 72] = -math.inf
+    cur.scatter_(-1, own[..., None], math.inf)
+    ties = ref.near_tie_rows(hist, (n - a)[:, None].expand_as(own)) | \
+        ref.near_tie_rows(cur, a[:, None].expand_as(own))
+    legal = orow['legal'].reshape(len(PSET_HEADS), 72, 16 * 32)
+    scores = orow['scores'].flatten(-2)
+    top = scores.masked_fill(~legal, -math.inf).topk(2, dim=-1).values
+    scale = scores.masked_fill(~legal, 0).abs().amax(-1).clamp_min(1e-300)
+    pset_ties = ((top[..., 0] - top[..., 1]).abs() <= 1e-3 * scale) | (top[..., 0].abs() <= 1e-3 * scale)
+    ties[torch.tensor(PSET_HEADS)] |= pset_ties
+    got_mask = ref.mask_from_ids(ids, P)
+    same = (got_mask == want_mask).all(-1)
+    print(f"full-size call: {int(same.sum())}/864 tables equal the oracle chain, {int(ties.sum())} near-tie rows",
+          flush=True)
+    assert bool((same | ties).all())
