@@ -309,14 +309,13 @@ __device__ __forceinline__ float unit_max(f32x16& S, int e, int pair, int lane, 
 // (log2 units), so probabilities stay below 2^kSlack and the rescale is rare.
 constexpr float kSlack = 8.0f;
 
-// `ls` is a lane's fp32 partial denominator (the two-term path's exact
-// pages and every rep tile), L the single-term path's exact pages (matrix-pipe
-// row sums).  C holds the code accumulator in items 0..3 (ranks 4 hh + i).
-__device__ __forceinline__ void update_max(float mloc, float& m, f32x16& L, float& ls, f32x16 (&O)[4], f32x16& C) {
+// `ls` is a lane's fp32 partial denominator (the sum of the fp32
+// probabilities of its keys, in either arithmetic, as the reference's l).
+// C holds the code accumulator in items 0..3 (ranks 4 hh + i).
+__device__ __forceinline__ void update_max(float mloc, float& m, float& ls, f32x16 (&O)[4], f32x16& C) {
   if (__any(mloc > m + kSlack)) {
     const float mnew = fmaxf(m, mloc);
     const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
-    L *= alpha;
     ls *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) O[dt] *= alpha;
@@ -337,8 +336,8 @@ __device__ __forceinline__ u32x2 split_pair(float p0, float p1) {
 }
 
 // P = 2^(S*scale + nb) as the bf16 B operands of the two k steps (pb; pl =
-// the low parts bf16(P - bf16(P)) for the two-term product, whose
-// denominator `ls` gathers the fp32 P of the lane).
+// the low parts bf16(P - bf16(P)) for the two-term product); the
+// denominator `ls` gathers the fp32 P of the lane in either arithmetic.
 template <bool PRECISE>
 __device__ __forceinline__ void probabilities(const f32x16& S, float nb, float scale_log2, u32x4 (&pb)[2],
                                               u32x4 (&pl)[2], float& ls) {
@@ -361,12 +360,10 @@ __device__ __forceinline__ void probabilities(const f32x16& S, float nb, float s
                      pack_bf16(P[o + 4], P[o + 5]), pack_bf16(P[o + 6], P[o + 7])};
     }
   }
-  if (PRECISE) {
-    float s = 0.f;
+  float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s += P[i];
-    ls += s;
-  }
+  for (int i = 0; i < 16; ++i) s += P[i];
+  ls += s;
 }
 
 // Haar view of one page's 4 rep probabilities w: hw = {a, b0, b1, b2}, the
@@ -390,21 +387,12 @@ __device__ __forceinline__ u32x2 halves(uint32_t lo, uint32_t hi) {
   return u32x2{s[0], s[1]};
 }
 
-// bf16 1.0 in both halves: the A operand whose product with P^T puts the
-// row sums of P in every row of the accumulator.
-constexpr uint32_t kOnes = 0x3F803F80u;
-
-// O^T += V^T P^T, and in the single-term path L += 1 P^T (the softmax
-// denominator of lane's query over the pair's 32 keys, summed by the matrix
-// pipe from the same bf16 P that multiplies V; the two-term path sums fp32 P
-// on the vector unit instead, as the reference's l does).
+// O^T += V^T P^T (two-term: hi and lo parts of P).
 template <bool PRECISE>
 __device__ __forceinline__ void pv(const u32x4 (&pb)[2], const u32x4 (&pl)[2], const lds_u8* vbuf, int pair,
-                                   int lane, f32x16& L, f32x16 (&O)[4]) {
-  const u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
+                                   int lane, f32x16 (&O)[4]) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    if (!PRECISE) L = mfma32(ones, pb[ks], L);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const u32x4 va = v_operand(vbuf, pair, ks, dt, lane);
@@ -553,7 +541,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   auto vslot = [&](int slot) { return vbase + slot * kBuf; };
 
   float m = -INFINITY;
-  f32x16 L = {}, O[4], C = {};
+  f32x16 O[4], C = {};
   float ls = 0.f;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) O[dt] = f32x16{};
@@ -575,7 +563,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   f32x16 S0 = s_tile(kslot(ibeg & 1), pair, lane, qop), S1;
   float mloc;
   float bias = unit_max(S0, unit(ibeg), pair, lane, p.scale_log2, mloc);
-  update_max(mloc, m, L, ls, O, C);
+  update_max(mloc, m, ls, O, C);
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
   // Unit ids run ahead in registers (u0 = unit i); the id of unit i+3 is
   // read from LDS in step i-1, so the read completes at its barrier.
@@ -662,7 +650,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       // operand read 4 products ahead; the P.V products of unit i then
       // carry the max of unit i+1.  Scheduling barriers hold the order.
       u32x4 ka[8], va[2][4], pb[2];
-      float P[16];
+      float P[16], ps = 0.f;
 #pragma unroll
       for (int st = 0; st < 4; ++st) ka[st] = k_read(kb, kl, st);
       __builtin_amdgcn_sched_barrier(0);
@@ -678,6 +666,8 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
           va[0][st - 4] = v_read(vb, vl, 0, st - 4);
         P[2 * st] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st], p.scale_log2, nb));
         P[2 * st + 1] = __builtin_amdgcn_exp2f(fmaf(Sc[2 * st + 1], p.scale_log2, nb));
+        ps += P[2 * st];
+        ps += P[2 * st + 1];
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -687,20 +677,18 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
                        pack_bf16(P[o + 6], P[o + 7])};
       }
       __builtin_amdgcn_sched_barrier(0);
-      const u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
       // the P.V products, the next max and the running-max update run at
       // raised wave priority: this wave then wins the SIMD's issue slots over
       // the other workgroup's wave in its exponentials or load issue, and the
       // step reaches its barrier sooner (general call only; measured ~6%)
       if (NB == 1) __builtin_amdgcn_s_setprio(1);
-      L = mfma32(ones, pb[0], L);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         O[dt] = mfma32(va[0][dt], pb[0], O[dt]);
         va[1][dt] = v_read(vb, vl, 1, dt);
+        if (dt == 1) ls += ps;
         __builtin_amdgcn_sched_barrier(0);
       }
-      L = mfma32(ones, pb[1], L);
       bias = unit_max<K>(Sn, u1, pair, lane, p.scale_log2, mloc);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) O[dt] = mfma32(va[1][dt], pb[1], O[dt]);
@@ -830,7 +818,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       rep_body(std::true_type{}, kind, cur, Sc, Sn, nb);
     else
       page_body(kind, cur, Sc, Sn, nb);
-    update_max(mloc, m, L, ls, O, C);
+    update_max(mloc, m, ls, O, C);
     if (NB == 1) __builtin_amdgcn_s_setprio(0);
     u0 = u1;
     u1 = u2;
@@ -878,7 +866,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     } else {
       u32x4 pb[2], pl[2];
       probabilities<PRECISE>(Sc, nb, p.scale_log2, pb, pl, ls);
-      pv<PRECISE>(pb, pl, vslot(cur), pair, lane, L, O);
+      pv<PRECISE>(pb, pl, vslot(cur), pair, lane, O);
     }
   };
   if (i + 1 < iend) {
@@ -886,7 +874,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     S1 = s_tile(kslot((i + 1) & 1), pair, lane, qop);
     unit_pv(i & 1, S0, bias - (m == -INFINITY ? 0.0f : m));
     bias = unit_max(S1, u1, pair, lane, p.scale_log2, mloc);
-    update_max(mloc, m, L, ls, O, C);
+    update_max(mloc, m, ls, O, C);
     u0 = u1;
     wait_loads();
     __syncthreads();
@@ -916,8 +904,8 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   __syncthreads();
   // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS.
   // Lanes l and l ^ 32 hold the fp32 partial sums of one query's two 16-key
-  // halves (ls); the single-term path adds its matrix-pipe sums L.
-  float l = PRECISE ? 0.0f : L[0];
+  // halves (ls).
+  float l = 0.0f;
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls), false, false);
     l += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
