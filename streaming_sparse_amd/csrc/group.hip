@@ -234,12 +234,16 @@ __device__ __forceinline__ double sum8(double x) {
 // One level of the balanced split: each workgroup takes one group of n rows
 // of one b, in the current order (rows in[0..n) of the group), and writes
 // them stably sorted by their projection on the power-iteration direction.
-// Thread: features 4 q .. 4 q + 3 (q = tid & 7), rows tid / 8 + 32 i.
-template <int SORTN>
-__global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int groups, int src) {
+// Thread: features 4 q .. 4 q + 3 (q = tid & 7), rows tid / 8 + (THREADS / 8) i.
+// The workgroup holds the group's sort keys in LDS and passes over its rows
+// in memory seven times; THREADS / 64 waves keep that many row loads in
+// flight.
+template <int SORTN, int THREADS>
+__global__ __launch_bounds__(THREADS) void level_kernel(GroupParams p, int n, int groups, int src) {
+  constexpr int RS = THREADS / 8;   // row slots
   __shared__ unsigned long long key[SORTN];
   __shared__ unsigned short pos[SORTN];
-  __shared__ double red[32][kR + 1];
+  __shared__ double red[RS][kR + 1];
   __shared__ double vec[3][kR];   // mean, direction, scratch
   __shared__ int axis;
   const int tid = threadIdx.x, q = tid & 7, rs = tid >> 3;
@@ -253,13 +257,13 @@ __global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int gr
     __syncthreads();
     if (tid < kR) {
       double s = 0.0;
-      for (int g = 0; g < 32; ++g) s += red[g][tid];
+      for (int g = 0; g < RS; ++g) s += red[g][tid];
       vec[slot][tid] = s;
     }
     __syncthreads();
   };
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
-  for (int i = rs; i < n; i += 32) {
+  for (int i = rs; i < n; i += RS) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] += x[(long long)i * kR + 4 * q + c];
   }
@@ -272,7 +276,7 @@ __global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int gr
   // highest-variance feature (first of equals) -> one-hot start direction
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = 0.0;
-  for (int i = rs; i < n; i += 32) {
+  for (int i = rs; i < n; i += RS) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const double xc = x[(long long)i * kR + 4 * q + c] - mean[c];
@@ -300,7 +304,7 @@ __global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int gr
   for (int it = 0; it < 4; ++it) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = 0.0;
-    for (int i = rs; i < n; i += 32) {
+    for (int i = rs; i < n; i += RS) {
       double xc[4], pr = 0.0;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -320,7 +324,7 @@ __global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int gr
     __syncthreads();
   }
   // projections -> sort keys (ascending score, ties -> current position)
-  for (int i = rs; i < SORTN; i += 32) {
+  for (int i = rs; i < SORTN; i += RS) {
     if (i < n) {
       double pr = 0.0;
 #pragma unroll
@@ -338,7 +342,7 @@ __global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int gr
   __syncthreads();
   for (int kk = 2; kk <= SORTN; kk <<= 1) {
     for (int j = kk >> 1; j > 0; j >>= 1) {
-      for (int e = tid; e < SORTN / 2; e += 256) {
+      for (int e = tid; e < SORTN / 2; e += THREADS) {
         const int a = (e / j) * 2 * j + (e % j), c = a + j;
         const bool asc = (a & kk) == 0;
         const unsigned long long ka = key[a], kc = key[c];
@@ -356,7 +360,7 @@ __global__ __launch_bounds__(256) void level_kernel(GroupParams p, int n, int gr
   }
   double* xo = p.x[src ^ 1] + row0 * kR;
   int32_t* io = p.ids[src ^ 1] + row0;
-  for (int j = rs; j < n; j += 32) {
+  for (int j = rs; j < n; j += RS) {
     const int s = pos[j];
 #pragma unroll
     for (int c = 0; c < 4; ++c) xo[(long long)j * kR + 4 * q + c] = x[(long long)s * kR + 4 * q + c];
@@ -597,8 +601,8 @@ int ssa_group_order(const void* k, const void* v, long long layer_stride, long l
   // buffers 0 -> 1 -> 0; levels 2..6 inside each 512-row group, which
   // writes the order (or the frame partition's input)
   int32_t* last_out = first_chunk ? p.ids[1] : order;
-  hipLaunchKernelGGL(level_kernel<8192>, dim3(p.B), dim3(256), 0, stream, p, kTokens, 1, 0);
-  hipLaunchKernelGGL(level_kernel<2048>, dim3(p.B * 3), dim3(256), 0, stream, p, kTokens / 3, 3, 1);
+  hipLaunchKernelGGL((level_kernel<8192, 1024>), dim3(p.B), dim3(1024), 0, stream, p, kTokens, 1, 0);
+  hipLaunchKernelGGL((level_kernel<2048, 512>), dim3(p.B * 3), dim3(512), 0, stream, p, kTokens / 3, 3, 1);
   hipLaunchKernelGGL(fused_levels_kernel, dim3(p.B * (kTokens / kFuse)), dim3(kFuseThreads), 0, stream, p, 0,
                      last_out);
   if (first_chunk) hipLaunchKernelGGL(frames_kernel, dim3(p.B), dim3(256), 0, stream, p.ids[1], order);
