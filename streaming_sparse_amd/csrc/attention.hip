@@ -309,19 +309,37 @@ __device__ __forceinline__ float unit_max(f32x16& S, int e, int pair, int lane, 
 // (log2 units), so probabilities stay below 2^kSlack and the rescale is rare.
 constexpr float kSlack = 8.0f;
 
+// The running max m of a lane.  With KEEP, two values are kept beside it,
+// so that a step reads them instead of re-forming them: neg = -m (0 while
+// m = -inf), the exponent offset of the probabilities, and thr = m +
+// kSlack (2 VGPRs that the two-term general call has no room for; it
+// re-forms them, with the same results).
+template <bool KEEP>
+struct RunMax {
+  float m = -INFINITY, neg_ = 0.0f, thr_ = -INFINITY;
+  __device__ __forceinline__ float neg() const { return KEEP ? neg_ : -(m == -INFINITY ? 0.0f : m); }
+  __device__ __forceinline__ float thr() const { return KEEP ? thr_ : m + kSlack; }
+};
+
 // `ls` is a lane's fp32 partial denominator (the sum of the fp32
 // probabilities of its keys, in either arithmetic, as the reference's l).
 // C holds the code accumulator in items 0..3 (ranks 4 hh + i).
-__device__ __forceinline__ void update_max(float mloc, float& m, float& ls, f32x16 (&O)[4], f32x16& C) {
-  if (__any(mloc > m + kSlack)) {
-    const float mnew = fmaxf(m, mloc);
-    const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
+template <bool KEEP>
+__device__ __forceinline__ void update_max(float mloc, RunMax<KEEP>& r, float& ls, f32x16 (&O)[4], f32x16& C) {
+  if (__any(mloc > r.thr())) {
+    const float mnew = fmaxf(r.m, mloc);
+    const float mu = mnew == -INFINITY ? 0.0f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(r.m - mu);
     ls *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) O[dt] *= alpha;
 #pragma unroll
     for (int i = 0; i < 4; ++i) C[i] *= alpha;
-    m = mnew;
+    r.m = mnew;
+    if (KEEP) {
+      r.neg_ = -mu;
+      r.thr_ = mnew + kSlack;
+    }
   }
 }
 
@@ -540,7 +558,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   auto kslot = [&](int slot) { return kbase + slot * kBuf; };
   auto vslot = [&](int slot) { return vbase + slot * kBuf; };
 
-  float m = -INFINITY;
+  RunMax<!(PRECISE && NB == 1)> rm;
   f32x16 O[4], C = {};
   float ls = 0.f;
 #pragma unroll
@@ -563,7 +581,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   f32x16 S0 = s_tile(kslot(ibeg & 1), pair, lane, qop), S1;
   float mloc;
   float bias = unit_max(S0, unit(ibeg), pair, lane, p.scale_log2, mloc);
-  update_max(mloc, m, ls, O, C);
+  update_max(mloc, rm, ls, O, C);
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
   // Unit ids run ahead in registers (u0 = unit i); the id of unit i+3 is
   // read from LDS in step i-1, so the read completes at its barrier.
@@ -577,12 +595,11 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     const lds_u8* kb = kslot(cur ^ 1);
     const lds_u8* vb = vslot(cur);
     uint32_t kl = klane, vl = vlane;
-    // the two-term kernel has the registers to keep its 8 K read addresses
-    // across units; the single-term one re-forms them each step
-    if (PRECISE)
-      asm volatile("" : "+v"(vl));
-    else
-      asm volatile("" : "+v"(kl), "+v"(vl));
+    // the 8 K read addresses stay in registers across units; the general
+    // call re-forms its 4 V read addresses each step (the two-block call,
+    // with registers to spare, keeps those too: 10 fewer vector
+    // instructions per step)
+    if (NB == 1) asm volatile("" : "+v"(vl));
     if (PRECISE) {
       // Two-term P.V in three stages of 8 matrix products, each carrying a
       // similar share of the vector work, so that the matrix and vector
@@ -813,12 +830,12 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       issue_rows<NB, K>(p, src, u2, 0, wave, lane, page_off, rep_off, kslot(cur));
       issue_rows<NB, K>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot(cur ^ 1));
     }
-    const float nb = bias - (m == -INFINITY ? 0.0f : m);
+    const float nb = bias + rm.neg();
     if constexpr (NB == 1 && KP == 1)
       rep_body(std::true_type{}, kind, cur, Sc, Sn, nb);
     else
       page_body(kind, cur, Sc, Sn, nb);
-    update_max(mloc, m, ls, O, C);
+    update_max(mloc, rm, ls, O, C);
     if (NB == 1) __builtin_amdgcn_s_setprio(0);
     u0 = u1;
     u1 = u2;
@@ -872,9 +889,9 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   if (i + 1 < iend) {
     issue_rows<NB>(p, src, u1, 1, wave, lane, page_off, rep_off, vslot((i + 1) & 1));
     S1 = s_tile(kslot((i + 1) & 1), pair, lane, qop);
-    unit_pv(i & 1, S0, bias - (m == -INFINITY ? 0.0f : m));
+    unit_pv(i & 1, S0, bias + rm.neg());
     bias = unit_max(S1, u1, pair, lane, p.scale_log2, mloc);
-    update_max(mloc, m, ls, O, C);
+    update_max(mloc, rm, ls, O, C);
     u0 = u1;
     wait_loads();
     __syncthreads();
@@ -890,7 +907,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) bop[dt] = ldg16(bp + 256 * dt);
     }
-    unit_pv(i & 1, S0, bias - (m == -INFINITY ? 0.0f : m));
+    unit_pv(i & 1, S0, bias + rm.neg());
     if constexpr (NB == 1) {
       // O^T += basis . C^T: the two-term operand of C holds the lo parts of
       // ranks 0..7 in k 0..7 and the hi parts in k 8..15
@@ -918,12 +935,13 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) d[(16 * dt + i) * 64] = O[dt][i];
-    xm[grp][qw][lane] = m;
+    xm[grp][qw][lane] = rm.m;
     xl[grp][qw][lane] = l;
   }
   __syncthreads();
   if (pair == 1) return;
   const float m1 = xm[grp][qw][lane], l1 = xl[grp][qw][lane];
+  const float m = rm.m;
   const float mt = fmaxf(m, m1);
   const float mu = mt == -INFINITY ? 0.0f : mt;
   const float a0 = __builtin_amdgcn_exp2f(m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
