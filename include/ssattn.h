@@ -26,6 +26,8 @@
  *   ssa_summary     <- the current-chunk summary recompute of VideoRuntime.forward
  *                      (VR/runtime.py:213-227; VR/summary_moments.py:113-137), with
  *                      k-means clusters as the token groups of RV/ops.py:43-76
+ *   ssa_summary_write <- the same, fused with the window write of the chunk's
+ *                      K/V before it (VR/runtime.py:205-206)
  *   ssa_pset        <- the Full_Pset branch of BatchGraphs.compute
  *                      (VB/graph.py:169-208): quota_pool.pool, read /
  *                      compact_scores (VR/page.py:17-21, VR/reader_reduce.py:150-190,
@@ -182,6 +184,21 @@ int ssa_select(const float* scores, const int32_t* own, const uint8_t* valid, in
 int ssa_summary(const void* k, const void* v, long long kv_token_stride, long long kv_head_stride,
                 const int32_t* init, const void* basis, void* keys, void* mean, void* detail, void* stats,
                 int head_pages, int heads, int first_page, int pages, int iters, hipStream_t stream);
+
+/* ssa_summary with the chunk's K/V written into the cache on the way:
+ * page first_page + i of k, v (strides kv_*) receives rows 64 i .. 64 i + 63
+ * of src_k, src_v (token stride src_token_stride, head stride
+ * src_head_stride, in elements), and the summaries of those pages are
+ * formed from the rows read.  Replaces the window write of the chunk's K/V
+ * (key_window.copy_(k), value_window.copy_(v), VR/runtime.py:205-206)
+ * followed by the summary recompute from k, v (VR/runtime.py:213-227): one
+ * pass over the rows instead of a copy and a re-read.  Cache and summaries
+ * equal a copy followed by ssa_summary, bit for bit.  src must not overlap
+ * the cache pages it fills. */
+int ssa_summary_write(const void* src_k, const void* src_v, long long src_token_stride, long long src_head_stride,
+                      void* k, void* v, long long kv_token_stride, long long kv_head_stride, const int32_t* init,
+                      const void* basis, void* keys, void* mean, void* detail, void* stats, int head_pages,
+                      int heads, int first_page, int pages, int iters, hipStream_t stream);
 
 /* Full_Pset page encodings of pages [first_page, first_page + pages) of the
  * summary slab (keys/mean/detail/stats as in ssa_route, capacity head_pages):

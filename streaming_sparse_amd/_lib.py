@@ -27,6 +27,8 @@ SIGNATURES = {
     "ssa_encode": [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                    _i, _vp],
     "ssa_summary": [_vp, _vp, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "ssa_summary_write": [_vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                          _vp],
     "ssa_pset": [_vp, _ll, _ll, _ll, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                  _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "ssa_anchor_rebase": [_vp, _ll, _ll, _vp, _ll, _ll, _vp, _i, _i, _i, _vp],

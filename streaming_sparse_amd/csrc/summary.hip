@@ -19,6 +19,10 @@
 // 2 lane, 2 lane + 1) accumulates over the cluster's member tokens in
 // ascending token order, from a wave-uniform membership mask.  LDS stays
 // under 40 KB so four workgroups share a CU.
+//
+// ssa_summary_write reads the page rows from the chunk's K/V instead and
+// writes them into the cache in the same pass (the window write that
+// precedes the summary recompute, VR/runtime.py:205-206).
 #include "common.h"
 
 using namespace ssa;
@@ -30,6 +34,11 @@ constexpr float kHaar[3][4] = {{1, 1, -1, -1}, {1, -1, 1, -1}, {1, -1, -1, 1}};
 struct SummaryParams {
   const uint16_t *k, *v;
   long long kv_tok, kv_head;
+  // write-through (src_k non-null): page pl's 64 rows are read from
+  // src_k / src_v tokens 64 pl .. 64 pl + 63 and written to the cache
+  // (k, v) at page first + pl before the summary is formed from them
+  const uint16_t *src_k, *src_v;
+  long long src_tok, src_head;
   const int32_t* init;          // [H, pages, 4] initial tokens
   const uint16_t* basis;        // [H, 128, 8]
   uint16_t *keys, *mean, *detail, *stats;
@@ -96,13 +105,22 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p) {
   }
   float kr[32];
   {
-    const uint16_t* kp = p.k + base + lane * p.kv_tok + 32 * wave;
-    const uint16_t* vp = p.v + base + lane * p.kv_tok + 32 * wave;
+    const long long crow = base + lane * p.kv_tok + 32 * wave;
+    const long long srow = ((long long)pl * 64 + lane) * p.src_tok + (long long)h * p.src_head + 32 * wave;
+    const uint16_t* kp = p.src_k ? p.src_k + srow : p.k + crow;
+    const uint16_t* vp = p.src_k ? p.src_v + srow : p.v + crow;
     u32x4 a[4], b[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       a[j] = ldg16(kp + 8 * j);
       b[j] = ldg16(vp + 8 * j);
+    }
+    if (p.src_k) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.k) + crow + 8 * j) = a[j];
+        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.v) + crow + 8 * j) = b[j];
+      }
     }
     float vn = 0.f;
 #pragma unroll
@@ -329,13 +347,11 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p) {
   }
 }
 
-}  // namespace
-
-extern "C" {
-
-int ssa_summary(const void* k, const void* v, long long kv_token_stride, long long kv_head_stride,
-                const int32_t* init, const void* basis, void* keys, void* mean, void* detail, void* stats,
-                int head_pages, int heads, int first_page, int pages, int iters, hipStream_t stream) {
+// Both entry points: src_k null reads the pages from the cache itself.
+int summary_launch(const void* src_k, const void* src_v, long long src_token_stride, long long src_head_stride,
+                   const void* k, const void* v, long long kv_token_stride, long long kv_head_stride,
+                   const int32_t* init, const void* basis, void* keys, void* mean, void* detail, void* stats,
+                   int head_pages, int heads, int first_page, int pages, int iters, hipStream_t stream) {
   if (heads <= 0 || pages <= 0 || first_page < 0 || first_page + pages > head_pages || iters < 1 ||
       init == nullptr)
     return (int)hipErrorInvalidValue;
@@ -344,6 +360,10 @@ int ssa_summary(const void* k, const void* v, long long kv_token_stride, long lo
   p.v = (const uint16_t*)v;
   p.kv_tok = kv_token_stride;
   p.kv_head = kv_head_stride;
+  p.src_k = (const uint16_t*)src_k;
+  p.src_v = (const uint16_t*)src_v;
+  p.src_tok = src_token_stride;
+  p.src_head = src_head_stride;
   p.init = init;
   p.basis = (const uint16_t*)basis;
   p.keys = (uint16_t*)keys;
@@ -356,6 +376,26 @@ int ssa_summary(const void* k, const void* v, long long kv_token_stride, long lo
   p.iters = iters;
   hipLaunchKernelGGL(summary_kernel, dim3(pages, heads), dim3(256), 0, stream, p);
   return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssa_summary(const void* k, const void* v, long long kv_token_stride, long long kv_head_stride,
+                const int32_t* init, const void* basis, void* keys, void* mean, void* detail, void* stats,
+                int head_pages, int heads, int first_page, int pages, int iters, hipStream_t stream) {
+  return summary_launch(nullptr, nullptr, 0, 0, k, v, kv_token_stride, kv_head_stride, init, basis, keys, mean,
+                        detail, stats, head_pages, heads, first_page, pages, iters, stream);
+}
+
+int ssa_summary_write(const void* src_k, const void* src_v, long long src_token_stride, long long src_head_stride,
+                      void* k, void* v, long long kv_token_stride, long long kv_head_stride, const int32_t* init,
+                      const void* basis, void* keys, void* mean, void* detail, void* stats, int head_pages,
+                      int heads, int first_page, int pages, int iters, hipStream_t stream) {
+  if (src_k == nullptr || src_v == nullptr || k == nullptr || v == nullptr) return (int)hipErrorInvalidValue;
+  return summary_launch(src_k, src_v, src_token_stride, src_head_stride, k, v, kv_token_stride, kv_head_stride,
+                        init, basis, keys, mean, detail, stats, head_pages, heads, first_page, pages, iters, stream);
 }
 
 }  // extern "C"

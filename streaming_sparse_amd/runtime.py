@@ -301,32 +301,33 @@ class StreamRuntime:
 
     def layer_call(self, step: int, layer: int, q, k, v):
         """One attention call of the current chunk: the chunk's K/V written into
-        the window, then a dense or sparse call (the clean step's commits
+        the window (a sparse call writes them in the pass of its current-page
+        summaries), then a dense or sparse call (the clean step's commits
         follow all its calls, see commit_chunk)."""
         cfg, L = self.cfg, self.layers[layer]
         n = self.ring.n
         P = n + CURRENT
         tok0 = 64 * n
-        L.k[0, tok0:tok0 + self.N].copy_(k)
-        L.v[0, tok0:tok0 + self.N].copy_(v)
         kw = L.k[:, :64 * P]
         vw = L.v[:, :64 * P]
         s = L.slab.slice(0, P)
         clean = step == cfg.steps
         if clean or layer == 0 or self.dense_window():
+            L.k[0, tok0:tok0 + self.N].copy_(k)
+            L.v[0, tok0:tok0 + self.N].copy_(v)
             out = attention(q, kw, vw, s, L.basis, self.dense_ids(P), self.ws, all_pages=True, single_av=True)
             self.calls['dense'] += 1
         else:
-            out = self.sparse_call(step, layer, q, kw, vw, P)
+            out = self.sparse_call(step, layer, q, kw, vw, P, (k, v))
         self.last = dict(step=step, layer=layer, pages=P, out=out)
         if self.record is not None:
             self.record.append(out.clone())
         return out
 
-    def sparse_call(self, step, layer, q, kw, vw, P):
+    def sparse_call(self, step, layer, q, kw, vw, P, src):
         cfg, L = self.cfg, self.layers[layer]
         correct = cfg.tier == 'intersection' and L.encoding is not None and step in cfg.pset_steps
-        summary.build(L.k, L.v, L.basis, self.init, L.slab, P - CURRENT, CURRENT)
+        summary.build(L.k, L.v, L.basis, self.init, L.slab, P - CURRENT, CURRENT, src=src)
         s = L.slab.slice(0, P)
         ops = self.ws.tensor('rt_rep_ops', (self.H, rep_tiles(P), REP_OP_ELEMS), q.device, torch.bfloat16)
         if cfg.tier == 'base':

@@ -23,15 +23,27 @@ _SLAB = (('keys', (4, 128), (512, 128, 1)), ('mean', (128,), (128, 1)), ('detail
 
 
 @torch.no_grad()
-def build(k, v, basis, init, out: Summary, first: int, pages: int, iters: int = 4) -> Summary:
+def build(k, v, basis, init, out: Summary, first: int, pages: int, iters: int = 4, src=None) -> Summary:
     """k, v [1, 64P, H, 128] bf16 cache; basis [H,128,8]; init [H, pages, 4]
     initial k-means tokens (0..63) per page; out: a summary slab (or prefix
-    slice) whose pages [first, first + pages) are overwritten."""
+    slice) whose pages [first, first + pages) are overwritten.
+
+    src = (src_k, src_v), each [64 pages, H, 128] bf16 with unit head-dim
+    stride: those rows are first written into the cache pages [first, first
+    + pages) (the window write of VR/runtime.py:205-206) in the same pass
+    that summarises them (ssa_summary_write); cache and summaries equal a
+    copy followed by the summary, bit for bit."""
     _, L, h, d = k.shape
     if d != HEAD_DIM or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or k.shape != v.shape:
         raise ValueError("k, v must be bf16 [1, 64P, H, 128]")
     if first < 0 or pages <= 0 or (first + pages) * 64 > L:
         raise ValueError("page range outside the K/V window")
+    if src is not None:
+        sk, sv = src
+        if sk.shape != (64 * pages, h, d) or sv.shape != sk.shape or sk.dtype != torch.bfloat16 or \
+                sv.dtype != torch.bfloat16 or sk.stride() != sv.stride() or sk.stride(2) != 1 or \
+                sk.device != k.device or sv.device != k.device:
+            raise ValueError("src must be two bf16 [64*pages, H, 128] tensors with equal strides on the cache device")
     hp = out.head_pages
     for name, shape, strides in _SLAB:
         t = getattr(out, name)
@@ -45,6 +57,13 @@ def build(k, v, basis, init, out: Summary, first: int, pages: int, iters: int = 
         raise ValueError("init must be [H, pages, 4]")
     b = basis if (basis.dtype == torch.bfloat16 and basis.is_contiguous()) else basis.to(torch.bfloat16).contiguous()
     tok, head = kv_strides(k, v)
+    if src is not None:
+        _lib.check(_lib.lib().ssa_summary_write(_lib.ptr(sk), _lib.ptr(sv), sk.stride(0), sk.stride(1), _lib.ptr(k),
+                                                _lib.ptr(v), tok, head, _lib.ptr(ini), _lib.ptr(b), _lib.ptr(out.keys),
+                                                _lib.ptr(out.mean), _lib.ptr(out.detail), _lib.ptr(out.stats), hp, h,
+                                                first, pages, iters, _lib.stream_handle(k.device)),
+                   "ssa_summary_write")
+        return out
     _lib.check(_lib.lib().ssa_summary(_lib.ptr(k), _lib.ptr(v), tok, head, _lib.ptr(ini), _lib.ptr(b),
                                       _lib.ptr(out.keys), _lib.ptr(out.mean), _lib.ptr(out.detail),
                                       _lib.ptr(out.stats), hp, h, first, pages, iters,

@@ -43,3 +43,39 @@ def test_current_chunk_summaries_match_oracle(device):
     # pages outside the range are untouched
     for f in Summary.FIELDS:
         assert torch.equal(getattr(slab, f)[:, :P - 72].cpu(), getattr(x.summary, f)[:, :P - 72])
+
+
+def test_summary_write_through_equals_copy_then_summary(device):
+    """ssa_summary_write: the chunk's K/V written into the cache pages in the
+    pass that summarises them gives the cache and the summaries of a copy
+    followed by ssa_summary, bit for bit; pages outside the range stay as
+    they were.  Sources: a fresh [4608, H, 128] chunk and a strided view
+    (every other token row of a larger buffer)."""
+    x = workload.make_call(cfg=3, frames=18)
+    P = x.pages
+    g = x.to(device)
+    init = workload.kmeans_init(12, 72, torch.Generator().manual_seed(11)).to(device)
+    gen = torch.Generator(device=device).manual_seed(5)
+    big_k = torch.randn(2 * 4608, 12, 128, generator=gen, device=device).to(torch.bfloat16)
+    big_v = torch.randn(2 * 4608, 12, 128, generator=gen, device=device).to(torch.bfloat16)
+    for name, sk, sv in (("contiguous", big_k[:4608], big_v[:4608]), ("strided", big_k[::2], big_v[::2])):
+        outs = []
+        for fused in (False, True):
+            k, v = g.k.clone(), g.v.clone()
+            slab = Summary(*(getattr(g.summary, f).clone() for f in Summary.FIELDS))
+            if fused:
+                summary.build(k, v, g.basis, init, slab, P - 72, 72, src=(sk, sv))
+            else:
+                k[0, 64 * (P - 72):].copy_(sk)
+                v[0, 64 * (P - 72):].copy_(sv)
+                summary.build(k, v, g.basis, init, slab, P - 72, 72)
+            outs.append((k, v, slab))
+        torch.cuda.synchronize()
+        (k0, v0, s0), (k1, v1, s1) = outs
+        same_kv = torch.equal(k0.view(torch.int16), k1.view(torch.int16)) and \
+            torch.equal(v0.view(torch.int16), v1.view(torch.int16))
+        same_s = all(torch.equal(getattr(s0, f).view(torch.int16), getattr(s1, f).view(torch.int16))
+                     for f in Summary.FIELDS)
+        print(f"{name}: cache equal {same_kv}, summaries equal {same_s}", flush=True)
+        assert same_kv and same_s
+        assert torch.equal(k1[0, :64 * (P - 72)].view(torch.int16), g.k[0, :64 * (P - 72)].view(torch.int16))

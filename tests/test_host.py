@@ -187,6 +187,11 @@ def test_c_abi_rejects_bad_shapes():
     assert sm(400, 72, 4, 16) == INVALID
     assert sm(360, 72, 0, 16) == INVALID
     assert sm(360, 72, 4, None) == INVALID
+    # ssa_summary_write: both sources and both cache tensors given, same range checks
+    sw = lambda sk, first: L.ssa_summary_write(sk, 16, 1536, 128, 16, 16, 1536, 128, 16, N, N, N, N, N, 432, 12,
+                                               first, 72, 4, N)
+    assert sw(None, 360) == INVALID
+    assert sw(16, 400) == INVALID
     # ssa_encode: hidden width <= 256, page range inside both slabs
     en = lambda pages, hidden: L.ssa_encode(N, N, N, N, 432, N, N, N, N, N, N, N, N, N, N, N, 432, 12, 360, pages,
                                             hidden, N)
