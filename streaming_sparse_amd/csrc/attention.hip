@@ -819,10 +819,10 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   // (before the last products, so it does not wait behind them in the matrix
   // pipe).  KP: the kind of unit i (page or rep tile); K: that of units
   // i+1 and i+2.
-  auto step = [&](auto pvkind, auto kind, int i, f32x16& Sc, f32x16& Sn) {
+  auto step = [&](auto pvkind, auto kind, auto parity, int i, f32x16& Sc, f32x16& Sn) {
     constexpr int KP = decltype(pvkind)::value;
     constexpr int K = decltype(kind)::value;
-    const int cur = i & 1;
+    constexpr int cur = decltype(parity)::value;   // i & 1: every paired loop keeps i even
     const int u3 = __builtin_amdgcn_readfirstlane(u3raw);
     // the general call issues its loads first; the two-block call (8 waves,
     // half the loads each) spreads them over the first products
@@ -850,26 +850,28 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   using PageUnits = std::integral_constant<int, 0>;
   using RepUnits = std::integral_constant<int, 1>;
   using AnyUnits = std::integral_constant<int, 2>;
+  using Even = std::integral_constant<int, 0>;
+  using Odd = std::integral_constant<int, 1>;
   const int npages = nexact_s;
   int i = ibeg;
   for (; i + 2 < iend && i + 3 < npages; i += 2) {
-    step(PageUnits{}, PageUnits{}, i, S0, S1);
-    step(PageUnits{}, PageUnits{}, i + 1, S1, S0);
+    step(PageUnits{}, PageUnits{}, Even{}, i, S0, S1);
+    step(PageUnits{}, PageUnits{}, Odd{}, i + 1, S1, S0);
   }
   for (; i + 2 < iend && i + 1 < npages; i += 2) {
-    step(PageUnits{}, AnyUnits{}, i, S0, S1);
-    step(PageUnits{}, AnyUnits{}, i + 1, S1, S0);
+    step(PageUnits{}, AnyUnits{}, Even{}, i, S0, S1);
+    step(PageUnits{}, AnyUnits{}, Odd{}, i + 1, S1, S0);
   }
   if constexpr (NB == 1) {
     // here unit i+1 is a rep tile; unit i is the last page when npages is odd
     if (i + 2 < iend && i < npages) {
-      step(PageUnits{}, RepUnits{}, i, S0, S1);
-      step(RepUnits{}, RepUnits{}, i + 1, S1, S0);
+      step(PageUnits{}, RepUnits{}, Even{}, i, S0, S1);
+      step(RepUnits{}, RepUnits{}, Odd{}, i + 1, S1, S0);
       i += 2;
     }
     for (; i + 2 < iend; i += 2) {
-      step(RepUnits{}, RepUnits{}, i, S0, S1);
-      step(RepUnits{}, RepUnits{}, i + 1, S1, S0);
+      step(RepUnits{}, RepUnits{}, Even{}, i, S0, S1);
+      step(RepUnits{}, RepUnits{}, Odd{}, i + 1, S1, S0);
     }
   }
   // one unit with a successor left (units i and i+1 = iend - 1): the same
