@@ -194,7 +194,8 @@ int ssa_summary(const void* k, const void* v, long long kv_token_stride, long lo
  * followed by the summary recompute from k, v (VR/runtime.py:213-227): one
  * pass over the rows instead of a copy and a re-read.  Cache and summaries
  * equal a copy followed by ssa_summary, bit for bit.  src must not overlap
- * the cache pages it fills. */
+ * the cache pages it fills; sources and cache 16-byte aligned, strides
+ * multiples of 8 elements. */
 int ssa_summary_write(const void* src_k, const void* src_v, long long src_token_stride, long long src_head_stride,
                       void* k, void* v, long long kv_token_stride, long long kv_head_stride, const int32_t* init,
                       const void* basis, void* keys, void* mean, void* detail, void* stats, int head_pages,

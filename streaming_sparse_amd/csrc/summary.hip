@@ -355,6 +355,10 @@ int summary_launch(const void* src_k, const void* src_v, long long src_token_str
   if (heads <= 0 || pages <= 0 || first_page < 0 || first_page + pages > head_pages || iters < 1 ||
       init == nullptr)
     return (int)hipErrorInvalidValue;
+  // the written-through rows move in 16-byte pieces
+  if (src_k && ((((uintptr_t)src_k | (uintptr_t)src_v | (uintptr_t)k | (uintptr_t)v) & 15) ||
+                ((src_token_stride | src_head_stride | kv_token_stride | kv_head_stride) & 7)))
+    return (int)hipErrorInvalidValue;
   SummaryParams p;
   p.k = (const uint16_t*)k;
   p.v = (const uint16_t*)v;

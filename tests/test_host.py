@@ -192,6 +192,7 @@ def test_c_abi_rejects_bad_shapes():
                                                first, 72, 4, N)
     assert sw(None, 360) == INVALID
     assert sw(16, 400) == INVALID
+    assert sw(8, 360) == INVALID                                       # source rows not 16-byte aligned
     # ssa_encode: hidden width <= 256, page range inside both slabs
     en = lambda pages, hidden: L.ssa_encode(N, N, N, N, 432, N, N, N, N, N, N, N, N, N, N, N, 432, 12, 360, pages,
                                             hidden, N)
