@@ -201,6 +201,19 @@ int ssa_summary_write(const void* src_k, const void* src_v, long long src_token_
                       const void* basis, void* keys, void* mean, void* detail, void* stats, int head_pages,
                       int heads, int first_page, int pages, int iters, hipStream_t stream);
 
+/* ssa_summary over `layers` (1..32) layers in one launch: k[l], v[l] (the
+ * layer's cache, all with the same strides), basis[l] and the slab fields
+ * keys[l], mean[l], detail[l], stats[l] (all with capacity head_pages) are
+ * host arrays of the layers' device pointers; init, the page range and the
+ * iterations are shared.  No counterpart in the reference, which summarises
+ * layer by layer (the commit's VR/runtime.py:356-370, the anchor rebase's
+ * VB/phase.py:4-25): for callers that refresh many layers at once.  Equal to
+ * one ssa_summary per layer, bit for bit. */
+int ssa_summary_layers(int layers, const void* const* k, const void* const* v, long long kv_token_stride,
+                       long long kv_head_stride, const int32_t* init, const void* const* basis, void* const* keys,
+                       void* const* mean, void* const* detail, void* const* stats, int head_pages, int heads,
+                       int first_page, int pages, int iters, hipStream_t stream);
+
 /* Full_Pset page encodings of pages [first_page, first_page + pages) of the
  * summary slab (keys/mean/detail/stats as in ssa_route, capacity head_pages):
  * coef [H,enc_pages,128] bf16 = co[85] (reader, [5,17]) | 11 zeros | A[32]
@@ -214,6 +227,19 @@ int ssa_encode(const void* keys, const void* mean, const void* detail, const voi
                const float* w2_phi, const float* b2_phi, const double* B, void* coef, double* mean_b,
                double* detail_b, int enc_pages, int heads, int first_page, int pages, int hidden,
                hipStream_t stream);
+
+/* ssa_encode over `layers` (1..32) layers in one launch: the slab fields,
+ * the basis and the encodings coef, mean_b, detail_b are host arrays of the
+ * layers' device pointers (equal capacities), the weights are shared.  No
+ * counterpart in the reference, which encodes layer by layer
+ * (VR/runtime.py:160-164 per layer): for callers that refresh many layers at
+ * once.  Equal to one ssa_encode per layer, bit for bit. */
+int ssa_encode_layers(int layers, const void* const* keys, const void* const* mean, const void* const* detail,
+                      const void* const* stats, int head_pages, const void* const* basis, const float* w1t,
+                      const float* b1, const float* w2_reader, const float* b2_reader, const float* w2_phi,
+                      const float* b2_phi, const double* B, void* const* coef, double* const* mean_b,
+                      double* const* detail_b, int enc_pages, int heads, int first_page, int pages, int hidden,
+                      hipStream_t stream);
 
 /* Full_Pset swap correction of the heads listed in heads[n_heads] (indices
  * into total_heads), after ssa_route in mode 1 produced risk, mask and ids.
@@ -256,6 +282,16 @@ int ssa_anchor_rebase(const void* src, long long src_token_stride, long long src
                       long long dst_token_stride, long long dst_head_stride, const double* phase, int pairs,
                       int tokens, int heads, hipStream_t stream);
 
+/* ssa_anchor_rebase over `layers` (1..32) layers in one launch: src[l] and
+ * dst[l] are host arrays of the layers' device pointers (equal strides), the
+ * phase is shared.  No counterpart in the reference, which rebases layer by
+ * layer (VB/phase.py:4-25): for callers that rebase every layer at a chunk
+ * boundary.  Equal to one ssa_anchor_rebase per layer, bit for bit. */
+int ssa_anchor_rebase_layers(int layers, const void* const* src, long long src_token_stride,
+                             long long src_head_stride, void* const* dst, long long dst_token_stride,
+                             long long dst_head_stride, const double* phase, int pairs, int tokens, int heads,
+                             hipStream_t stream);
+
 /* Commit of a chunk's pages into the ring slots of the resident K/V cache
  * (RV/runtime.py:22-55 PageStore.commit / commit_indexed): row r of
  * destination page slots[p] (p < chunk_pages, slots[p] < dst_pages) takes
@@ -267,6 +303,18 @@ int ssa_commit_pages(const void* k_src, const void* v_src, long long src_token_s
                      const int32_t* order, int chunk_pages, const int32_t* slots, int dst_pages, void* k_dst,
                      void* v_dst, long long dst_token_stride, long long dst_head_stride, int heads,
                      hipStream_t stream);
+
+/* ssa_commit_pages over `layers` (1..32) layers in one launch: k_src[l],
+ * v_src[l], order[l] (NULL entries: token order), k_dst[l], v_dst[l] are host
+ * arrays of the layers' device pointers (equal strides), the slots are
+ * shared.  No counterpart in the reference, which commits layer by layer
+ * (VR/runtime.py:356-370): for callers that commit every layer at the clean
+ * step.  Equal to one ssa_commit_pages per layer, bit for bit. */
+int ssa_commit_pages_layers(int layers, const void* const* k_src, const void* const* v_src,
+                            long long src_token_stride, long long src_head_stride, const int32_t* const* order,
+                            int chunk_pages, const int32_t* slots, int dst_pages, void* const* k_dst,
+                            void* const* v_dst, long long dst_token_stride, long long dst_head_stride, int heads,
+                            hipStream_t stream);
 
 /* Clean-commit token grouping (RV/runtime.py:57-68 GroupingOps.group with the
  * features of LE/all_sparse_model.py:16-23, LE/response_hard.py:20-31

@@ -27,6 +27,11 @@ SIGNATURES = {
     "ssa_encode": [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                    _i, _vp],
     "ssa_summary": [_vp, _vp, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "ssa_summary_layers": [_i, _vp, _vp, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "ssa_encode_layers": [_i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                          _i, _i, _i, _i, _vp],
+    "ssa_anchor_rebase_layers": [_i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _i, _i, _i, _vp],
+    "ssa_commit_pages_layers": [_i, _vp, _vp, _ll, _ll, _vp, _i, _vp, _i, _vp, _vp, _ll, _ll, _i, _vp],
     "ssa_summary_write": [_vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                           _vp],
     "ssa_pset": [_vp, _ll, _ll, _ll, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
@@ -55,6 +60,12 @@ def lib():
 
 def ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def ptrs(tensors):
+    """A host array of the tensors' device pointers (None -> NULL), for the
+    entries that take one tensor per layer."""
+    return (ctypes.c_void_p * len(tensors))(*[None if t is None else t.data_ptr() for t in tensors])
 
 
 def stream_handle(device=None):

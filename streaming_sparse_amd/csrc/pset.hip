@@ -24,6 +24,7 @@
 #include "common.h"
 
 #include <mutex>
+#include <type_traits>
 
 using namespace ssa;
 
@@ -55,13 +56,36 @@ struct EncodeParams {
   int EP, first, pages, hidden;
 };
 
+// Per-layer tensors of a batched encode (blockIdx.z = layer): the summary
+// slab, the basis and the encodings of each layer; the weights are shared.
+constexpr int kMaxLayers = 32;
+struct EncodeLayers {
+  const uint16_t *keys[kMaxLayers], *mean[kMaxLayers], *detail[kMaxLayers], *stats[kMaxLayers],
+      *basis[kMaxLayers];
+  uint16_t* coef[kMaxLayers];
+  double *mean_b[kMaxLayers], *detail_b[kMaxLayers];
+};
+struct OneLayer {};
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   return v;
 }
 
-__global__ __launch_bounds__(256) void encode_kernel(EncodeParams p) {
+template <class Layers>
+__global__ __launch_bounds__(256) void encode_kernel(EncodeParams p, Layers layers) {
+  if constexpr (std::is_same_v<Layers, EncodeLayers>) {
+    const int l = blockIdx.z;
+    p.keys = layers.keys[l];
+    p.mean = layers.mean[l];
+    p.detail = layers.detail[l];
+    p.stats = layers.stats[l];
+    p.basis = layers.basis[l];
+    p.coef = layers.coef[l];
+    p.mean_b = layers.mean_b[l];
+    p.detail_b = layers.detail_b[l];
+  }
   __shared__ alignas(16) float f[kFeatures][kEncPages];
   __shared__ alignas(16) float hid[2 * kMaxHidden][kEncPages];
   __shared__ double pb[8][16];
@@ -898,15 +922,13 @@ __global__ __launch_bounds__(256) void pset_scores_kernel(PsetParams p) {
   for (int i = 1 + nsel + tid; i < p.C; i += 256) ids[i] = -1;
 }
 
-}  // namespace
-
-extern "C" {
-
-int ssa_encode(const void* keys, const void* mean, const void* detail, const void* stats, int head_pages,
-               const void* basis, const float* w1t, const float* b1, const float* w2_reader, const float* b2_reader,
-               const float* w2_phi, const float* b2_phi, const double* B, void* coef, double* mean_b,
-               double* detail_b, int enc_pages, int heads, int first_page, int pages, int hidden,
-               hipStream_t stream) {
+// Both entry points: a non-null `layers` table runs `nlayers` layers in one
+// launch (entry 0's tensors are also the single-layer arguments).
+int encode_launch(const EncodeLayers* layers, int nlayers, const void* keys, const void* mean, const void* detail,
+                  const void* stats, int head_pages, const void* basis, const float* w1t, const float* b1,
+                  const float* w2_reader, const float* b2_reader, const float* w2_phi, const float* b2_phi,
+                  const double* B, void* coef, double* mean_b, double* detail_b, int enc_pages, int heads,
+                  int first_page, int pages, int hidden, hipStream_t stream) {
   if (heads <= 0 || pages <= 0 || first_page < 0 || first_page + pages > head_pages ||
       first_page + pages > enc_pages || hidden <= 0 || hidden > kMaxHidden)
     return (int)hipErrorInvalidValue;
@@ -931,8 +953,52 @@ int ssa_encode(const void* keys, const void* mean, const void* detail, const voi
   p.first = first_page;
   p.pages = pages;
   p.hidden = hidden;
-  hipLaunchKernelGGL(encode_kernel, dim3((pages + kEncPages - 1) / kEncPages, heads), dim3(256), 0, stream, p);
+  const dim3 grid((pages + kEncPages - 1) / kEncPages, heads, nlayers);
+  if (layers)
+    hipLaunchKernelGGL((encode_kernel<EncodeLayers>), grid, dim3(256), 0, stream, p, *layers);
+  else
+    hipLaunchKernelGGL((encode_kernel<OneLayer>), grid, dim3(256), 0, stream, p, OneLayer{});
   return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssa_encode(const void* keys, const void* mean, const void* detail, const void* stats, int head_pages,
+               const void* basis, const float* w1t, const float* b1, const float* w2_reader, const float* b2_reader,
+               const float* w2_phi, const float* b2_phi, const double* B, void* coef, double* mean_b,
+               double* detail_b, int enc_pages, int heads, int first_page, int pages, int hidden,
+               hipStream_t stream) {
+  return encode_launch(nullptr, 1, keys, mean, detail, stats, head_pages, basis, w1t, b1, w2_reader, b2_reader,
+                       w2_phi, b2_phi, B, coef, mean_b, detail_b, enc_pages, heads, first_page, pages, hidden, stream);
+}
+
+int ssa_encode_layers(int layers, const void* const* keys, const void* const* mean, const void* const* detail,
+                      const void* const* stats, int head_pages, const void* const* basis, const float* w1t,
+                      const float* b1, const float* w2_reader, const float* b2_reader, const float* w2_phi,
+                      const float* b2_phi, const double* B, void* const* coef, double* const* mean_b,
+                      double* const* detail_b, int enc_pages, int heads, int first_page, int pages, int hidden,
+                      hipStream_t stream) {
+  if (layers < 1 || layers > kMaxLayers || !keys || !mean || !detail || !stats || !basis || !coef || !mean_b ||
+      !detail_b)
+    return (int)hipErrorInvalidValue;
+  EncodeLayers t;
+  for (int l = 0; l < layers; ++l) {
+    if (!keys[l] || !mean[l] || !detail[l] || !stats[l] || !basis[l] || !coef[l] || !mean_b[l] || !detail_b[l])
+      return (int)hipErrorInvalidValue;
+    t.keys[l] = (const uint16_t*)keys[l];
+    t.mean[l] = (const uint16_t*)mean[l];
+    t.detail[l] = (const uint16_t*)detail[l];
+    t.stats[l] = (const uint16_t*)stats[l];
+    t.basis[l] = (const uint16_t*)basis[l];
+    t.coef[l] = (uint16_t*)coef[l];
+    t.mean_b[l] = mean_b[l];
+    t.detail_b[l] = detail_b[l];
+  }
+  return encode_launch(&t, layers, keys[0], mean[0], detail[0], stats[0], head_pages, basis[0], w1t, b1, w2_reader,
+                       b2_reader, w2_phi, b2_phi, B, coef[0], mean_b[0], detail_b[0], enc_pages, heads, first_page,
+                       pages, hidden, stream);
 }
 
 }  // extern "C"

@@ -25,6 +25,8 @@
 // precedes the summary recompute, VR/runtime.py:205-206).
 #include "common.h"
 
+#include <type_traits>
+
 using namespace ssa;
 
 namespace {
@@ -44,6 +46,15 @@ struct SummaryParams {
   uint16_t *keys, *mean, *detail, *stats;
   int HP, first, pages, iters;
 };
+
+// Per-layer tensors of a batched call (blockIdx.z = layer): the cache, the
+// basis and the summary slab of each layer; everything else is shared.
+constexpr int kMaxLayers = 32;
+struct SummaryLayers {
+  const uint16_t *k[kMaxLayers], *v[kMaxLayers], *basis[kMaxLayers];
+  uint16_t *keys[kMaxLayers], *mean[kMaxLayers], *detail[kMaxLayers], *stats[kMaxLayers];
+};
+struct OneLayer {};
 
 struct SumSmem {
   // row t = token, 64 words (bf16 pairs); 16 B chunk c of row t sits at
@@ -80,7 +91,18 @@ __device__ __forceinline__ void next4(const uint32_t* rows, uint64_t& m, int lan
   }
 }
 
-__global__ __launch_bounds__(256) void summary_kernel(SummaryParams p) {
+template <class Layers>
+__global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers layers) {
+  if constexpr (std::is_same_v<Layers, SummaryLayers>) {
+    const int l = blockIdx.z;
+    p.k = layers.k[l];
+    p.v = layers.v[l];
+    p.basis = layers.basis[l];
+    p.keys = layers.keys[l];
+    p.mean = layers.mean[l];
+    p.detail = layers.detail[l];
+    p.stats = layers.stats[l];
+  }
   __shared__ SumSmem s;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -347,11 +369,13 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p) {
   }
 }
 
-// Both entry points: src_k null reads the pages from the cache itself.
+// The entry points: src_k null reads the pages from the cache itself; a
+// non-null `layers` table runs `nlayers` layers in one launch.
 int summary_launch(const void* src_k, const void* src_v, long long src_token_stride, long long src_head_stride,
                    const void* k, const void* v, long long kv_token_stride, long long kv_head_stride,
                    const int32_t* init, const void* basis, void* keys, void* mean, void* detail, void* stats,
-                   int head_pages, int heads, int first_page, int pages, int iters, hipStream_t stream) {
+                   int head_pages, int heads, int first_page, int pages, int iters, hipStream_t stream,
+                   const SummaryLayers* layers = nullptr, int nlayers = 1) {
   if (heads <= 0 || pages <= 0 || first_page < 0 || first_page + pages > head_pages || iters < 1 ||
       init == nullptr)
     return (int)hipErrorInvalidValue;
@@ -378,7 +402,11 @@ int summary_launch(const void* src_k, const void* src_v, long long src_token_str
   p.first = first_page;
   p.pages = pages;
   p.iters = iters;
-  hipLaunchKernelGGL(summary_kernel, dim3(pages, heads), dim3(256), 0, stream, p);
+  if (layers)
+    hipLaunchKernelGGL((summary_kernel<SummaryLayers>), dim3(pages, heads, nlayers), dim3(256), 0, stream, p,
+                       *layers);
+  else
+    hipLaunchKernelGGL((summary_kernel<OneLayer>), dim3(pages, heads), dim3(256), 0, stream, p, OneLayer{});
   return (int)hipGetLastError();
 }
 
@@ -400,6 +428,29 @@ int ssa_summary_write(const void* src_k, const void* src_v, long long src_token_
   if (src_k == nullptr || src_v == nullptr || k == nullptr || v == nullptr) return (int)hipErrorInvalidValue;
   return summary_launch(src_k, src_v, src_token_stride, src_head_stride, k, v, kv_token_stride, kv_head_stride,
                         init, basis, keys, mean, detail, stats, head_pages, heads, first_page, pages, iters, stream);
+}
+
+int ssa_summary_layers(int layers, const void* const* k, const void* const* v, long long kv_token_stride,
+                       long long kv_head_stride, const int32_t* init, const void* const* basis, void* const* keys,
+                       void* const* mean, void* const* detail, void* const* stats, int head_pages, int heads,
+                       int first_page, int pages, int iters, hipStream_t stream) {
+  if (layers < 1 || layers > kMaxLayers || !k || !v || !basis || !keys || !mean || !detail || !stats)
+    return (int)hipErrorInvalidValue;
+  SummaryLayers t;
+  for (int l = 0; l < layers; ++l) {
+    if (!k[l] || !v[l] || !basis[l] || !keys[l] || !mean[l] || !detail[l] || !stats[l])
+      return (int)hipErrorInvalidValue;
+    t.k[l] = (const uint16_t*)k[l];
+    t.v[l] = (const uint16_t*)v[l];
+    t.basis[l] = (const uint16_t*)basis[l];
+    t.keys[l] = (uint16_t*)keys[l];
+    t.mean[l] = (uint16_t*)mean[l];
+    t.detail[l] = (uint16_t*)detail[l];
+    t.stats[l] = (uint16_t*)stats[l];
+  }
+  return summary_launch(nullptr, nullptr, 0, 0, k[0], v[0], kv_token_stride, kv_head_stride, init, basis[0], keys[0],
+                        mean[0], detail[0], stats[0], head_pages, heads, first_page, pages, iters, stream, &t,
+                        layers);
 }
 
 }  // extern "C"

@@ -104,6 +104,42 @@ def encode(summary: Summary, basis: torch.Tensor, reader: Reader, out: Encoding 
 
 
 @torch.no_grad()
+def encode_layers(summaries, bases, reader: Reader, outs, first: int, pages: int):
+    """encode() of the same page range over several layers in one launch
+    (ssa_encode_layers): one summary slab, basis and encoding per layer (at
+    most 32), with equal slab and encoding capacities; the reader weights are
+    shared.  Equal to an encode() per layer, bit for bit."""
+    n = len(summaries)
+    if not 1 <= n <= 32 or not len(bases) == len(outs) == n:
+        raise ValueError("one slab, basis and encoding per layer, 1..32 layers")
+    h = summaries[0].mean.shape[0]
+    hp = _summary_ok(summaries[0])
+    ep = outs[0].coef.shape[1]
+    dev = summaries[0].mean.device
+    bs = []
+    for s_, basis, out in zip(summaries, bases, outs):
+        if _summary_ok(s_) != hp or s_.mean.shape[0] != h or s_.mean.device != dev:
+            raise ValueError("every layer's slab must have the first one's heads and capacity")
+        if out.coef.shape != (h, ep, COEF_STRIDE) or not out.coef.is_contiguous() or \
+                out.mean.shape != (h, ep, 16) or not out.mean.is_contiguous() or \
+                out.detail.shape != (h, ep, 3, 16) or not out.detail.is_contiguous():
+            raise ValueError("every layer's encoding must have the first one's shape, contiguous")
+        b = basis if (basis.dtype == torch.bfloat16 and basis.is_contiguous()) else \
+            basis.to(torch.bfloat16).contiguous()
+        if b.shape != (h, HEAD_DIM, 8):
+            raise ValueError("basis must be [H,128,8]")
+        bs.append(b)
+    _lib.check(_lib.lib().ssa_encode_layers(
+        n, _lib.ptrs([s_.keys for s_ in summaries]), _lib.ptrs([s_.mean for s_ in summaries]),
+        _lib.ptrs([s_.detail for s_ in summaries]), _lib.ptrs([s_.stats for s_ in summaries]), hp, _lib.ptrs(bs),
+        _lib.ptr(reader.w1t), _lib.ptr(reader.b1), _lib.ptr(reader.w2r), _lib.ptr(reader.b2r), _lib.ptr(reader.w2p),
+        _lib.ptr(reader.b2p), _lib.ptr(reader.B), _lib.ptrs([o.coef for o in outs]), _lib.ptrs([o.mean for o in outs]),
+        _lib.ptrs([o.detail for o in outs]), ep, h, first, pages, reader.hidden, _lib.stream_handle(dev)),
+        "ssa_encode_layers")
+    return outs
+
+
+@torch.no_grad()
 def correct(q, summary: Summary, encoding: Encoding, reader: Reader, risk, lse, mask, ids, own, heads,
             workspace=None, want_scores=False, no_alloc=False, probe_layout=None):
     """Full_Pset correction of the scoped `heads` in place on `mask` (uint8 or

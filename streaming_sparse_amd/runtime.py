@@ -118,6 +118,12 @@ def runs(slots) -> list:
     return [tuple(r) for r in out]
 
 
+def _batches(items, size: int = 32):
+    """`items` in runs of at most `size` (the layer limit of one batched
+    launch)."""
+    return [items[i:i + size] for i in range(0, len(items), size)]
+
+
 def rebase_offset(chunk: int) -> int:
     """Temporal shift of the anchor frame for a chunk (0 before the window is full)."""
     return 3 * chunk - 15 if chunk >= REBASE_FROM_CHUNK else 0
@@ -280,19 +286,19 @@ class StreamRuntime:
     def rebase_anchor(self, offset: int):
         """Anchor keys of every layer = the chunk-0 anchor keys with the
         temporal RoPE pairs shifted by `offset` frames; the anchor pages'
-        summaries and encodings rebuilt from them."""
+        summaries and encodings rebuilt from them.  Each of the three steps
+        runs every layer in one launch (the reference loops over the layers,
+        VB/phase.py:4-25)."""
         ph = self.freqs[offset, :TEMPORAL_PAIRS]
         phase = torch.view_as_real(ph).to(torch.float64).contiguous().pin_memory().to(self.device, non_blocking=True)
         H = self.H
-        for li, L in enumerate(self.layers):
-            src = L.canonical
-            tok, head = kv_strides(L.k, L.v)
-            _lib.check(_lib.lib().ssa_anchor_rebase(_lib.ptr(src), H * HEAD_DIM, HEAD_DIM, _lib.ptr(L.k), tok, head,
-                                                    _lib.ptr(phase), TEMPORAL_PAIRS, ANCHOR_TOKENS, H,
-                                                    _lib.stream_handle(self.device)), "ssa_anchor_rebase")
-            summary.build(L.k, L.v, L.basis, self.init[:, :ANCHORS], L.slab, 0, ANCHORS)
-            if L.encoding is not None:
-                pset.encode(L.slab, L.basis, self.reader, out=L.encoding, first=0, pages=ANCHORS)
+        for group_ in _batches(self.layers):
+            tok, head = kv_strides(group_[0].k, group_[0].v)
+            _lib.check(_lib.lib().ssa_anchor_rebase_layers(
+                len(group_), _lib.ptrs([L.canonical for L in group_]), H * HEAD_DIM, HEAD_DIM,
+                _lib.ptrs([L.k for L in group_]), tok, head, _lib.ptr(phase), TEMPORAL_PAIRS, ANCHOR_TOKENS, H,
+                _lib.stream_handle(self.device)), "ssa_anchor_rebase_layers")
+        self._summarise(0, ANCHORS, self.init[:, :ANCHORS])
 
     def dense_window(self, chunk: int | None = None) -> bool:
         n = self.ring.n
@@ -352,31 +358,39 @@ class StreamRuntime:
     def commit_chunk(self, inputs):
         """The clean step's commit of every layer: one batched grouping of the
         chunk's tokens (the first chunk re-sorted by frame so the anchor frame
-        fills pages 0..23), then per layer the grouped pages into the ring
-        slots with their summaries and encodings."""
+        fills pages 0..23), then the grouped pages of every layer into the
+        ring slots (tokens in `order[layer]` [H, 4608], None: token order)
+        with their summaries and encodings (VR/runtime.py:356-370), each step
+        over all layers in one launch."""
         order = None
         if self.cfg.grouping:
             order = group.order(inputs.clean_k, inputs.clean_v, self.group_weights, first_chunk=self.chunk == 0,
                                 page_dst=self.page_dst, workspace=self.ws)
         self.last_order = order
-        for layer in range(self.cfg.layers):
-            self.commit(layer, inputs.clean_k[layer], inputs.clean_v[layer],
-                        None if order is None else order[layer])
-
-    def commit(self, layer: int, k, v, order=None):
-        """The chunk's pages (tokens in `order` [H, 4608], None: token order)
-        into the ring slots, then their summaries and (Full_Pset layers)
-        encodings at those slots (VR/runtime.py:356-370)."""
-        L = self.layers[layer]
-        tok, head = kv_strides(L.k, L.v)
-        _lib.check(_lib.lib().ssa_commit_pages(_lib.ptr(k), _lib.ptr(v), self.H * HEAD_DIM, HEAD_DIM, _lib.ptr(order),
-                                               CURRENT, _lib.ptr(self.slots_dev), self.cap, _lib.ptr(L.k),
-                                               _lib.ptr(L.v), tok, head, self.H, _lib.stream_handle(self.device)),
-                   "ssa_commit_pages")
+        for group_ in _batches(list(range(self.cfg.layers))):
+            Ls = [self.layers[layer] for layer in group_]
+            tok, head = kv_strides(Ls[0].k, Ls[0].v)
+            ks = [inputs.clean_k[layer] for layer in group_]
+            vs = [inputs.clean_v[layer] for layer in group_]
+            src_tok, src_head = ks[0].stride(0), ks[0].stride(1)
+            orders = [None if order is None else order[layer] for layer in group_]
+            _lib.check(_lib.lib().ssa_commit_pages_layers(
+                len(group_), _lib.ptrs(ks), _lib.ptrs(vs), src_tok, src_head, _lib.ptrs(orders), CURRENT,
+                _lib.ptr(self.slots_dev), self.cap, _lib.ptrs([L.k for L in Ls]), _lib.ptrs([L.v for L in Ls]), tok,
+                head, self.H, _lib.stream_handle(self.device)), "ssa_commit_pages_layers")
         for first, length, off in runs(self.slots):
-            summary.build(L.k, L.v, L.basis, self.init[:, off:off + length], L.slab, first, length)
-            if L.encoding is not None:
-                pset.encode(L.slab, L.basis, self.reader, out=L.encoding, first=first, pages=length)
+            self._summarise(first, length, self.init[:, off:off + length])
+
+    def _summarise(self, first: int, length: int, init):
+        """Summaries of pages [first, first + length) of every layer, and the
+        encodings of the Full_Pset layers, each in one launch per 32 layers."""
+        for group_ in _batches(self.layers):
+            summary.build_layers([L.k for L in group_], [L.v for L in group_], [L.basis for L in group_], init,
+                                 [L.slab for L in group_], first, length)
+        encoded = [L for L in self.layers if L.encoding is not None]
+        for group_ in _batches(encoded):
+            pset.encode_layers([L.slab for L in group_], [L.basis for L in group_], self.reader,
+                               [L.encoding for L in group_], first, length)
 
     def end_chunk(self):
         if self.chunk == 0:

@@ -23,6 +23,8 @@ def declared():
 def test_header_declares_entry_points():
     assert set(declared()) == {"ssa_rep_operands", "ssa_attention", "ssa_attention_workspace_bytes", "ssa_route", "ssa_select", "ssa_encode", "ssa_pset",
                                "ssa_summary", "ssa_summary_write", "ssa_pset_noalloc", "ssa_anchor_rebase", "ssa_commit_pages",
+                               "ssa_summary_layers", "ssa_encode_layers", "ssa_anchor_rebase_layers",
+                               "ssa_commit_pages_layers",
                                "ssa_group_order"}
 
 

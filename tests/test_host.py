@@ -2,6 +2,7 @@
 checks, K/V stride detection, summary slab slicing, and the C ABI's own
 argument checks (every rejected call returns hipErrorInvalidValue before any
 HIP call, so these run without a GPU)."""
+import ctypes
 import os
 
 import pytest
@@ -193,6 +194,23 @@ def test_c_abi_rejects_bad_shapes():
     assert sw(None, 360) == INVALID
     assert sw(16, 400) == INVALID
     assert sw(8, 360) == INVALID                                       # source rows not 16-byte aligned
+    # the layer-batched entries: 1..32 layers, non-null arrays and entries
+    arr = lambda n, v=16: _lib.ptrs([None] * n) if v is None else (ctypes.c_void_p * n)(*([v] * n))
+    sl = lambda n, a: L.ssa_summary_layers(n, a, a, 1536, 128, 16, a, a, a, a, a, 432, 12, 360, 72, 4, N)
+    assert sl(0, arr(1)) == INVALID
+    assert sl(33, arr(33)) == INVALID
+    assert sl(2, arr(2, None)) == INVALID
+    assert sl(2, None) == INVALID
+    rb = lambda n, a: L.ssa_anchor_rebase_layers(n, a, 1536, 128, a, 1536, 128, 16, 32, 1536, 12, N)
+    assert rb(33, arr(33)) == INVALID
+    assert rb(2, arr(2, None)) == INVALID
+    cm = lambda n, a: L.ssa_commit_pages_layers(n, a, a, 1536, 128, a, 72, 16, 432, a, a, 1536, 128, 12, N)
+    assert cm(0, arr(1)) == INVALID
+    assert cm(2, arr(2, None)) == INVALID
+    el = lambda n, a: L.ssa_encode_layers(n, a, a, a, a, 432, a, N, N, N, N, N, N, N, a, a, a, 432, 12, 360, 72, 256,
+                                          N)
+    assert el(33, arr(33)) == INVALID
+    assert el(2, arr(2, None)) == INVALID
     # ssa_encode: hidden width <= 256, page range inside both slabs
     en = lambda pages, hidden: L.ssa_encode(N, N, N, N, 432, N, N, N, N, N, N, N, N, N, N, N, 432, 12, 360, pages,
                                             hidden, N)
