@@ -15,10 +15,16 @@
 // One workgroup (256 threads, 4 waves) per (page, head).  Thread (token
 // t = lane, quarter q = wave) keeps dims 32q..32q+31 of its key in registers
 // for the distance passes; the page's K and V are also staged in LDS as bf16
-// pairs for the per-cluster sums, which thread (cluster r = wave, dims
-// 2 lane, 2 lane + 1) accumulates over the cluster's member tokens in
-// ascending token order, from a wave-uniform membership mask.  LDS stays
-// under 40 KB so four workgroups share a CU.
+// pairs.  The cluster sums of each Lloyd step (and the page and cluster V
+// sums after the last) run on the matrix pipe: wave w forms out[cluster][dim]
+// = M^T . rows for dims 32w..32w+31, with the 0/1 membership M built from
+// the wave-uniform member masks and the rows read by LDS transpose reads; a
+// sum of at most 64 bf16 values is exact in fp32 whenever their exponents
+// span no more than 10 binades, so it does not depend on the order of the
+// additions.  The key variances and the V spread, thread (cluster r = wave,
+// dims 2 lane, 2 lane + 1), accumulate over the cluster's member tokens in
+// ascending token order.  LDS stays under 40 KB so four workgroups share a
+// CU.
 //
 // ssa_summary_write reads the page rows from the chunk's K/V instead and
 // writes them into the cache in the same pass (the window write that
@@ -66,6 +72,7 @@ struct SumSmem {
   union {
     f32x4 dist[4][64];                 // [quarter][token] partial distances to the 4 centroids
     float vnp[4][64];                  // [quarter][token] partial |v|^2 (before the first distance pass)
+    float vm[4][128];                  // [cluster][dim] cluster V means (after the last assignment)
   } u;
   float kmean[128], vmean[128];
   float code[4][8];
@@ -89,6 +96,52 @@ __device__ __forceinline__ void next4(const uint32_t* rows, uint64_t& m, int lan
       w[u] = rows[word(t, lane)];
     }
   }
+}
+
+typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// B operand of the cluster sums: the page rows (K or V) at dims
+// 32 dt + lane % 32 for the tokens 16 ks + 8 (e / 4) + 4 (lane / 32) + e % 4
+// of its 8 elements e, by two LDS transpose reads (ds_read_b64_tr_b16) of the
+// token-major rows.
+__device__ __forceinline__ u32x4 rows_operand(const uint32_t* rows, int dt, int ks, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int chunk = 4 * dt + 2 * (g & 1) + ((i & 3) >> 1);
+  const int r0 = 16 * ks + 4 * (g >> 1) + (i >> 2), r1 = r0 + 8;
+  const lds_u8* base = (const lds_u8*)rows + (i & 1) * 8;
+  const bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + r0 * 256 + ((chunk ^ (r0 & 15)) << 4)));
+  const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(base + r1 * 256 + ((chunk ^ (r1 & 15)) << 4)));
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return u32x4{ua[0], ua[1], ub[0], ub[1]};
+}
+
+// A operand of the cluster sums: row m = lane % 32 is the 0/1 membership of
+// cluster m (m < 4) or all ones (m == 4: the page sum) or zero, over the
+// tokens of rows_operand's k order.
+__device__ __forceinline__ u32x4 member_operand(const uint64_t (&mk)[4], int ks, int lane) {
+  const int m = lane & 31, hh = lane >> 5;
+  const uint64_t msk = m < 4 ? mk[m] : (m == 4 ? ~0ull : 0ull);
+  const uint32_t bits = (uint32_t)((msk >> (16 * ks + 4 * hh)) & 0xFu) |
+                        ((uint32_t)((msk >> (16 * ks + 8 + 4 * hh)) & 0xFu) << 4);
+  u32x4 w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = ((bits >> (2 * j)) & 1u ? 0x3F80u : 0u) | ((bits >> (2 * j + 1)) & 1u ? 0x3F800000u : 0u);
+  return w;
+}
+
+// Sums over the member tokens of each cluster (and over the whole page) of
+// dims 32 dt .. 32 dt + 31 of the rows: out[cluster][dim] = M^T . rows on
+// v_mfma_f32_32x32x16_bf16 (fp32 sums of bf16 values times 1).  Lane l < 32
+// gets the 4 cluster sums of dim 32 dt + l in items 0..3, lane l + 32 the
+// page sum of that dim in item 0.
+__device__ __forceinline__ f32x16 cluster_sums(const uint32_t* rows, const uint64_t (&mk)[4], int dt, int lane) {
+  f32x16 c = {};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) c = mfma32(member_operand(mk, ks, lane), rows_operand(rows, dt, ks, lane), c);
+  return c;
 }
 
 template <class Layers>
@@ -162,26 +215,13 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers la
     s.u.vnp[wave][lane] = vn;
   }
   __syncthreads();
-  // initial centroids, page K / V means, max token |v| (wave 1 keeps it)
+  // initial centroids, max token |v| (wave 1 keeps it)
   {
     const uint32_t w = s.K[word(init_tok, lane)];
     s.cent[wave][d0] = bf16_lo(w);
     s.cent[wave][d1] = bf16_hi(w);
   }
   float vmax = 0.f;
-  if (wave < 2) {
-    const uint32_t* rows = wave == 0 ? s.K : s.V;
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll 16
-    for (int t = 0; t < 64; ++t) {
-      const uint32_t w = rows[word(t, lane)];
-      a0 += bf16_lo(w);
-      a1 += bf16_hi(w);
-    }
-    float* dst = wave == 0 ? s.kmean : s.vmean;
-    dst[d0] = a0 / 64.f;
-    dst[d1] = a1 / 64.f;
-  }
   if (wave == 1) {
     vmax = sqrtf(((s.u.vnp[0][lane] + s.u.vnp[1][lane]) + s.u.vnp[2][lane]) + s.u.vnp[3][lane]);
     vmax = wave_reduce(vmax, [](float a, float b) { return fmaxf(a, b); });
@@ -191,7 +231,7 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers la
   // Lloyd iterations: assign each token to its nearest centroid (squared
   // distance, ties -> lower cluster), then move every non-empty centroid to
   // its cluster mean
-  uint64_t mr = 0;   // member tokens of cluster `wave` (wave-uniform)
+  uint64_t memb[4] = {0, 0, 0, 0};   // member tokens of each cluster (wave-uniform)
   for (int it = 0; it < p.iters; ++it) {
     float d[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -221,71 +261,67 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers la
         best = r;
       }
     }
-    mr = __ballot(best == wave);
-    // thread (cluster wave, dims 2 lane, 2 lane + 1): the new centroid
-    if (mr) {
-      float a0 = 0.f, a1 = 0.f;
-      uint64_t m = mr;
-      while (m) {
-        uint32_t w[4];
-        next4(s.K, m, lane, w);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          a0 += bf16_lo(w[u]);
-          a1 += bf16_hi(w[u]);
-        }
-      }
-      const float c = (float)__popcll(mr);
-      s.cent[wave][d0] = a0 / c;
-      s.cent[wave][d1] = a1 / c;
+    for (int r = 0; r < 4; ++r) memb[r] = __ballot(best == r);
+    // the cluster sums of dims 32 wave .. 32 wave + 31 (and the page sum, on
+    // the first pass) on the matrix pipe; lane l < 32 then holds the 4
+    // cluster sums of dim 32 wave + l, lane l + 32 its page sum
+    const f32x16 cs = cluster_sums(s.K, memb, wave, lane);
+    if (lane < 32) {
+      const int d = 32 * wave + lane;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (memb[r]) s.cent[r][d] = cs[r] / (float)__popcll(memb[r]);
+    } else if (it == 0) {
+      s.kmean[32 * wave + lane - 32] = cs[0] / 64.f;
     }
     __syncthreads();
   }
+  const uint64_t mr = memb[wave];   // member tokens of cluster `wave`
+  // the cluster V means of dims 32 wave .. 32 wave + 31 (an empty cluster
+  // takes the page V mean), through LDS to the threads of each cluster
+  {
+    const f32x16 cs = cluster_sums(s.V, memb, wave, lane);
+    const float page = __shfl_xor(cs[0], 32);
+    if (lane < 32) {
+      const int d = 32 * wave + lane;
+      const float vmean = page / 64.f;
+      s.vmean[d] = vmean;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s.u.vm[r][d] = memb[r] ? cs[r] / (float)__popcll(memb[r]) : vmean;
+    }
+  }
+  __syncthreads();
 
-  // thread (cluster r = wave, dims 2 lane, 2 lane + 1): cluster V mean (empty
-  // cluster -> page V mean), key variance, V spread
+  // thread (cluster r = wave, dims 2 lane, 2 lane + 1): key variance and V
+  // spread over the cluster's member tokens, in ascending token order
   const int r = wave;
   const int cnt = __popcll(mr);
   const float div = (float)max(cnt, 1);
   const float c0 = s.cent[r][d0], c1 = s.cent[r][d1];
-  float vm0, vm1, var0 = 0.f, var1 = 0.f, spread = 0.f;
+  const float vm0 = s.u.vm[r][d0], vm1 = s.u.vm[r][d1];
+  float var0 = 0.f, var1 = 0.f, spread = 0.f;
   {
-    float v0 = 0.f, v1 = 0.f;
     uint64_t mk = mr, mv = mr;
     while (mk) {
       uint32_t wk[4], wv[4];
-      const uint64_t m0 = mk;
+      const int n = __popcll(mk);
       next4(s.K, mk, lane, wk);
       next4(s.V, mv, lane, wv);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        v0 += bf16_lo(wv[u]);
-        v1 += bf16_hi(wv[u]);
         // absent slots: skip, as (0 - c)^2 is not 0
-        if (u < __popcll(m0)) {
+        if (u < n) {
           const float x0 = bf16_lo(wk[u]) - c0, x1 = bf16_hi(wk[u]) - c1;
           var0 = fmaf(x0, x0, var0);
           var1 = fmaf(x1, x1, var1);
+          const float y0 = bf16_lo(wv[u]) - vm0, y1 = bf16_hi(wv[u]) - vm1;
+          spread = fmaf(y0, y0, fmaf(y1, y1, spread));
         }
       }
     }
-    vm0 = cnt > 0 ? v0 / (float)cnt : s.vmean[d0];
-    vm1 = cnt > 0 ? v1 / (float)cnt : s.vmean[d1];
     var0 /= div;
     var1 /= div;
-    uint64_t m = mr;
-    while (m) {
-      const uint64_t m0 = m;
-      uint32_t wv[4];
-      next4(s.V, m, lane, wv);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (u < __popcll(m0)) {
-          const float x0 = bf16_lo(wv[u]) - vm0, x1 = bf16_hi(wv[u]) - vm1;
-          spread = fmaf(x0, x0, fmaf(x1, x1, spread));
-        }
-      }
-    }
     spread = wave_sum(spread);
   }
   // code[r][kk] = vm_r . bf16(basis)[:, kk]
