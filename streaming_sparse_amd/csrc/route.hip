@@ -5,7 +5,10 @@
 //   z    = bf16(probe) . bf16(repK)^T * D^-1/2           (VR/tensor_bmm.py:56-66)
 //   norm = max / sum exp over the P*4 reps of each probe  (VR/risk_online.py:88-113)
 //   risk = mean over 16 probes of ((t0 x0 + t1 x1) + t2 x2) + t3 x3
-//          (VR/runtime.py:27-40; kernels VR/risk_online.py:24-59,77-86)
+//          (VR/runtime.py:27-40; kernels VR/risk_online.py:24-59,77-86),
+//          here summed as (t0 x0 + t1 x1) + c sum_r prob_r W_r, the two
+//          terms linear in the probabilities folded into one coefficient
+//          per rep that a matrix product forms
 //   mask = quota selection (VB/quota_mask.py:7-39) or the base LUT
 //          (VR/runtime.py:279-288) or fixed top-k (VR/fixed_page_select.py:8-47)
 //   ids  = own first, then descending risk                (VB/graph.py:210)
@@ -323,16 +326,24 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   // linear in the probabilities of its reps, so each page value is formed
   // with 2^(z2 - m) and rescaled by 2^(m - MX) / DEN once the totals are
   // known.  Page values and the max they were formed with stay in registers.
-  u32x4 bq, bqn, bone;
+  // B operands of the per-rep products, each value as two bf16 terms (the
+  // hi parts in the lanes of k 0..7, the lo parts in those of k 8..15, or
+  // hi | lo in one word):
+  //   bq  = q2_g            against st[r, 0..7]        -> U = u_r
+  //   bq3 = theta3 q2_g     against st[r, 0..7], and
+  //   bwt = (theta2 qn, theta3 qn^2) against (st8, st8^2) -> W = theta2 beta + theta3 (u + beta^2)
+  //   bone = 1              against st9 or st10         -> their broadcast
+  u32x4 bq, bq3, bwt, bone;
   {
+    auto rnd = [](float x) { return bf16_lo(pack_bf16(x, 0.f)); };
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float a = q2[2 * w], b = q2[2 * w + 1];
-      const float ah = bf16_lo(pack_bf16(a, 0.f)), bh = bf16_lo(pack_bf16(b, 0.f));
-      bq[w] = hh == 0 ? pack_bf16(a, b) : pack_bf16(a - ah, b - bh);
+      const float a = q2[2 * w], b = q2[2 * w + 1], a3 = th3 * a, b3 = th3 * b;
+      bq[w] = hh == 0 ? pack_bf16(a, b) : pack_bf16(a - rnd(a), b - rnd(b));
+      bq3[w] = hh == 0 ? pack_bf16(a3, b3) : pack_bf16(a3 - rnd(a3), b3 - rnd(b3));
     }
-    const float qh = bf16_lo(pack_bf16(qn, 0.f));
-    bqn = u32x4{hh == 0 ? pack_bf16(qh, qn - qh) : 0u, 0u, 0u, 0u};
+    const float w2 = th2 * qn, w3 = th3 * (qn * qn), w2h = rnd(w2), w3h = rnd(w3);
+    bwt = hh == 0 ? u32x4{pack_bf16(w2h, w2 - w2h), pack_bf16(w3h, w3 - w3h), pack_bf16(w3h, 0.f), 0u} : u32x4{};
     bone = u32x4{hh == 0 ? 0x3F80u : 0u, 0u, 0u, 0u};
   }
   struct TileStats {
@@ -367,8 +378,13 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   auto soft = [&](f32x16 S, const TileStats& ts, int tile, float (&v4)[4], float& mt) {
     const u32x4 ag = {ts.w01[0], ts.w01[1], ts.w23[0], ts.w23[1]};
     const uint32_t st8 = ts.w45[0] & 0xffffu, st9 = ts.w45[0] >> 16, st10 = ts.w45[1] & 0xffffu;
+    // st8^2 is exact in fp32 (a bf16 has 8 significant bits) and splits
+    // exactly into a bf16 hi part and a bf16 remainder
+    const float s8 = bf16_to_f32(st8), sq = s8 * s8, sqh = bf16_lo(pack_bf16(sq, 0.f));
+    const uint32_t sqw = pack_bf16(sqh, sqh);
+    const u32x4 aw = {(st8 | (st8 << 16)) & lo_only, sqw & lo_only, pack_bf16(sq - sqh, 0.f) & lo_only, 0u};
     const f32x16 U = mfma32(ag, bq, f32x16{});
-    const f32x16 Bt = mfma32(u32x4{(st8 | (st8 << 16)) & lo_only, 0u, 0u, 0u}, bqn, f32x16{});
+    const f32x16 W = mfma32(ag, bq3, mfma32(aw, bwt, f32x16{}));
     const f32x16 F9 = mfma32(u32x4{st9 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
     const f32x16 F10 = mfma32(u32x4{st10 & lo_only, 0u, 0u, 0u}, bone, f32x16{});
     if (tile * 8 + 8 > P) {
@@ -390,19 +406,17 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       const float alpha = ((prob[0] + prob[1]) + prob[2]) + prob[3];
       asum += alpha;
       const float c = ts.s111[jj] + bmax;
-      float x0 = alpha * ts.s011[jj], x1 = 0.f, x2 = 0.f, x3 = 0.f;
+      // x0, x1 as the reference forms them; theta2 x2 + theta3 x3 =
+      // c sum_r prob_r W_r.  u = sum_g q2_g st_g >= 0 (slots 0..7 hold mean
+      // squares), so sqrt(|u|) is the reference's sqrt(max(u, 0)).
+      float x0 = alpha * ts.s011[jj], x1 = 0.f, xw = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float u = max2f(U[4 * jj + i], 0.f);
-        const float beta = Bt[4 * jj + i];
         x0 += fabsf(prob[i] - alpha * 0.25f) * F9[4 * jj + i];
-        x1 += prob[i] * __builtin_amdgcn_sqrtf(u) * F10[4 * jj + i];
-        x2 += prob[i] * beta;
-        x3 += prob[i] * (u + beta * beta);
+        x1 += prob[i] * __builtin_amdgcn_sqrtf(fabsf(U[4 * jj + i])) * F10[4 * jj + i];
+        xw += prob[i] * W[4 * jj + i];
       }
-      x2 *= c;
-      x3 *= c;
-      v4[jj] = ((x0 * th0 + x1 * th1) + x2 * th2) + x3 * th3;
+      v4[jj] = fmaf(c, xw, fmaf(x1, th1, x0 * th0));
     }
     den = den * __builtin_amdgcn_exp2f(mx - mnew) + asum;
     mx = mnew;
