@@ -288,6 +288,16 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   auto uniform = [](float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v))); };
   const float th0 = uniform(p.theta[h * 4 + 0]), th1 = uniform(p.theta[h * 4 + 1]);
   const float th2 = uniform(p.theta[h * 4 + 2]), th3 = uniform(p.theta[h * 4 + 3]);
+  // the selection's inputs, requested here so that their latency overlaps
+  // the setup's: the own page of the two blocks and the head's current quota
+  int own_raw[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int tb = min(t0 + q, p.T - 1);
+    own_raw[q] = __builtin_amdgcn_readfirstlane(p.own ? p.own[(long long)h * p.T + tb] : P - p.T + tb);
+  }
+  const int cur_raw = __builtin_amdgcn_readfirstlane(p.mode == 1 && P != kCurrent ? p.current[h] : p.total);
+  asm volatile("" ::"s"(own_raw[0]), "s"(own_raw[1]), "s"(cur_raw));
   // the loads above are complete past this point
 #pragma unroll
   for (int st = 0; st < 8; ++st) asm volatile("" ::"v"(qop[st]));
@@ -494,13 +504,10 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   // partitions (base / top-k: one group).
   const int b = tid >> 7, bt = tid & 127;
   int own[2];
+  // own pages outside the window are clamped into it (memory safety of the
+  // per-page state; a valid own is in [0, P))
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int tb = min(t0 + q, p.T - 1);
-    // own pages outside the window are clamped into it (memory safety of
-    // the per-page state; a valid own is in [0, P))
-    own[q] = min(max(p.own ? p.own[(long long)h * p.T + tb] : P - p.T + tb, 0), P - 1);
-  }
+  for (int q = 0; q < 2; ++q) own[q] = min(max(own_raw[q], 0), P - 1);
   // Quota partitions (VB/quota_mask.py:18-31): anchors [0,24), history
   // [24,cur_lo), current [cur_lo,P).  With P == 72 the anchor frame is the
   // chunk's first frame (VB/graph.py:143-148): current = [24,72), no history,
@@ -512,7 +519,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   const int ncur = P - cur_lo, nhist = cur_lo - kAnchors;
   int A = 0, nh = 0;
   if (p.mode == 1) {
-    const int araw = P == kCurrent ? p.total : p.current[h];
+    const int araw = cur_raw;
     A = min(max(araw, 0), ncur);
     nh = min(max(p.total - araw, 0), nhist);
   }
