@@ -262,8 +262,11 @@ int ssa_encode_layers(int layers, const void* const* keys, const void* const* me
  * removes (then the anchor pages other than own as stand-ins) x the first 16
  * of 32 adds (the unselected pages by descending risk, then the selected
  * pages in page order).
+ * A padded add slot k takes the k-th page that is neither selected nor a
+ * valid add; when there is none (the reference's pool indexes page P
+ * there) the slot holds -1, an empty candidate of zero mass.
  * Requires pages == 72 with 24 <= count <= 72, or 96 < pages <= 512 with
- * pages - count >= 64. */
+ * 1 <= count <= pages. */
 int ssa_pset(const void* q, long long q_head_stride, long long q_block_stride, long long q_row_stride,
              int gathered, const void* keys, int head_pages, const void* coef, const double* mean_b,
              const double* detail_b, int enc_pages, const float* wq, const float* risk, const float* probe_lse,

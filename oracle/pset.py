@@ -139,7 +139,11 @@ def pool(risk, mask, own):
     """Stratified pool with slot padding (VB/quota_pool.py:32-46): invalid
     remove slot i -> anchor page i; invalid add slot j -> the j-th smallest page
     that is neither selected nor a valid add.  Padded slots are never legal.
-    A 72-page window takes the first chunk's pool (first_chunk_pool)."""
+    When fewer than j + 1 such pages exist, slot j holds P, as the
+    reference's `spare` does (`topk` of a tensor filled with P): page P is
+    past the window, and grouped_scores reads it as an empty candidate (zero
+    mass, zero values).  A 72-page window takes the first chunk's pool
+    (first_chunk_pool)."""
     if risk.shape[-1] == CURRENT:
         return first_chunk_pool(risk, mask, own)
     r, a, legal = stratified_pool(risk, mask, own)
@@ -168,7 +172,11 @@ def _exclude(logs, values):
     k = logs.shape[-1]
     eye = torch.eye(k, dtype=torch.bool)
     excluded = logs[:, :, None, :].expand(-1, -1, k, -1).masked_fill(eye, -torch.inf)
-    return excluded.logsumexp(-1), excluded.softmax(-1) @ values
+    lse = excluded.logsumexp(-1)
+    # a group whose other members all have zero mass has no mixture (its
+    # weight e^(lse - den) is 0); zero instead of softmax's 0/0
+    mix = torch.where(torch.isfinite(lse)[..., None], excluded.softmax(-1) @ values, 0.0)
+    return lse, mix
 
 
 def grouped_scores(rp, beta, lm, cen, mask, remove, add):
@@ -177,6 +185,14 @@ def grouped_scores(rp, beta, lm, cen, mask, remove, add):
     add [B,A] -> [B,R,A] = mean over probes of 2 E.delta - |delta|^2, where
     E = target - H and delta is the change of the mixture H after the swap."""
     rp, beta, lm, cen = (x.double() for x in (rp, beta, lm, cen))
+    p = mask.shape[-1]
+    if bool((add >= p).any()):
+        # an add slot past the spare pages holds page P (pool): one more page
+        # of zero mass and zero values, outside the selection
+        def pad(x, value):
+            return torch.cat([x, torch.full_like(x[:, :, :1], value)], 2)
+        rp, cen, beta, lm = pad(rp, 0.0), pad(cen, 0.0), pad(beta, 0.0), pad(lm, -torch.inf)
+        mask = torch.cat([mask, torch.zeros_like(mask[:, :1])], 1)
     le = lm + beta
     v = cen + rp
     logs = torch.where(mask[:, None], le, lm)
@@ -227,8 +243,12 @@ def apply_best(mask, remove, add, scores):
     execute = (gain > 0) & torch.isfinite(flat).all(-1)
     rr = remove.gather(1, (j // add.shape[-1])[:, None])
     aa = add.gather(1, (j % add.shape[-1])[:, None])
-    result = mask.scatter(1, rr, ~execute[:, None])
-    result = result.scatter(1, aa, execute[:, None])
+    # rows that execute swap rr out and aa in; the others keep their mask
+    # (their argmax may name an illegal slot: a selected page or page P)
+    p = mask.shape[-1]
+    swapped = torch.cat([mask, torch.zeros_like(mask[:, :1])], 1)
+    swapped = swapped.scatter(1, rr, False).scatter(1, aa, True)[:, :p]
+    result = torch.where(execute[:, None], swapped, mask)
     return result, gain, execute, j
 
 

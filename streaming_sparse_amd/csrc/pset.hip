@@ -374,6 +374,16 @@ __global__ __launch_bounds__(256) void pset_pool_kernel(PsetParams p) {
       const int q = (sl - 16) >> 4, k = (sl - 16) & 15;
       valid = k < (q ? nuc : nuh);
       page = valid ? page_at(nmh + nmc + (q ? nuh : 0) + k) : s.spare[sl - 16];   // spare (never legal)
+      if (page < 0) {
+        // no spare page left for this slot (the reference's pool would index
+        // page P, past the window): an empty candidate -- zero mass (lm =
+        // -inf), zero values -- that adds nothing to any sum, while every
+        // page outside the pool stays in the background.  The rows kernel
+        // writes no endpoint data for it (no page maps to the slot).
+        double* c = p.cand + ((((long long)hs * p.T + t) * 16) * kCand + sl) * kCandVals;
+        for (int m = 0; m < 16; ++m)
+          for (int v = 0; v < kCandVals; ++v) c[(long long)m * kCand * kCandVals + v] = v == 0 ? -INFINITY : 0.0;
+      }
     }
     int32_t* po = p.pool + ((long long)hs * p.T + t) * kPoolInts;
     po[sl] = page;
@@ -1013,10 +1023,11 @@ int pset_launch(const void* q, long long q_head_stride, long long q_block_stride
                 double* rows, int32_t* pool, double* gain, int32_t* info, double* scores, long long* stats,
                 int total_heads, int blocks, int pages, int count, hipStream_t stream) {
   // a 72-page window (the first chunk) or a window beyond the anchor frame
-  // and the current chunk with at least 64 unselected pages
+  // and the current chunk; any table size (an add slot past the spare pages
+  // is an empty candidate)
   const bool first = pages == kCurrent;
   if (n_heads <= 0 || n_heads > total_heads || blocks <= 0 || pages > kMaxPages ||
-      (!first && (pages <= kAnchors + kCurrent || pages - count < 64)) || head_pages < pages ||
+      (!first && pages <= kAnchors + kCurrent) || head_pages < pages ||
       enc_pages < pages || count < (first ? kAnchors : 1) || count > pages ||
       heads == nullptr || probe_lse == nullptr || cand == nullptr || rows == nullptr || pool == nullptr ||
       gain == nullptr || info == nullptr || stats == nullptr)

@@ -212,3 +212,56 @@ def test_pset_first_chunk_matches_oracle(device, n):
     assert (got_ids[..., 0] == x.own).all() and got_mask[..., :24].all()
     want_ids = ref.lut(risk.cpu(), got_mask, x.own, 24 + n)
     assert torch.equal(got_ids.sort(-1).values, want_ids.sort(-1).values)
+
+
+def test_pset_short_spares_matches_oracle(device):
+    """A table too full for the stratified pool's spare pages: 216-page
+    window, A = 66 of 72 current and B = 100 of 120 history pages (190 of
+    216 selected).  Each row has 6 unselected current and 20 unselected
+    history pages, so padded current add slot k (22..31) finds no spare page
+    k and is an empty candidate: -1 in the pool, P in the oracle's (the
+    reference's spare fill value), zero mass in the scores.  Pools equal
+    (P -> -1), scores within 1e-4 of the row scale, decisions and masks
+    equal off near ties."""
+    x = workload.make_call(cfg=3, frames=9)
+    w = workload.reader_weights()
+    P = x.pages
+    a = torch.full((12,), 66, dtype=torch.int32)
+    n = 166
+    g, reader, enc = gpu_encoding(x, w, device)
+    ws = Workspace()
+    lse = torch.empty(12, 72, 16, device=device)
+    ids, mask, risk, _ = route(g.q, g.summary, g.theta, tier='intersection', own=g.own, current_slots=a, n=n,
+                               workspace=ws, lse_out=lse)
+    mask0 = mask.clone()
+    stats, rows = pset.correct(g.q, g.summary, enc, reader, risk, lse, mask, ids, g.own, HEADS, want_scores=True)
+    torch.cuda.synchronize()
+    pr = ref.probes(x.q)
+    z = ref.route_logits(pr, x.summary.keys)
+    enc_o = dict(co=enc.co.cpu(), A=enc.A.cpu(), mean=enc.mean.cpu(), detail=enc.detail.cpu())
+    m0 = mask0.cpu()
+    assert (m0.sum(-1) == 24 + n).all()
+    want_mask, orow, ostats = opset.correct(pr.bfloat16().float(), z, risk.cpu(), m0, x.own, enc_o, w['wq'], HEADS)
+    pool = rows['pool'].cpu()
+    want_add = orow['add'].masked_fill(orow['add'] == P, -1)
+    assert int((want_add == -1).sum()) >= 10 * len(HEADS) * 72
+    assert torch.equal(pool[..., :16].long(), orow['remove'])
+    assert torch.equal(pool[..., 16:48].long(), want_add)
+    legal = orow['legal'].reshape(len(HEADS), 72, 16, 32)
+    got_s = rows['scores'].cpu()
+    want_s = orow['scores']
+    assert torch.isfinite(want_s.masked_fill(~legal, 0)).all()
+    scale = want_s.masked_fill(~legal, 0).abs().flatten(-2).amax(-1).clamp_min(1e-300)
+    err = ((got_s - want_s).abs().masked_fill(~legal, 0).flatten(-2).amax(-1) / scale)
+    print(f"short spares: scores max err / row scale {float(err.max()):.2e}; gpu executed {int(stats[0])}, "
+          f"oracle executed {int(ostats[0])} of {int(ostats[1])}", flush=True)
+    assert float(err.max()) < 1e-4
+    assert int(stats[2]) == 0
+    ties = _near_tie(want_s, legal)
+    ex_g = rows['executed'].cpu().bool()
+    same = (ex_g == orow['executed']) & (~ex_g | (rows['argmax'].cpu().long() == orow['argmax']))
+    assert bool((same | ties).all())
+    hs = torch.tensor(HEADS)
+    got_mask = mask.cpu()
+    assert bool(((got_mask[hs] == want_mask[hs]).all(-1) | ties).all())
+    assert (got_mask[..., P - 72:].sum(-1) == 66).all() and got_mask[..., :24].all()

@@ -216,14 +216,21 @@ def test_c_abi_rejects_bad_shapes():
                                             hidden, N)
     assert en(73, 256) == INVALID
     assert en(72, 257) == INVALID
-    # ssa_pset: a 72-page window (the first chunk) or 96 < pages <= 512 with at least 64 unselected pages
-    ps = lambda pages, count: L.ssa_pset(N, 128, 64 * 12 * 128, 12 * 128, 0, N, pages, N, N, N, pages, N, N, N, N,
-                                         N, N, N, 3, N, N, N, N, N, N, N, 12, 72, pages, count, N)
-    assert ps(96, 40) == INVALID
+    # ssa_pset: a 72-page window (the first chunk, 24 <= count <= 72) or 96 < pages <= 512 with
+    # 1 <= count <= pages.  Every pointer the check requires is given (never dereferenced: the call
+    # returns before any launch), so the shapes alone decide.
+    D = ctypes.c_void_p(256)
+    ps = lambda pages, count, heads=D: L.ssa_pset(N, 128, 64 * 12 * 128, 12 * 128, 0, N, pages, N, N, N, pages, N,
+                                                  N, D, N, N, N, heads, 3, D, D, D, D, D, N, D, 12, 72, pages,
+                                                  count, N)
+    assert ps(96, 40) == INVALID                                      # no history partition
     assert ps(80, 40) == INVALID
+    assert ps(513, 40) == INVALID
     assert ps(72, 73) == INVALID
     assert ps(72, 23) == INVALID                                      # fewer than the 24 anchors
-    assert ps(432, 400) == INVALID
+    assert ps(432, 433) == INVALID
+    assert ps(432, 0) == INVALID
+    assert ps(432, 64, heads=N) == INVALID
     # ssa_rep_operands: heads >= 1, pages in (0, 512], ceil(pages/16) tiles, aligned output
     ro = lambda heads, pages, tiles, out=16: L.ssa_rep_operands(16, out, heads, pages, 512, tiles, N)
     assert ro(0, 432, 27) == INVALID

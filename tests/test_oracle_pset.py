@@ -103,7 +103,8 @@ def _rule_pool(risk, sel, own, p):
     rm = [page if ok else slot for slot, (page, ok) in enumerate(removes)]
     valid_adds = {page for page, ok in adds if ok}
     spare = [i for i in range(p) if not sel[i] and i not in valid_adds]
-    ad = [page if ok else spare[slot] for slot, (page, ok) in enumerate(adds)]
+    # past the spare pages a slot holds P (the reference's topk of a tensor filled with P)
+    ad = [page if ok else (spare[slot] if slot < len(spare) else p) for slot, (page, ok) in enumerate(adds)]
     legal = [[removes[x][1] and adds[y][1] and ((x < 8) == (y < 16)) for y in range(32)] for x in range(16)]
     return rm, ad, legal
 
@@ -119,14 +120,77 @@ def test_pool_rules(p):
     mask.scatter_(-1, own[..., None], True)
     mask[1, 1, p - 72:] = True                  # current partition full: no adds there
     mask[1, 2, 24:p - 72] = False               # history partition empty: no removes there
+    # nearly everything selected: 6 unselected current and 20 unselected
+    # history pages leave 4 spare pages, and padded slot k takes spare k:
+    # current slots 22..31 find none
+    mask[0, 3] = True
+    mask[0, 3, torch.arange(p - 72, p - 66)] = False
+    mask[0, 3, torch.arange(24, 44)] = False
     r, a, legal = pset.pool(risk, mask, own)
+    short = 0
     for hh in range(h):
         for tt in range(t):
             rm, ad, lg = _rule_pool(risk[hh, tt], mask[hh, tt].tolist(), int(own[hh, tt]), p)
             assert r[hh, tt].tolist() == rm
             assert a[hh, tt].tolist() == ad
             assert legal[hh, tt].tolist() == lg
-            assert len(set(rm + ad)) == 48
+            real = [x for x in rm + ad if x < p]
+            assert len(set(real)) == len(real) and len(real) + ad.count(p) == 48
+            short += ad.count(p)
+    assert a[0, 3, 22:].tolist() == [p] * 10 and a[0, 3, :22].max() < p
+    assert short == 10
+
+
+def test_empty_add_slot_equals_a_spare_page():
+    """An add slot past the spare pages holds page P, an empty candidate of
+    zero mass (pool).  It scores every legal swap as a spare page in that
+    slot does: a padded slot is an inactive add, and the reference's pool
+    comment calls such pages equivalent background terms
+    (VB/quota_pool.py:41-42).  Checked by moving a real spare page out of
+    its slot (the page goes back to the background) and comparing all legal
+    scores, and by the correction's decisions."""
+    p, b, m = 216, 3, 4
+    g = torch.Generator().manual_seed(21)
+    risk = torch.rand(1, b, p, generator=g)
+    mask = torch.rand(1, b, p, generator=g) < 0.5
+    mask[..., :24] = True
+    own = (torch.arange(b) + p - 72)[None].contiguous()
+    mask.scatter_(-1, own[..., None], True)
+    mask[0, :, p - 72:p - 62] = True             # 10 selected current pages at the partition start
+    mask[0, :, p - 62:p - 52] = False
+    mask[0, :, p - 52:] = True                   # 10 unselected current pages: 6 padded add slots
+    r, a, legal = pset.pool(risk, mask, own)
+    r, a, legal, mk = r[0], a[0], legal[0], mask[0]
+    rp = torch.randn(b, m, p, 16, generator=g, dtype=torch.float64) * 0.3
+    beta = torch.randn(b, m, p, generator=g, dtype=torch.float64) * 0.6
+    z = torch.randn(b, m, p, generator=g, dtype=torch.float64)
+    lm = z - z.logsumexp(-1, keepdim=True)
+    cen = torch.randn(b, m, p, 16, generator=g, dtype=torch.float64)
+    base = pset.grouped_scores(rp, beta, lm, cen, mk, r, a)
+    padded = ~mk.gather(1, a) & ~legal.any(1)                 # spare pages in add slots (never legal)
+    padded &= a < p
+    assert int(padded.sum(-1).min()) >= 6
+    emptied = torch.where(padded, p, a)
+    got = pset.grouped_scores(rp, beta, lm, cen, mk, r, emptied)
+    scale = base.masked_fill(~legal, 0).abs().amax()
+    err = (got - base).abs().masked_fill(~legal, 0).amax()
+    assert float(err) <= 1e-12 * float(scale), (float(err), float(scale))
+    s0 = base.masked_fill(~legal, -1e30)
+    s1 = got.masked_fill(~legal, -1e30)
+    n0, _, e0, j0 = pset.apply_best(mk, r, a, s0)
+    n1, _, e1, j1 = pset.apply_best(mk, r, emptied, s1)
+    assert torch.equal(e0, e1) and torch.equal(j0, j1) and torch.equal(n0, n1)
+
+
+def test_apply_best_leaves_rows_without_a_swap():
+    """A row with no legal pair (or no gain) keeps its mask, even when its
+    argmax names a padded slot holding a selected page or page P."""
+    mask = torch.tensor([[True, True, False, True]])
+    remove = torch.tensor([[1]])
+    add = torch.tensor([[4, 3]])                 # page 4 = P (empty), page 3 selected
+    scores = torch.full((1, 1, 2), -1e30, dtype=torch.float64)
+    new, gain, executed, j = pset.apply_best(mask, remove, add, scores)
+    assert not bool(executed[0]) and torch.equal(new, mask)
 
 
 def _rule_pool72(risk, sel, own):
