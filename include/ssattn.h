@@ -158,6 +158,15 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
               int pages, int head_pages, int count, int mode, int total, const void* detail, void* rep_ops,
               int rep_tiles, float tie_eps, int32_t* tie_rows, int32_t* tie_count, hipStream_t stream);
 
+/* Measurement only, no counterpart in the reference: the phase stamps of the
+ * last ssa_route launch, from the library built with -DSSA_ROUTE_STAMPS
+ * (python -m streaming_sparse_amd.build --route-stamps ->
+ * libssattn_stamps.so).  Copies [1024 workgroups, 4 waves, 16] uint64
+ * shader-clock stamps (lane 0 of each wave; slots 0..10 at the kernel's
+ * phase boundaries) into host memory out of `bytes` >= 524288 and returns 0
+ * after the copy; the product library returns hipErrorNotSupported. */
+int ssa_route_stamps(void* out, long long bytes);
+
 /* Page selection from given scores (RV/ops.py:113-138 RouteOps.select), one
  * row per (head, block): scores [rows,pages] fp32, own [rows] int32, valid
  * [rows,pages] 0/1 bytes or NULL (all valid).  Pages rank with own first,

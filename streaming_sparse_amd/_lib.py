@@ -17,6 +17,7 @@ _vp, _i, _ll, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_fl
 # return type of the entry points that do not return a status
 RESTYPES = {"ssa_attention_workspace_bytes": _ll}
 SIGNATURES = {
+    "ssa_route_stamps": [_vp, _ll],
     "ssa_rep_operands": [_vp, _vp, _i, _i, _i, _i, _vp],
     "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp, _ll,
                       _vp],
@@ -44,17 +45,30 @@ SIGNATURES = {
 }
 
 
+def load(path):
+    """A ctypes handle of the library at `path` with the entry points typed."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run `python -m streaming_sparse_amd.build`")
+    handle = ctypes.CDLL(path)
+    for name, args in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = args
+        fn.restype = RESTYPES.get(name, ctypes.c_int)
+    return handle
+
+
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m streaming_sparse_amd.build`")
-        handle = ctypes.CDLL(LIB_PATH)
-        for name, args in SIGNATURES.items():
-            fn = getattr(handle, name)
-            fn.argtypes = args
-            fn.restype = RESTYPES.get(name, ctypes.c_int)
-        _lib = handle
+        _lib = load(LIB_PATH)
+    return _lib
+
+
+def use(path):
+    """Route every later call of this process through the library at `path`
+    (a measurement build of the same sources, streaming_sparse_amd.build)."""
+    global _lib
+    _lib = load(path)
     return _lib
 
 

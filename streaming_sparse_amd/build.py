@@ -16,6 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libssattn.so")
+# measurement build: the same sources with the router's phase stamps compiled in
+STAMPS_LIB = os.path.join(HERE, "libssattn_stamps.so")
 SOURCES = ("attention.hip", "route.hip", "pset.hip", "summary.hip", "runtime.hip", "group.hip")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
          # packed fp32 VALU forms are excluded from code generation
@@ -40,13 +42,19 @@ def _stderr(res) -> str:
     return "\n".join(line for line in res.stderr.splitlines() if NOISE not in line)
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, route_stamps: bool = False) -> str:
+    """Compile and link the library; with route_stamps, the measurement build
+    (-DSSA_ROUTE_STAMPS: route_kernel records its phase boundaries, read by
+    ssa_route_stamps; streaming_sparse_amd.route_phases prints them) into
+    libssattn_stamps.so instead."""
     cc = hipcc()
+    target = STAMPS_LIB if route_stamps else LIB
+    defs = ["-DSSA_ROUTE_STAMPS"] if route_stamps else []
     with tempfile.TemporaryDirectory(prefix="ssattn_build_") as tmpdir:
         objs, procs = [], []
         for src in SOURCES:
             obj = os.path.join(tmpdir, src.replace(".hip", ".o"))
-            cmd = [cc, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+            cmd = [cc, *FLAGS, *defs, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
             procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
             objs.append(obj)
         errs = []
@@ -59,14 +67,14 @@ def build(verbose: bool = False) -> str:
                 print(_stderr(res), file=sys.stderr)
         if errs:
             raise RuntimeError("\n".join(errs))
-        tmp = LIB + ".tmp"
+        tmp = target + ".tmp"
         cmd = [cc, "--offload-arch=gfx950", "-fPIC", "-shared", *objs, "-o", tmp]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"link failed ({res.returncode}):\n{' '.join(cmd)}\n{_stderr(res)}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, target)
+    return target
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, route_stamps="--route-stamps" in sys.argv[1:]))

@@ -37,6 +37,24 @@ constexpr int kAnchors = 24;
 constexpr int kCurrent = 72;
 constexpr int kTilesPerWave = kMaxPages / 32;   // tiles of 8 pages, every 4th to a wave
 
+// Phase stamps of a measurement build (-DSSA_ROUTE_STAMPS, see
+// streaming_sparse_amd/build.py): lane 0 of each wave of the first
+// kStampBlocks workgroups records the shader clock (s_memtime, counted per
+// XCD: only differences within one wave are meaningful) at the kernel's
+// phase boundaries, read back by ssa_route_stamps.  The product library
+// compiles the stamps out.
+constexpr int kStampBlocks = 1024, kStampSlots = 16;
+#ifdef SSA_ROUTE_STAMPS
+__device__ unsigned long long route_stamps[kStampBlocks * 4 * kStampSlots];
+#define ROUTE_STAMP(k)                                                                       \
+  do {                                                                                       \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < kStampBlocks)                                \
+      route_stamps[(blockIdx.x * 4 + (threadIdx.x >> 6)) * kStampSlots + (k)] = __builtin_amdgcn_s_memtime(); \
+  } while (0)
+#else
+#define ROUTE_STAMP(k) ((void)0)
+#endif
+
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
@@ -223,6 +241,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     return;
   }
   const int work = xcd_remap(blockIdx.x, p.H * NP);
+  ROUTE_STAMP(0);
   const int h = work / NP, t0 = 2 * (work % NP);
   const int P = p.P;
   const int pi = lane & 31, hh = lane >> 5;
@@ -303,6 +322,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   for (int st = 0; st < 8; ++st) asm volatile("" ::"v"(qop[st]));
 #pragma unroll
   for (int i = 0; i < 8; ++i) asm volatile("" ::"v"(bw[i]));
+  ROUTE_STAMP(1);   // the setup's loads are in
   // the first two rep tiles are in flight during the rest of the setup
   issue_tile(mine(0), 0, true);
   issue_tile(mine(1), 1, true);
@@ -385,6 +405,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   const uint32_t lo_only = hh == 0 ? 0xffffffffu : 0u;
   float mx = -INFINITY, den = 0.f;
   float vals[kTilesPerWave][4], mj[kTilesPerWave];
+  ROUTE_STAMP(2);   // probe norms, B operands, first tiles issued
   auto soft = [&](f32x16 S, const TileStats& ts, int tile, float (&v4)[4], float& mt) {
     const u32x4 ag = {ts.w01[0], ts.w01[1], ts.w23[0], ts.w23[1]};
     const uint32_t st8 = ts.w45[0] & 0xffffu, st9 = ts.w45[0] >> 16, st10 = ts.w45[1] & 0xffffu;
@@ -442,6 +463,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     }
   }
   wait_loads();                                      // the ring takes the probe sums, then the selection
+  ROUTE_STAMP(3);   // tiles done
   {
     const float omx = __shfl_xor(mx, 32), oden = __shfl_xor(den, 32);
     const float mm = fmaxf(mx, omx);
@@ -461,6 +483,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) DEN += s.part[w][pi][1] * __builtin_amdgcn_exp2f(s.part[w][pi][0] - MX);
   const float nlse = -(MX + __log2f(DEN));
+  ROUTE_STAMP(4);   // probe totals
   if (p.lse && wave == 0 && hh == 0 && t0 + blk < p.T)
     p.lse[((long long)h * p.T + t0 + blk) * 16 + m] = (MX + __log2f(DEN)) * 0.69314718055994531f;
   // page values: rescaled into LDS by probe ([block][page][probe], the tile
@@ -481,6 +504,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   }
   __syncthreads();
   const int nrow = min(2, p.T - t0);
+  ROUTE_STAMP(5);   // page values in LDS
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
     for (int pg = tid; pg < P; pg += kThreads) {
@@ -495,6 +519,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   }
   __syncthreads();
   if (p.mode < 0) return;
+  ROUTE_STAMP(6);   // probe sums, risk rows written
 
   // ---------------------------------------------------------------- select
   Sel& sl = *reinterpret_cast<Sel*>(&s.ring[0][0][0]);
@@ -543,12 +568,15 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     }
     keys[i] = key;
   }
+  ROUTE_STAMP(7);   // sort keys
   sort512_desc(keys, bt, sl.key[b]);
+  ROUTE_STAMP(8);   // sorted
 #pragma unroll
   for (int i = 0; i < 4; ++i) sl.key[b][4 * bt + i] = keys[i];
   __syncthreads();
   // sl.key[b] sorted descending; the page of entry i is 1023 - (key & 1023)
   auto page_at = [&](int i) -> int { return 1023 - (int)(sl.key[b][i] & 1023ull); };
+  ROUTE_STAMP(9);   // sorted keys in LDS
   const bool row_ok = b < nrow;
   if (p.tie_rows && bt == 0 && row_ok) {
     // Near ties at the selection boundaries, in the sorted runs of the
@@ -634,6 +662,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
     for (int pg = bt; pg < P; pg += 128)
       if (row_ok) p.mask[((long long)h * p.T + t0 + b) * P + pg] = sl.sel[b][pg];
   }
+  ROUTE_STAMP(10);  // table, near-tie report and mask written
 }
 
 
@@ -745,6 +774,20 @@ __global__ __launch_bounds__(128) void select_kernel(SelectParams p) {
 }  // namespace
 
 extern "C" {
+
+// Phase stamps of the last ssa_route launch in a measurement build: copies
+// [kStampBlocks, 4 waves, 16] uint64 into `out` (host memory, `bytes` >= its
+// size) and returns 0; hipErrorNotSupported in the product library.
+int ssa_route_stamps(void* out, long long bytes) {
+#ifdef SSA_ROUTE_STAMPS
+  if (out == nullptr || bytes < (long long)sizeof(route_stamps)) return (int)hipErrorInvalidValue;
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(route_stamps), sizeof(route_stamps));
+#else
+  (void)out;
+  (void)bytes;
+  return (int)hipErrorNotSupported;
+#endif
+}
 
 // mode: -1 risk only; 0 base (own + 24 anchors + top C-25); 1 anchor/current/
 // history quota with `total` = A+B non-anchor pages and current[h] = A;

@@ -25,7 +25,7 @@ def test_header_declares_entry_points():
                                "ssa_summary", "ssa_summary_write", "ssa_pset_noalloc", "ssa_anchor_rebase", "ssa_commit_pages",
                                "ssa_summary_layers", "ssa_encode_layers", "ssa_anchor_rebase_layers",
                                "ssa_commit_pages_layers",
-                               "ssa_group_order"}
+                               "ssa_group_order", "ssa_route_stamps"}
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libssattn.so not built")
@@ -35,3 +35,11 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(handle, name), name
         assert len(_lib.SIGNATURES[name]) == nargs, name
     _lib.lib()
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libssattn.so not built")
+def test_product_library_has_no_phase_stamps():
+    """The router's phase stamps exist only in the measurement build: the
+    product library's ssa_route_stamps reports hipErrorNotSupported (801)
+    without touching its arguments."""
+    assert _lib.lib().ssa_route_stamps(None, 0) == 801
