@@ -116,7 +116,9 @@ long long ssa_attention_workspace_bytes(int n_tokens, int heads, int pages, int 
  * h*q_head_stride + t*q_block_stride + m*q_row_stride; gathered=0 -> q is the
  * query tensor and probe m of block t is query row 64t + offset[m] with
  * offsets {0,4,8,13,17,21,25,29,34,38,42,46,50,55,59,63}.
- * keys [H,head_pages,4,128] bf16, stats [H,head_pages,4,12] bf16, theta
+ * keys [H,head_pages,4,128] bf16, stats [H,head_pages,4,12] bf16 in the
+ * reference's summary contract (RV/ops.py:66-75; slots 0..7 are mean squares,
+ * >= 0, so the feature sqrt(max(u, 0)) is taken as sqrt(|u|)), theta
  * [H,4] fp32, own [H,blocks] int32 or NULL (own = pages - blocks + t).
  * mode 0: base tier, ids = [own, 0..23, top count-25 by risk];
  * mode 1: anchor/current/history quota (VB/quota_mask.py:7-39), total = A+B
