@@ -1,7 +1,8 @@
-"""The full streaming workload at its real size, through size-independent
-properties (the oracle would take hours here): 30 layers x 12 heads, 4
+"""The full streaming workload at its real size: 30 layers x 12 heads, 4
 denoise steps + the clean step, a 360-page history ring (432-page window),
-Full_Pset on layers {3,4,5,8,14,17,27} x heads {3,4,9} at step 0.
+Full_Pset on layers {3,4,5,8,14,17,27} x heads {3,4,9} at step 0.  The
+oracle would take hours over a whole chunk, so the whole chunk is checked
+through size-independent properties and single calls against the oracle.
 
 Two runtimes built from the same seed run chunks 0..6 (the window fills at
 chunk 5; chunk 6 runs after the ring wrapped and the anchor was rebased):
@@ -10,7 +11,9 @@ chunk 5; chunk 6 runs after the ring wrapped and the anchor was rebased):
   order-dependent reductions anywhere on the path);
 * the call counts are the workload's: 116 sparse calls (7 with Full_Pset)
   and 34 dense ones per full-window chunk;
-* every output is finite."""
+* every output is finite;
+and, against the oracle, one Full_Pset call of chunk 7 (page table and
+output), its first (dense) call and its commit grouping on three layers."""
 import pytest
 import torch
 
@@ -119,3 +122,49 @@ def test_full_stream_call_matches_oracle(device):
     print(f"full-size call: {int(same.sum())}/864 tables equal the oracle chain, {int(ties.sum())} near-tie rows",
           flush=True)
     assert bool((same | ties).all())
+
+
+def test_full_stream_dense_call_and_commit_match_oracle(device):
+    """The rest of a full-window chunk against the oracle: after chunks 0..6,
+    chunk 7 runs whole.  Its first call (step 0, layer 0: dense, every one
+    of the 432 pages exact, single-term P.V) matches dense attention over
+    the window as the call saw it, on 4 query blocks x 12 heads; and its
+    clean step's token grouping equals the float64 oracle's order token for
+    token on three of the 30 layers (12 heads each; the first chunk's frame
+    sort does not apply), with the ring's page order of a 360-page history."""
+    from oracle import group as og
+    from oracle import reference as ref
+    from streaming_sparse_amd.runtime import CURRENT
+
+    rt, _ = run(device)
+    inputs = rt.chunk_inputs()
+    rt.begin_chunk()
+    P = rt.ring.n + CURRENT
+    assert P == 432
+    L0 = rt.layers[0]
+    q, k, v = inputs[0][0]
+    out = rt.layer_call(0, 0, q, k, v).clone()
+    kw, vw = L0.k[:, :64 * P].clone(), L0.v[:, :64 * P].clone()
+    for step in range(rt.cfg.steps + 1):
+        for layer in range(rt.cfg.layers):
+            if (step, layer) != (0, 0):
+                rt.layer_call(step, layer, *inputs[step][layer])
+    rt.commit_chunk(inputs)
+    torch.cuda.synchronize()
+    assert rt.dense_window() is False and rt.calls['dense'] > 0
+    tiles = [0, 23, 48, 71]
+    rows = torch.cat([torch.arange(t * 64, (t + 1) * 64) for t in tiles])
+    want = ref.dense_attention(q[:, rows].cpu(), kw.cpu(), vw.cpu()).bfloat16().float()
+    got = out[:, rows].cpu().float()
+    err, mx = ref.rel_l2(got, want), float((got - want).abs().max())
+    print(f"full-size dense call: rel-L2 {err:.3e} max-abs {mx:.3e}", flush=True)
+    assert err <= 5e-3 and mx <= 2e-2
+    order = rt.last_order.cpu()
+    w = rt.group_weights
+    pages = og.page_order(rt.cfg.history_pages)
+    for layer in (1, 14, 29):
+        want_o = og.group_order(inputs.clean_k[layer].cpu().transpose(0, 1), inputs.clean_v[layer].cpu().transpose(0, 1),
+                                w.bank[layer].cpu(), w.group_v[layer].cpu(), w.gate[layer].cpu(), pages=pages)
+        same = (order[layer].long() == want_o).all(-1)
+        print(f"full-size commit, layer {layer}: {int(same.sum())}/12 heads in the oracle's order", flush=True)
+        assert torch.equal(order[layer].long(), want_o)
