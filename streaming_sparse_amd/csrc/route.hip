@@ -98,6 +98,7 @@ struct Sel {                   // selection state, aliasing the tile ring once t
 struct Smem {
   alignas(16) uint8_t ring[4][2][kSlotBytes];   // per-wave double buffer of rep tiles
   float part[4][32][2];        // per-wave (max, sum) of each probe
+  float bmax[4];               // per-wave maximum of stats[p,1,11]
   float risk[2][kMaxPages];
 };
 static_assert(sizeof(Sel) <= sizeof(Smem::ring), "selection state must fit in the tile ring");
@@ -246,7 +247,6 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   const int P = p.P;
   const int pi = lane & 31, hh = lane >> 5;
   const int blk = pi >> 4, m = pi & 15;
-  const int tq = min(t0 + blk, p.T - 1);
 
   const uint16_t* rkh = p.rk + (long long)h * p.HP * 4 * kHeadDim;
   const uint16_t* sth = p.stats + (long long)h * p.HP * 48;
@@ -293,17 +293,36 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   // the first rep tiles go out: the compiler's wait for one of these loads
   // would otherwise also wait for tile loads issued after it.
   //
-  // probe operand (B): dims 16*st + 8*hh + [0,8) (the k order of read_reps)
-  const long long row = p.gathered ? m : probe_row(m);
-  const uint16_t* qp = p.q + (long long)h * p.q_head + (long long)tq * p.q_block + row * p.q_row;
-  u32x4 qop[8];
+  // probe rows: the workgroup's 32 probes (row r: block t0 + r / 16, probe
+  // r % 16) go into this wave's ring slot 1 by 8 row-coalesced 1 KB loads,
+  // 4 rows each with their chunks swizzled as a rep tile's (gathering each
+  // lane's 16-byte operand pieces from global memory instead costs the
+  // address unit one row per lane and load); slot 1 takes the wave's second
+  // rep tile once the operand is read.
+  {
+    const uint16_t* qb = p.q + (long long)h * p.q_head + (long long)t0 * p.q_block;
 #pragma unroll
-  for (int st = 0; st < 8; ++st) qop[st] = ldg16(qp + 16 * st + 8 * hh);
-  // max_p stats[p,1,11] over the head's pages, in every wave (pages <= 512:
-  // up to 8 per lane), so the tiles need no barrier first
-  uint32_t bw[8];
+    for (int jj = 0; jj < 8; ++jj) {
+      const int r = 4 * jj + (lane >> 4);
+      const int dt = min(t0 + (r >> 4), p.T - 1) - t0;
+      const long long prow = p.gathered ? (r & 15) : probe_row(r & 15);
+      const int chunk = (lane & 15) ^ (r & 15);
+      const uint32_t off = (uint32_t)(2 * (dt * p.q_block + prow * p.q_row + 8 * chunk));
+      dma16(qb, off, ring_addr + kSlotBytes + jj * 1024);
+    }
+  }
+  // max_p stats[p,1,11] over the head's pages: wave w reads pages
+  // 128 w + lane and 128 w + 64 + lane (pages <= 512), the workgroup
+  // combines the four partial maxima in LDS before the tiles (each page's
+  // value is a lone 2-byte word, so a wave's loads cost the address unit one
+  // cache line per lane: reading every page in every wave queued 8 such
+  // loads per wave behind one another)
+  uint32_t bw[2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) bw[i] = lane + 64 * i < P ? sth[(long long)(lane + 64 * i) * 48 + 23] : 0xff80u;
+  for (int i = 0; i < 2; ++i) {
+    const int pg = 128 * wave + 64 * i + lane;
+    bw[i] = pg < P ? sth[(long long)pg * 48 + 23] : 0xff80u;
+  }
   auto uniform = [](float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v))); };
   const float th0 = uniform(p.theta[h * 4 + 0]), th1 = uniform(p.theta[h * 4 + 1]);
   const float th2 = uniform(p.theta[h * 4 + 2]), th3 = uniform(p.theta[h * 4 + 3]);
@@ -319,10 +338,14 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   asm volatile("" ::"s"(own_raw[0]), "s"(own_raw[1]), "s"(cur_raw));
   // the loads above are complete past this point
 #pragma unroll
-  for (int st = 0; st < 8; ++st) asm volatile("" ::"v"(qop[st]));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) asm volatile("" ::"v"(bw[i]));
+  for (int i = 0; i < 2; ++i) asm volatile("" ::"v"(bw[i]));
+  wait_loads();
   ROUTE_STAMP(1);   // the setup's loads are in
+  // probe operand (B): dims 16*st + 8*hh + [0,8) of probe pi, the k order of
+  // read_reps
+  u32x4 qop[8];
+  read_reps(ring + kSlotBytes, lane, qop);
+  wait_lds();
   // the first two rep tiles are in flight during the rest of the setup
   issue_tile(mine(0), 0, true);
   issue_tile(mine(1), 1, true);
@@ -346,10 +369,10 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   for (int g = 0; g < 8; ++g) qsum += q2[g];
   const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
 
-  float bmax = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) bmax = fmaxf(bmax, bf16_to_f32(bw[i]));
-  bmax = wave_max(bmax);
+  float bmax = wave_max(fmaxf(bf16_to_f32(bw[0]), bf16_to_f32(bw[1])));
+  if (lane == 0) s.bmax[wave] = bmax;
+  __syncthreads();
+  bmax = fmaxf(fmaxf(s.bmax[0], s.bmax[1]), fmaxf(s.bmax[2], s.bmax[3]));
 
   // One pass over the reps.  Each lane keeps a running max m and sum of
   // exponentials den of its probe over its reps; the features of a page are
