@@ -178,36 +178,53 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers la
       bas1[2 * w + 1] = bf16_hi(b1[w]);
     }
   }
+  // The page's K and V rows reach LDS by row-coalesced 1 KB DMA loads (wave
+  // w: rows 16 w .. 16 w + 15, 4 rows per load, each lane one 16-byte chunk
+  // at its swizzled place); a load in which every lane read a piece of its
+  // own token's row would cost the address unit 64 rows per instruction.
+  const uint16_t* ksrc = p.src_k ? p.src_k + (long long)pl * 64 * p.src_tok + (long long)h * p.src_head : p.k + base;
+  const uint16_t* vsrc = p.src_k ? p.src_v + (long long)pl * 64 * p.src_tok + (long long)h * p.src_head : p.v + base;
+  const long long stok = p.src_k ? p.src_tok : p.kv_tok;
+  {
+    const uint32_t kl = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)s.K);
+    const uint32_t vl = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)s.V);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int r = 16 * wave + 4 * jj + (lane >> 4);
+      const uint32_t off = (uint32_t)(2 * (r * stok + 8 * ((lane & 15) ^ (r & 15))));
+      const uint32_t dst = (uint32_t)((16 * wave + 4 * jj) * 256);
+      dma16(ksrc, off, kl + dst);
+      dma16(vsrc, off, vl + dst);
+    }
+  }
+  wait_loads();
+  __syncthreads();
+  if (p.src_k) {
+    // write-through: the same rows into the window, 4 rows per store
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int r = 16 * wave + 4 * jj + (lane >> 4), c = lane & 15;
+      const int at = r * 64 + 4 * (c ^ (r & 15));
+      const long long dst = base + (long long)r * p.kv_tok + 8 * c;
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.k) + dst) = *reinterpret_cast<const u32x4*>(&s.K[at]);
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.v) + dst) = *reinterpret_cast<const u32x4*>(&s.V[at]);
+    }
+  }
+  // thread (token lane, quarter wave): dims 32 wave .. 32 wave + 31 of its
+  // key in registers for the distance passes, and its share of |v|^2
   float kr[32];
   {
-    const long long crow = base + lane * p.kv_tok + 32 * wave;
-    const long long srow = ((long long)pl * 64 + lane) * p.src_tok + (long long)h * p.src_head + 32 * wave;
-    const uint16_t* kp = p.src_k ? p.src_k + srow : p.k + crow;
-    const uint16_t* vp = p.src_k ? p.src_v + srow : p.v + crow;
-    u32x4 a[4], b[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      a[j] = ldg16(kp + 8 * j);
-      b[j] = ldg16(vp + 8 * j);
-    }
-    if (p.src_k) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.k) + crow + 8 * j) = a[j];
-        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(p.v) + crow + 8 * j) = b[j];
-      }
-    }
     float vn = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int chunk = (4 * wave + j) ^ (lane & 15);
-      *reinterpret_cast<u32x4*>(&s.K[lane * 64 + 4 * chunk]) = a[j];
-      *reinterpret_cast<u32x4*>(&s.V[lane * 64 + 4 * chunk]) = b[j];
+      const u32x4 a = *reinterpret_cast<const u32x4*>(&s.K[lane * 64 + 4 * chunk]);
+      const u32x4 b = *reinterpret_cast<const u32x4*>(&s.V[lane * 64 + 4 * chunk]);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        kr[8 * j + 2 * w] = bf16_lo(a[j][w]);
-        kr[8 * j + 2 * w + 1] = bf16_hi(a[j][w]);
-        const float x0 = bf16_lo(b[j][w]), x1 = bf16_hi(b[j][w]);
+        kr[8 * j + 2 * w] = bf16_lo(a[w]);
+        kr[8 * j + 2 * w + 1] = bf16_hi(a[w]);
+        const float x0 = bf16_lo(b[w]), x1 = bf16_hi(b[w]);
         vn = fmaf(x0, x0, vn);
         vn = fmaf(x1, x1, vn);
       }
