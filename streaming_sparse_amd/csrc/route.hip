@@ -109,12 +109,6 @@ static_assert(sizeof(Sel) <= sizeof(Smem::ring), "selection state must fit in th
 __device__ __forceinline__ float max3f(float a, float b, float c) { return __builtin_fmaxf(__builtin_fmaxf(a, b), c); }
 __device__ __forceinline__ float max2f(float a, float b) { return __builtin_fmaxf(a, b); }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-
 // Rep tiles reach LDS by 16-byte global->LDS loads, 1 KB per wave
 // instruction: load jj fills rows 4jj..4jj+3 of the tile, lane l the 16 bytes
 // of row 4jj + l/16 at physical chunk l%16, which holds logical chunk
@@ -361,7 +355,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
       const float a = bf16_lo(qop[st][w]), b = bf16_hi(qop[st][w]);
       part += a * a + b * b;
     }
-    const float other = __shfl_xor(part, 32);
+    const float other = xor_lane<32>(part);
     q2[st] = (part + other) / kHeadDim;
   }
   float qsum = 0.f;
@@ -369,7 +363,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   for (int g = 0; g < 8; ++g) qsum += q2[g];
   const float qn = sqrtf(qsum * kHeadDim) / sqrtf((float)kHeadDim);
 
-  float bmax = wave_max(fmaxf(bf16_to_f32(bw[0]), bf16_to_f32(bw[1])));
+  float bmax = wave_reduce(fmaxf(bf16_to_f32(bw[0]), bf16_to_f32(bw[1])), [](float a, float b) { return fmaxf(a, b); });
   if (lane == 0) s.bmax[wave] = bmax;
   __syncthreads();
   bmax = fmaxf(fmaxf(s.bmax[0], s.bmax[1]), fmaxf(s.bmax[2], s.bmax[3]));
@@ -488,7 +482,7 @@ __global__ __launch_bounds__(kThreads, 2) void route_kernel(RouteParams p) {
   wait_loads();                                      // the ring takes the probe sums, then the selection
   ROUTE_STAMP(3);   // tiles done
   {
-    const float omx = __shfl_xor(mx, 32), oden = __shfl_xor(den, 32);
+    const float omx = xor_lane<32>(mx), oden = xor_lane<32>(den);
     const float mm = fmaxf(mx, omx);
     const float mu = mm == -INFINITY ? 0.f : mm;   // a wave without tiles (P <= 24) has none
     den = den * __builtin_amdgcn_exp2f(mx - mu) + oden * __builtin_amdgcn_exp2f(omx - mu);
