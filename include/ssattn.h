@@ -162,12 +162,25 @@ int ssa_route(const void* q, long long q_head_stride, long long q_block_stride, 
 
 /* Measurement only, no counterpart in the reference: the phase stamps of the
  * last ssa_route launch, from the library built with -DSSA_ROUTE_STAMPS
- * (python -m streaming_sparse_amd.build --route-stamps ->
- * libssattn_stamps.so).  Copies [1024 workgroups, 4 waves, 16] uint64
- * shader-clock stamps (lane 0 of each wave; slots 0..10 at the kernel's
- * phase boundaries) into host memory out of `bytes` >= 524288 and returns 0
- * after the copy; the product library returns hipErrorNotSupported. */
+ * (python -m streaming_sparse_amd.build --stamps -> libssattn_stamps.so).
+ * Copies [1024 workgroups, 4 waves, 16] uint64 shader-clock stamps (lane 0
+ * of each wave; slots 0..10 at the kernel's phase boundaries) into host
+ * memory out of `bytes` >= 524288 and returns 0 after the copy; the product
+ * library returns hipErrorNotSupported. */
 int ssa_route_stamps(void* out, long long bytes);
+
+/* Measurement only, no counterpart in the reference: the step stamps of the
+ * last one-block attention launch (ssa_attention without the every-page
+ * flag), from the same measurement build (-DSSA_ATTN_STAMPS).  Copies
+ * [1024 workgroups, 4 waves, 296] uint64 into host memory out of `bytes` >=
+ * 9699328 and returns 0 after the copy; the product library returns
+ * hipErrorNotSupported.  A wave's record: 0 start, 1 unit list built,
+ * 2 prologue done, 3 paired steps done, 4 last units done, 5 key halves
+ * exchanged (shader clock, per XCD); 6 npages | nunits << 16 | ibeg << 32 |
+ * (end of the paired steps) << 48; 7 HW_ID | XCC_ID << 32; then three clock
+ * stamps per paired step k (unit ibeg + k, k < 96): step start, body done,
+ * loads waited for. */
+int ssa_attn_stamps(void* out, long long bytes);
 
 /* Page selection from given scores (RV/ops.py:113-138 RouteOps.select), one
  * row per (head, block): scores [rows,pages] fp32, own [rows] int32, valid

@@ -18,6 +18,7 @@ _vp, _i, _ll, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_fl
 RESTYPES = {"ssa_attention_workspace_bytes": _ll}
 SIGNATURES = {
     "ssa_route_stamps": [_vp, _ll],
+    "ssa_attn_stamps": [_vp, _ll],
     "ssa_rep_operands": [_vp, _vp, _i, _i, _i, _i, _vp],
     "ssa_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _ll, _ll, _i, _vp, _ll,
                       _vp],

@@ -16,7 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libssattn.so")
-# measurement build: the same sources with the router's phase stamps compiled in
+# measurement build: the same sources with the router's phase stamps and the
+# attention kernel's step stamps compiled in
 STAMPS_LIB = os.path.join(HERE, "libssattn_stamps.so")
 SOURCES = ("attention.hip", "route.hip", "pset.hip", "summary.hip", "runtime.hip", "group.hip")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -42,14 +43,16 @@ def _stderr(res) -> str:
     return "\n".join(line for line in res.stderr.splitlines() if NOISE not in line)
 
 
-def build(verbose: bool = False, route_stamps: bool = False) -> str:
-    """Compile and link the library; with route_stamps, the measurement build
-    (-DSSA_ROUTE_STAMPS: route_kernel records its phase boundaries, read by
-    ssa_route_stamps; streaming_sparse_amd.route_phases prints them) into
-    libssattn_stamps.so instead."""
+def build(verbose: bool = False, stamps: bool = False) -> str:
+    """Compile and link the library; with stamps, the measurement build into
+    libssattn_stamps.so instead: -DSSA_ROUTE_STAMPS (route_kernel records its
+    phase boundaries, read by ssa_route_stamps and printed by
+    streaming_sparse_amd.route_phases) and -DSSA_ATTN_STAMPS (attn_kernel
+    records its steps, read by ssa_attn_stamps and printed by
+    streaming_sparse_amd.attn_steps)."""
     cc = hipcc()
-    target = STAMPS_LIB if route_stamps else LIB
-    defs = ["-DSSA_ROUTE_STAMPS"] if route_stamps else []
+    target = STAMPS_LIB if stamps else LIB
+    defs = ["-DSSA_ROUTE_STAMPS", "-DSSA_ATTN_STAMPS"] if stamps else []
     with tempfile.TemporaryDirectory(prefix="ssattn_build_") as tmpdir:
         objs, procs = [], []
         for src in SOURCES:
@@ -77,4 +80,4 @@ def build(verbose: bool = False, route_stamps: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True, route_stamps="--route-stamps" in sys.argv[1:]))
+    print(build(verbose=True, stamps="--stamps" in sys.argv[1:]))

@@ -79,6 +79,28 @@ struct AttnParams {
 // epilogue's lane layout), then m [qw][32] and l [qw][32].
 constexpr int kPieceFloats = 2 * 16 * 64 * 4 + 2 * 64;
 
+// Step stamps of a measurement build (-DSSA_ATTN_STAMPS, see
+// streaming_sparse_amd/build.py): in the one-block kernels, lane 0 of each
+// wave of the first kAStampWGs workgroups records the shader clock
+// (s_memtime, counted per XCD: only differences within one wave are
+// meaningful) into LDS and copies the record out at the end, read back by
+// ssa_attn_stamps.  Record of a wave (uint64): 0 start, 1 unit list built,
+// 2 prologue done, 3 paired steps done, 4 last units done, 5 key halves
+// exchanged, 6 npages | nunits << 16 | ibeg << 32 | (end of the paired
+// steps) << 48, 7 HW_ID | XCC_ID << 32; then per paired step k (unit ibeg + k)
+// three stamps: step start (after the previous barrier), body and max update
+// done, loads waited for (before the barrier).  The product library compiles
+// the stamps out.
+constexpr int kAStampWGs = 1024, kAStampSteps = 96, kAStampRec = 8 + 3 * kAStampSteps;
+#ifdef SSA_ATTN_STAMPS
+__device__ unsigned long long attn_stamps[kAStampWGs * 4 * kAStampRec];
+#define ATTN_TICK(k) tick(k)
+#define ATTN_STAMP(k, v) stamp(k, v)
+#else
+#define ATTN_TICK(k) ((void)0)
+#define ATTN_STAMP(k, v) ((void)0)
+#endif
+
 // K tile: 16-byte chunk c of row r at chunk c ^ (r & 15).
 __device__ __forceinline__ int k_off(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
 // V tile: chunk c of row r at chunk c ^ vswz(r & 3); keeps the transpose reads
@@ -498,6 +520,14 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   __shared__ float xm[NB][2][64], xl[NB][2][64];
   __shared__ int nunits_s, nexact_s, wcount[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#ifdef SSA_ATTN_STAMPS
+  __shared__ unsigned long long stl[4][kAStampRec];
+  auto stamp = [&](int slot, unsigned long long v) {
+    if (NB == 1 && lane == 0 && slot < kAStampRec) stl[wave & 3][slot] = v;
+  };
+  auto tick = [&](int slot) { stamp(slot, __builtin_amdgcn_s_memtime()); };
+#endif
+  ATTN_TICK(0);
   const int grp = wave >> 2, pair = (wave >> 1) & 1, qw = wave & 1;
   const int TB = p.T / NB;
   // whole tiles first (XCD-grouped), then the pieces of the split tiles
@@ -534,6 +564,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     if (tid == 0) nunits_s = nexact_s = p.P;
   }
   __syncthreads();
+  ATTN_TICK(1);
   const int nunits = __builtin_amdgcn_readfirstlane(nunits_s);
   // the piece state's slot: tile (work - split_from) of the split ones, or
   // every tile in a staged call
@@ -583,6 +614,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
   float bias = unit_max(S0, unit(ibeg), pair, lane, p.scale_log2, mloc);
   update_max(mloc, rm, ls, O, C);
   __syncthreads();   // every wave is done with K slot 0 before unit 2's K lands there
+  ATTN_TICK(2);
   // Unit ids run ahead in registers (u0 = unit i); the id of unit i+3 is
   // read from LDS in step i-1, so the read completes at its barrier.
   int u0 = unit(ibeg), u1 = unit(min(ibeg + 1, iend - 1)), u2 = unit(min(ibeg + 2, iend - 1));
@@ -824,6 +856,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     constexpr int K = decltype(kind)::value;
     constexpr int cur = decltype(parity)::value;   // i & 1: every paired loop keeps i even
     const int u3 = __builtin_amdgcn_readfirstlane(u3raw);
+    ATTN_TICK(8 + 3 * (i - ibeg));
     // the general call issues its loads first; the two-block call (8 waves,
     // half the loads each) spreads them over the first products
     if (NB == 1) {
@@ -837,11 +870,13 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       page_body(kind, cur, Sc, Sn, nb);
     update_max(mloc, rm, ls, O, C);
     if (NB == 1) __builtin_amdgcn_s_setprio(0);
+    ATTN_TICK(9 + 3 * (i - ibeg));
     u0 = u1;
     u1 = u2;
     u2 = u3;
     u3raw = units[min(i + 4, iend - 1)];
     wait_loads();
+    ATTN_TICK(10 + 3 * (i - ibeg));
     __syncthreads();
   };
   // Units are the exact pages, then the rep tiles; every step knows the kind
@@ -874,6 +909,9 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       step(RepUnits{}, RepUnits{}, Odd{}, i + 1, S1, S0);
     }
   }
+  ATTN_TICK(3);
+  ATTN_STAMP(6, (unsigned long long)npages | (unsigned long long)nunits << 16 | (unsigned long long)ibeg << 32 |
+               (unsigned long long)i << 48);
   // one unit with a successor left (units i and i+1 = iend - 1): the same
   // work without the interleaving, each kind chosen at run time
   auto unit_pv = [&](int cur, const f32x16& Sc, float nb) {
@@ -920,6 +958,7 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
       for (int dt = 0; dt < 4; ++dt) O[dt] = mfma32(bop[dt], cb, O[dt]);
     }
   }
+  ATTN_TICK(4);
   __syncthreads();
   // merge the two key halves: pair 1 hands (m, l, O) to pair 0 through LDS.
   // Lanes l and l ^ 32 hold the fp32 partial sums of one query's two 16-key
@@ -941,6 +980,16 @@ __global__ __launch_bounds__(kThreads * NB, 2 / NB) void attn_kernel(AttnParams 
     xl[grp][qw][lane] = l;
   }
   __syncthreads();
+#ifdef SSA_ATTN_STAMPS
+  tick(5);
+  stamp(7, (unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 4) |
+               (unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32);
+  if (NB == 1 && blockIdx.x < kAStampWGs) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's stamp writes
+    for (int k = lane; k < kAStampRec; k += 64)
+      attn_stamps[((long long)blockIdx.x * 4 + wave) * kAStampRec + k] = stl[wave & 3][k];
+  }
+#endif
   if (pair == 1) return;
   const float m1 = xm[grp][qw][lane], l1 = xl[grp][qw][lane];
   const float m = rm.m;
@@ -1102,6 +1151,21 @@ long long staged_bytes(int wgs) { return (long long)wgs * 2 * kPieceFloats * 4; 
 }  // namespace
 
 extern "C" {
+
+// Step stamps of the last one-block attention launch in a measurement build:
+// copies [kAStampWGs, 4 waves, kAStampRec] uint64 into `out` (host memory,
+// `bytes` >= its size) and returns 0; hipErrorNotSupported in the product
+// library.
+int ssa_attn_stamps(void* out, long long bytes) {
+#ifdef SSA_ATTN_STAMPS
+  if (out == nullptr || bytes < (long long)sizeof(attn_stamps)) return (int)hipErrorInvalidValue;
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(attn_stamps), sizeof(attn_stamps));
+#else
+  (void)out;
+  (void)bytes;
+  return (int)hipErrorNotSupported;
+#endif
+}
 
 long long ssa_attention_workspace_bytes(int n_tokens, int heads, int pages, int count, int flags) {
   if (n_tokens <= 0 || n_tokens % 64 || heads <= 0 || pages <= 0 || count <= 0 || count > pages) return -1;

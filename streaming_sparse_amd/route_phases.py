@@ -1,10 +1,10 @@
 """Per-phase time of the router kernel, from the measurement build.
 
-    python -m streaming_sparse_amd.build --route-stamps
+    python -m streaming_sparse_amd.build --stamps
     python -m streaming_sparse_amd.route_phases
 
 The measurement build (libssattn_stamps.so, the same sources compiled with
--DSSA_ROUTE_STAMPS) has lane 0 of every router wave record the shader clock
+-DSSA_ROUTE_STAMPS and -DSSA_ATTN_STAMPS) has lane 0 of every router wave record the shader clock
 at the kernel's phase boundaries.  This module runs the full-window base and
 intersection calls (12 heads x 4608 queries, 432 pages) through that library
 after a warm-up, reads the stamps of the last launch (ssa_route_stamps) and

@@ -25,7 +25,7 @@ def test_header_declares_entry_points():
                                "ssa_summary", "ssa_summary_write", "ssa_pset_noalloc", "ssa_anchor_rebase", "ssa_commit_pages",
                                "ssa_summary_layers", "ssa_encode_layers", "ssa_anchor_rebase_layers",
                                "ssa_commit_pages_layers",
-                               "ssa_group_order", "ssa_route_stamps"}
+                               "ssa_group_order", "ssa_route_stamps", "ssa_attn_stamps"}
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libssattn.so not built")
@@ -39,7 +39,9 @@ def test_library_exports_every_declared_symbol():
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libssattn.so not built")
 def test_product_library_has_no_phase_stamps():
-    """The router's phase stamps exist only in the measurement build: the
-    product library's ssa_route_stamps reports hipErrorNotSupported (801)
-    without touching its arguments."""
+    """The router's phase stamps and the attention kernel's step stamps exist
+    only in the measurement build: the product library's ssa_route_stamps and
+    ssa_attn_stamps report hipErrorNotSupported (801) without touching their
+    arguments."""
     assert _lib.lib().ssa_route_stamps(None, 0) == 801
+    assert _lib.lib().ssa_attn_stamps(None, 0) == 801
