@@ -43,9 +43,9 @@ sys.path.insert(0, ROOT)
 
 # HBM bytes per attn_kernel launch of the base-tier call, keyed by (pages, exact pages, single-term P.V),
 # measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this bench (profiles/attn_kernel_base432_traffic.md):
-# 139.8 MB read + 20.0 MB written by attn_kernel<true, 1, 0> (the two-term headline; the figure leaves out
+# 139.9 MB read + 20.0 MB written by attn_kernel<true, 1, 0> (the two-term headline; the figure leaves out
 # merge_kernel's 6.5 MB read and 1.6 MB written).  The single-term kernel was not measured: traffic null.
-MEASURED_TRAFFIC = {(432, 64, False): 159.8e6}
+MEASURED_TRAFFIC = {(432, 64, False): 159.9e6}
 METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
