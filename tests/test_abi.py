@@ -6,7 +6,7 @@ import re
 
 import pytest
 
-from streaming_sparse_amd import _lib
+from streaming_sparse_amd import _lib, build
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -45,3 +45,15 @@ def test_product_library_has_no_phase_stamps():
     arguments."""
     assert _lib.lib().ssa_route_stamps(None, 0) == 801
     assert _lib.lib().ssa_attn_stamps(None, 0) == 801
+
+
+@pytest.mark.skipif(not os.path.exists(build.STAMPS_LIB), reason="libssattn_stamps.so not built")
+def test_measurement_library_exports_every_declared_symbol():
+    """The measurement build (the same sources with the router's and the
+    attention kernel's stamps compiled in) exports the same entry points, so
+    streaming_sparse_amd.route_phases and attn_steps can route every call
+    through it."""
+    handle = ctypes.CDLL(build.STAMPS_LIB)
+    for name in declared():
+        assert hasattr(handle, name), name
+
