@@ -175,26 +175,29 @@ __global__ __launch_bounds__(1024) void features_kernel(GroupParams p) {
   double* raw = p.x[0] + (long long)b * kTokens * kR;
   const double* vp = p.x[1] + (long long)b * kTokens * kR;
   constexpr int kPer = kTokens / 32;
-  double s = 0.0;
-  for (int i = 0; i < kPer; ++i) s += raw[(t0 + 32 * i) * kR + r];
-  const double mean_raw = sum_over_tokens(s, red, tid) / kTokens;
-  // score = centred key projection / sqrt(D); its RMS over (t, r) and max over t
-  double sq = 0.0, mx = -INFINITY;
+  double s = 0.0, mraw = -INFINITY;
   for (int i = 0; i < kPer; ++i) {
-    const double sc = (raw[(t0 + 32 * i) * kR + r] - mean_raw) / kInvSqrtD;
-    sq = fma(sc, sc, sq);
-    mx = fmax(mx, sc);
+    const double x = raw[(t0 + 32 * i) * kR + r];
+    s += x;
+    mraw = fmax(mraw, x);
   }
-  const double rms = fmax(sqrt(sum_all(sq, red, tid) / (kTokens * kR)), 1e-6);
-  mx = max_over_tokens(mx, red, tid);
-  // softmax over tokens: denominator and sum of e * vp
-  double den = 0.0, num = 0.0;
+  const double mean_raw = sum_over_tokens(s, red, tid) / kTokens;
+  // score = centred key projection / sqrt(D).  Its max over t is the score
+  // of the largest projection: (x - mean) / sqrt(D) rounds monotonically in
+  // x, so this equals the max of the rounded scores bit for bit
+  const double mx = (max_over_tokens(mraw, red, tid) - mean_raw) / kInvSqrtD;
+  // one pass: the scores' RMS over (t, r), and the softmax over tokens
+  // (denominator and sum of e * vp), each sum in token order
+  double sq = 0.0, den = 0.0, num = 0.0;
   for (int i = 0; i < kPer; ++i) {
     const int e = (t0 + 32 * i) * kR + r;
-    const double ex = exp((raw[e] - mean_raw) / kInvSqrtD - mx);
+    const double sc = (raw[e] - mean_raw) / kInvSqrtD;
+    sq = fma(sc, sc, sq);
+    const double ex = exp(sc - mx);
     den += ex;
     num = fma(ex, vp[e], num);
   }
+  const double rms = fmax(sqrt(sum_all(sq, red, tid) / (kTokens * kR)), 1e-6);
   den = sum_over_tokens(den, red, tid);
   const double mean_a = sum_over_tokens(num, red, tid) / den;
   double sq2 = 0.0;
