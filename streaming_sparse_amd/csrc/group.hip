@@ -343,6 +343,11 @@ __global__ __launch_bounds__(THREADS) void level_kernel(GroupParams p, int n, in
     }
   }
   __syncthreads();
+  // A step of distance j <= 64 pairs elements within [2 e0, 2 e0 + 128) for
+  // each aligned run e0 .. e0 + 63 of pairs, and wave w takes the same runs
+  // (e0 = 64 w + THREADS m) in every step, so between two such steps it only
+  // needs its own LDS writes before its reads; a workgroup barrier goes
+  // before and after every step of a longer distance, and after the last.
   for (int kk = 2; kk <= SORTN; kk <<= 1) {
     for (int j = kk >> 1; j > 0; j >>= 1) {
       for (int e = tid; e < SORTN / 2; e += THREADS) {
@@ -358,7 +363,14 @@ __global__ __launch_bounds__(THREADS) void level_kernel(GroupParams p, int n, in
           pos[c] = pa;
         }
       }
-      __syncthreads();
+      const int next = j > 1 ? j >> 1 : (2 * kk <= SORTN ? kk : 0);   // the next step's distance, 0: none
+      if (j > 64 || next > 64 || next == 0) {
+        __syncthreads();
+      } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
     }
   }
   double* xo = p.x[src ^ 1] + row0 * kR;
@@ -512,7 +524,11 @@ __global__ __launch_bounds__(kFuseThreads, 1) void fused_levels_kernel(GroupPara
     __syncthreads();
     // bitonic stages up to size n: every aligned block of n sorts on its own,
     // ascending (the direction bit of the last stage is masked to the block);
-    // threads 0..255 each take one compare-exchange
+    // threads 0..255 each take one compare-exchange.  A step of distance
+    // j <= 64 pairs elements within [128 w, 128 w + 128) for the pairs
+    // e = 64 w .. 64 w + 63 of wave w, so between two such steps the wave only
+    // needs its own LDS writes before its reads; a workgroup barrier goes
+    // before and after every step of a longer distance, and after the last
     for (int kk = 2; kk <= n; kk <<= 1) {
       for (int j = kk >> 1; j > 0; j >>= 1) {
         const int e = tid & (kFuse / 2 - 1), a = (e / j) * 2 * j + (e % j), c = a + j;
@@ -526,7 +542,14 @@ __global__ __launch_bounds__(kFuseThreads, 1) void fused_levels_kernel(GroupPara
           pos[a] = pc;
           pos[c] = pa;
         }
-        __syncthreads();
+        const int next = j > 1 ? j >> 1 : (2 * kk <= n ? kk : 0);   // the next step's distance, 0: none
+        if (j > 64 || next > 64 || next == 0) {
+          __syncthreads();
+        } else {
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
       }
     }
     for (int i = tid; i < kFuse; i += kFuseThreads) perm[cur ^ 1][i] = pm[pos[i]];
