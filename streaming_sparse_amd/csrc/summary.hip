@@ -84,17 +84,20 @@ __device__ __forceinline__ float wave_sum(float v) {
   return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
-// Word `lane` of up to 4 member tokens of m (removed from m), 0 for absent
-// slots (a bf16 pair of +0, which changes no sum).
-__device__ __forceinline__ void next4(const uint32_t* rows, uint64_t& m, int lane, uint32_t (&w)[4]) {
+// Words `lane` of the K and V rows of the next kWalk member tokens of m
+// (removed from m), in ascending token order.  The token ids come from the
+// wave-uniform mask without branches and every read is issued before the
+// first use; a slot past the last member re-reads token 0, which the caller
+// does not accumulate.
+constexpr int kWalk = 8;
+__device__ __forceinline__ void next_members(const uint32_t* krows, const uint32_t* vrows, uint64_t& m, int lane,
+                                             uint32_t (&wk)[kWalk], uint32_t (&wv)[kWalk]) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    w[u] = 0u;
-    if (m) {
-      const int t = __builtin_ctzll(m);
-      m &= m - 1;
-      w[u] = rows[word(t, lane)];
-    }
+  for (int u = 0; u < kWalk; ++u) {
+    const int t = m ? __builtin_ctzll(m) : 0;
+    m &= m - 1;
+    wk[u] = krows[word(t, lane)];
+    wv[u] = vrows[word(t, lane)];
   }
 }
 
@@ -145,7 +148,7 @@ __device__ __forceinline__ f32x16 cluster_sums(const uint32_t* rows, const uint6
 }
 
 template <class Layers>
-__global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers layers) {
+__global__ __launch_bounds__(256, 4) void summary_kernel(SummaryParams p, Layers layers) {
   if constexpr (std::is_same_v<Layers, SummaryLayers>) {
     const int l = blockIdx.z;
     p.k = layers.k[l];
@@ -247,7 +250,10 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers la
 
   // Lloyd iterations: assign each token to its nearest centroid (squared
   // distance, ties -> lower cluster), then move every non-empty centroid to
-  // its cluster mean
+  // its cluster mean.  An assignment equal to the previous one is a fixed
+  // point: the update would rebuild the same centroids from the same member
+  // sums, and every later iteration would repeat both, so the loop ends
+  // there with the result of all p.iters iterations, bit for bit.
   uint64_t memb[4] = {0, 0, 0, 0};   // member tokens of each cluster (wave-uniform)
   for (int it = 0; it < p.iters; ++it) {
     float d[4] = {0.f, 0.f, 0.f, 0.f};
@@ -278,8 +284,18 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers la
         best = r;
       }
     }
+    uint64_t nm[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) memb[r] = __ballot(best == r);
+    for (int r = 0; r < 4; ++r) nm[r] = __ballot(best == r);
+    // every wave forms the same assignment from the same distances, so the
+    // exit is uniform; the barrier keeps the distance slots (a union with
+    // the cluster V means written next) until every wave has read them
+    if (it > 0 && nm[0] == memb[0] && nm[1] == memb[1] && nm[2] == memb[2] && nm[3] == memb[3]) {
+      __syncthreads();
+      break;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) memb[r] = nm[r];
     // the cluster sums of dims 32 wave .. 32 wave + 31 (and the page sum, on
     // the first pass) on the matrix pipe; lane l < 32 then holds the 4
     // cluster sums of dim 32 wave + l, lane l + 32 its page sum
@@ -319,15 +335,14 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryParams p, Layers la
   const float vm0 = s.u.vm[r][d0], vm1 = s.u.vm[r][d1];
   float var0 = 0.f, var1 = 0.f, spread = 0.f;
   {
-    uint64_t mk = mr, mv = mr;
+    uint64_t mk = mr;
     while (mk) {
-      uint32_t wk[4], wv[4];
+      uint32_t wk[kWalk], wv[kWalk];
       const int n = __popcll(mk);
-      next4(s.K, mk, lane, wk);
-      next4(s.V, mv, lane, wv);
+      next_members(s.K, s.V, mk, lane, wk, wv);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        // absent slots: skip, as (0 - c)^2 is not 0
+      for (int u = 0; u < kWalk; ++u) {
+        // absent slots: skip
         if (u < n) {
           const float x0 = bf16_lo(wk[u]) - c0, x1 = bf16_hi(wk[u]) - c1;
           var0 = fmaf(x0, x0, var0);
