@@ -15,7 +15,11 @@ from streaming_sparse_amd.ops import Summary
 pytestmark = pytest.mark.gpu
 
 
-def test_current_chunk_summaries_match_oracle(device):
+@pytest.mark.parametrize("iters", [4, 1, 2, 6])
+def test_current_chunk_summaries_match_oracle(device, iters):
+    """The kernel ends its Lloyd loop at the first assignment that repeats
+    the previous one; the oracle runs every iteration.  1 iteration never
+    reaches that exit, 6 reach it on nearly every page."""
     x = workload.make_call(cfg=3, frames=18)
     P = x.pages
     g = x.to(device)
@@ -23,11 +27,11 @@ def test_current_chunk_summaries_match_oracle(device):
     slab = Summary(*(getattr(g.summary, f).clone() for f in Summary.FIELDS))
     for f in Summary.FIELDS:
         getattr(slab, f)[:, P - 72:].zero_()
-    summary.build(g.k, g.v, g.basis, init.to(device), slab, P - 72, 72)
+    summary.build(g.k, g.v, g.basis, init.to(device), slab, P - 72, 72, iters=iters)
     torch.cuda.synchronize()
     kp = x.k[0].transpose(0, 1).reshape(12, P, 64, 128)[:, P - 72:]
     vp = x.v[0].transpose(0, 1).reshape(12, P, 64, 128)[:, P - 72:]
-    want = osum.summaries(kp, vp, x.basis, init)
+    want = osum.summaries(kp, vp, x.basis, init, iters=iters)
     ok = want['margin'] > 1e-5
     print(f"{int(ok.sum())}/{ok.numel()} pages without a k-means near tie", flush=True)
     assert int(ok.sum()) >= ok.numel() * 0.95
