@@ -128,6 +128,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p, Layers laye
   if (tid < 128) {
     const int k = tid >> 4, e = tid & 15;
     double acc = 0.0;
+#pragma unroll 32
     for (int d = 0; d < 128; ++d)
       acc += (double)bf16_to_f32(p.basis[((long long)h * 128 + d) * 8 + k]) * p.B[d * 16 + e];
     pb[k][e] = acc;
@@ -142,7 +143,9 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p, Layers laye
     for (int i = 0; i < kEncPages; ++i) ar[i] = ap[i] = 0.f;
     const float* wr = p.w1t + tid;
     const float* wp = p.w1t + H + tid;
-#pragma unroll 8
+    // 32 rows of the weights in flight per thread: the loop streams 1.46 MB
+    // of weights through each workgroup and waits on their latency otherwise
+#pragma unroll 32
     for (int k = 0; k < kFeatures; ++k) {
       const float a = wr[(long long)k * 2 * H], b = wp[(long long)k * 2 * H];
 #pragma unroll
@@ -188,6 +191,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeParams p, Layers laye
     if (pl >= npg) continue;
     const long long pg = (long long)h * p.HP + p.first + g0 + pl;
     double acc = 0.0;
+#pragma unroll 32
     for (int d = 0; d < 128; ++d) acc += (double)bf16_to_f32(p.mean[pg * 128 + d]) * p.B[d * 16 + e];
     p.mean_b[((long long)h * p.EP + p.first + g0 + pl) * 16 + e] = acc;
   }
