@@ -51,7 +51,8 @@ METRIC = "ms per sparse-attn call at 432-page window, 12 heads; MFMA util + HBM 
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 PSET_HEADS = (3, 4, 9)
-# untimed calls before a line whose inputs were just made on the host (ms)
+# untimed calls before a line whose inputs were just made on the host, or that
+# follows calls of another kind (ms)
 LINE_WARMUP_MS = 100.0
 
 
@@ -292,8 +293,7 @@ def main():
         kd = g.k[0].transpose(0, 1)[None]
         vd = g.v[0].transpose(0, 1)[None]
         dense = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)
-        for _ in range(3):
-            dense()
+        device_warmup(dense, LINE_WARMUP_MS)
         dense_ms = time_loop(dense, max(5, iters // 5), stream)
         # this library's kernel with every page exact (the dense layers' call)
         own = torch.arange(N // 64, device=dev) + P - N // 64
@@ -304,8 +304,7 @@ def main():
         dids = dids[keep].reshape(N // 64, P)[None].expand(H, -1, -1).to(torch.int32).contiguous()
         for name, sgl in (("two_term", False), ("single_term", True)):
             fn = lambda s=sgl: attention(g.q, g.k, g.v, g.summary, basis, dids, ws, single_av=s, all_pages=True)
-            for _ in range(3):
-                fn()
+            device_warmup(fn, LINE_WARMUP_MS)
             dense_own[name] = time_loop(fn, max(5, iters // 5), stream)
 
     log(f"dense: sdpa {dense_ms} ms, this kernel {dense_own}")
